@@ -1,0 +1,192 @@
+/*
+ * smx.h -- C-ABI of libsmx.so, the MI355X (gfx950) backend for SmallMind's quantized
+ * transformer forward path.
+ *
+ * Plain C types only.  Every entry point returns an int status (0 = SMX_OK, < 0 = error);
+ * smx_last_error() returns a thread-local message for the last failing call on the calling
+ * thread.  Pointers named *_dev are HIP device pointers; `stream` is a hipStream_t (NULL =
+ * the library context's stream for model/session calls, the null stream for operator calls).
+ *
+ * Reference interfaces each group replaces (paths relative to the SmallMind repository):
+ *   operator level  IWeightTensor            src/SmallMind.Quantization/Abstractions/IWeightTensor.cs:7-42
+ *   dequantization  GgufModelLoader.Convert* src/SmallMind.Runtime/GgufModelLoader.cs:419-956
+ *   quantization    Q8Tensor/Q4Tensor.Quantize src/SmallMind.Quantization/Tensors/Q8Tensor.cs:72-128,
+ *                                            Q4Tensor.cs:75-134
+ *   model level     TransformerModel.Forward src/SmallMind.Transformers/Core/TransformerModel.cs:272-344
+ *                   + Enable/Reset/DisableKVCache (:476-506)
+ *   session level   InferenceSession.GenerateNextTokenAsync src/SmallMind.Runtime/InferenceSession.cs:478-607
+ */
+#ifndef SMX_H
+#define SMX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMX_API __attribute__((visibility("default")))
+
+enum smx_status {
+    SMX_OK = 0,
+    SMX_EINVAL = -1,        /* bad argument / shape mismatch (ArgumentException in the reference) */
+    SMX_ENOMEM = -2,        /* device allocation failed */
+    SMX_EDEVICE = -3,       /* HIP runtime error */
+    SMX_EBUSY = -4,         /* session already in use on another thread (InferenceSession.cs:127-144) */
+    SMX_EUNSUPPORTED = -5,  /* tensor type or shape the backend does not implement */
+    SMX_ESTATE = -6,        /* call out of order (e.g. model not finalized) */
+    SMX_ERANGE = -7         /* position / token out of range (TransformerModel.cs:282-285) */
+};
+
+/* GGUF tensor type ids (src/SmallMind.Quantization/IO/Gguf/GgufTensorType.cs:6-52). */
+enum smx_type {
+    SMX_TYPE_F32 = 0,
+    SMX_TYPE_F16 = 1,
+    SMX_TYPE_Q4_0 = 2,
+    SMX_TYPE_Q8_0 = 8,
+    SMX_TYPE_Q4_K = 12,
+    SMX_TYPE_Q5_K = 13,
+    SMX_TYPE_Q6_K = 14
+};
+
+/* ---- library ----------------------------------------------------------------------------- */
+SMX_API const char *smx_version(void);
+SMX_API const char *smx_last_error(void);
+/* Elements / bytes per GGUF block; 0 for unknown types. */
+SMX_API int smx_type_block_elems(int type);
+SMX_API int smx_type_block_bytes(int type);
+/* GGUF bytes of one row of k elements (k must be a multiple of the block size), else -1. */
+SMX_API int64_t smx_type_row_bytes(int type, int64_t k);
+
+/* ---- dequantization / quantization (device pointers) ----------------------------------- */
+/* Replaces GgufModelLoader.ReadAndDequantizeTensor -> Convert{Q8_0,Q4_0,Q4_K,Q5_K,Q6_K,F16,F32}
+ * (GgufModelLoader.cs:419-917): n elements of GGUF-layout blocks -> fp32, bit-identical. */
+SMX_API int smx_dequant(int type, const void *blocks_dev, int64_t n, float *out_dev, void *stream);
+/* Replaces Q8Tensor.Quantize / Q4Tensor.Quantize (Q8Tensor.cs:72-128, Q4Tensor.cs:75-134),
+ * emitting GGUF block layout (block 32, fp16 scale) for Q8_0/Q4_0, plus this build's K-quant
+ * encoders for Q4_K/Q5_K/Q6_K.  n must be a multiple of the block size. */
+SMX_API int smx_quantize(int type, const float *x_dev, int64_t n, void *blocks_dev, void *stream);
+/* Seeded N(0, std) fill used to synthesise weights (counter-based, splitmix64 + Box-Muller).
+ * Replaces the seeded weight initialisation of Tensor.InitializeXavier/Random (Tensor.cs:262-285). */
+SMX_API int smx_fill_normal(uint64_t seed, int64_t n, float std, float *out_dev, void *stream);
+
+/* ---- operator level: IWeightTensor ----------------------------------------------------- */
+typedef struct smx_weight smx_weight;
+/* Creates a device weight [rows][cols] (GGUF dims ne0 = cols) from GGUF-layout blocks.
+ * The bytes are copied and repacked into the backend layout; the repack is lossless.
+ * blocks_on_device != 0: blocks is a device pointer, else a host pointer.
+ * Replaces the IWeightTensor implementations (Q8WeightTensor.cs, Q4KWeightTensor.cs, ...). */
+SMX_API int smx_weight_create(int type, int64_t rows, int64_t cols, const void *blocks,
+                              int blocks_on_device, smx_weight **out);
+SMX_API int smx_weight_info(const smx_weight *w, int *type, int64_t *rows, int64_t *cols);
+/* IWeightTensor.MatMul (IWeightTensor.cs:33): out[m][n] = act[m][k] . W^T with k == cols and
+ * n == rows (the GGUF-loader semantics y = x W^T).  Output fully overwritten.
+ * SMX_EINVAL on dimension mismatch, as the reference throws ArgumentException
+ * (Q8WeightTensor.cs:43-48). */
+SMX_API int smx_weight_matmul(const smx_weight *w, const float *act_dev, float *out_dev, int m,
+                              int k, int n, void *stream);
+/* IWeightTensor.ToFloat32 (IWeightTensor.cs:41): [rows][cols] fp32, bit-identical to the
+ * reference dequantization of the original blocks. */
+SMX_API int smx_weight_to_float32(const smx_weight *w, float *out_dev, void *stream);
+SMX_API int smx_weight_destroy(smx_weight *w);
+
+/* ---- elementwise / attention operators (device pointers) -------------------------------- */
+/* RMSNormOps.RMSNorm (src/SmallMind.Core/Core/RMSNormOps.cs:28-219). */
+SMX_API int smx_rmsnorm(const float *x_dev, const float *gamma_dev, float *y_dev, int rows, int n,
+                        float eps, void *stream);
+/* LayerNormOps.LayerNorm (src/SmallMind.Core/Core/LayerNormOps.cs:27-280). */
+SMX_API int smx_layernorm(const float *x_dev, const float *gamma_dev, const float *beta_dev,
+                          float *y_dev, int rows, int n, float eps, void *stream);
+/* RotaryEmbedding.PrecomputeTables (src/SmallMind.Transformers/Core/RotaryEmbedding.cs:45-60),
+ * host buffers [max_pos][head_dim/2]. */
+SMX_API int smx_rope_tables(int max_pos, int head_dim, float theta, float *cos_host,
+                            float *sin_host);
+/* RotaryEmbedding.ApplyRotationInPlace (RotaryEmbedding.cs:85-121) on data [heads][seq][hd]
+ * at positions pos0..pos0+seq-1; tables are device copies of smx_rope_tables output. */
+SMX_API int smx_rope(float *data_dev, int n_heads, int seq, int head_dim, int pos0,
+                     const float *cos_dev, const float *sin_dev, void *stream);
+/* OptimizedOps.FusedScaleMaskSoftmax (src/SmallMind.Core/Optimized/OptimizedOps.cs:39-93),
+ * in place on [seq][k_seq] with FastExp (src/SmallMind.Core/Utilities/MathUtils.cs:20-32). */
+SMX_API int smx_scale_mask_softmax(float *scores_dev, float scale, int seq, int k_seq,
+                                   int cache_offset, void *stream);
+/* One decode position of MultiHeadAttention (MultiHeadAttention.cs:676-844): q [n_head][hd],
+ * caches [n_kv_head][ctx_stride][hd] holding n_pos positions, out [n_head][hd]. */
+SMX_API int smx_attention_decode(const float *q_dev, const float *k_cache_dev,
+                                 const float *v_cache_dev, float *out_dev, int n_head,
+                                 int n_kv_head, int head_dim, int ctx_stride, int n_pos,
+                                 void *stream);
+/* ActivationOps.FusedSiLUMul (src/SmallMind.Core/Simd/ActivationOps.cs:565-580). */
+SMX_API int smx_silu_mul(const float *gate_dev, const float *up_dev, float *y_dev, int64_t n,
+                         void *stream);
+/* ActivationOps.GELU (ActivationOps.cs:217-296). */
+SMX_API int smx_gelu(const float *x_dev, float *y_dev, int64_t n, void *stream);
+/* Greedy next-token selection (replaces the T->0 limit of InferenceSession.cs:565-606):
+ * index of the maximum, lowest index on ties. */
+SMX_API int smx_argmax(const float *x_dev, int n, int32_t *out_dev, void *stream);
+
+/* ---- model / session level --------------------------------------------------------------- */
+typedef struct smx_context smx_context;
+typedef struct smx_model smx_model;
+typedef struct smx_session smx_session;
+
+enum smx_arch { SMX_ARCH_LLAMA = 0, SMX_ARCH_GPT2 = 1 };
+
+/* ModelConfig (src/SmallMind.Transformers/ModelConfig.cs:142-258).  llama: RoPE, RMSNorm,
+ * SwiGLU, optional biases; gpt2: learned positions, LayerNorm, GELU MLP of 4*d, biases. */
+typedef struct smx_model_config {
+    int32_t arch;
+    int32_t vocab;
+    int32_t ctx;          /* ContextLength (block size) */
+    int32_t d_model;
+    int32_t n_layer;
+    int32_t n_head;
+    int32_t n_kv_head;
+    int32_t d_ff;         /* FeedForwardLength (ignored for gpt2: 4*d_model) */
+    float rope_theta;
+    float norm_eps;
+    int32_t reserved[6];  /* must be zero */
+} smx_model_config;
+
+typedef struct smx_gen_stats {
+    double prefill_ms;    /* GPU time of the steps that only filled the KV cache */
+    double decode_ms;     /* GPU time of the steps that produced a token */
+    int32_t n_prefill_steps;
+    int32_t n_decode_steps;
+} smx_gen_stats;
+
+SMX_API int smx_context_create(int device, smx_context **out);
+SMX_API int smx_context_destroy(smx_context *ctx);
+
+SMX_API int smx_model_create(smx_context *ctx, const smx_model_config *cfg, smx_model **out);
+/* Uploads one GGUF tensor by its GGUF name (token_embd.weight, blk.N.attn_q.weight, ...).
+ * dims are GGUF order (dims[0] = ne0 = fastest).  Q/K/V are merged into one fused matrix as
+ * GgufModelLoader.MergeQKVWeights does (GgufModelLoader.cs:1027-1110); gate/up rows are
+ * interleaved for the fused SwiGLU kernel.  bytes_on_device selects a device or host source. */
+SMX_API int smx_model_upload_tensor(smx_model *m, const char *name, int type,
+                                    const int64_t *dims, int ndims, const void *bytes,
+                                    size_t nbytes, int bytes_on_device);
+/* Validates the tensor set and ties output.weight to token_embd.weight when absent
+ * (GgufModelLoader.HandleWeightTying, GgufModelLoader.cs:1126-1147). */
+SMX_API int smx_model_finalize(smx_model *m);
+SMX_API int smx_model_weight_bytes(const smx_model *m, int64_t *bytes);
+SMX_API int smx_model_destroy(smx_model *m);
+
+SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out);
+/* TransformerModel.Forward(idx[1,T], positionOffset) with the KV cache enabled: runs
+ * n_tokens tokens at positions pos_offset.. and writes the last row's logits (vocab floats,
+ * host memory) when logits_out != NULL.  SMX_ERANGE when pos_offset + n_tokens > max_ctx. */
+SMX_API int smx_session_forward(smx_session *s, const int32_t *tokens, int n_tokens,
+                                int pos_offset, float *logits_out);
+/* Greedy generation entirely on the device: prefill the prompt, then n_new tokens by argmax.
+ * out_tokens (host, n_new).  logits_out (host, n_new*vocab) may be NULL. */
+SMX_API int smx_session_generate(smx_session *s, const int32_t *prompt, int n_prompt, int n_new,
+                                 int32_t *out_tokens, float *logits_out, smx_gen_stats *stats);
+/* ResetKVCache (TransformerModel.cs:476-506): next forward starts at position 0. */
+SMX_API int smx_session_reset(smx_session *s);
+SMX_API int smx_session_destroy(smx_session *s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

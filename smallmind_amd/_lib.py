@@ -1,0 +1,119 @@
+"""ctypes binding of libsmx.so (the C-ABI declared in include/smx.h).
+
+The product path always runs through this library; there is no CPU fallback.  Importing
+fails loudly when the library has not been built.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsmx.so")
+
+# GGUF tensor type ids (GgufTensorType.cs:6-52)
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 8, 12, 13, 14
+ARCH_LLAMA, ARCH_GPT2 = 0, 1
+
+STATUS = {0: "SMX_OK", -1: "SMX_EINVAL", -2: "SMX_ENOMEM", -3: "SMX_EDEVICE", -4: "SMX_EBUSY",
+          -5: "SMX_EUNSUPPORTED", -6: "SMX_ESTATE", -7: "SMX_ERANGE"}
+
+# Every function include/smx.h declares.
+EXPORTS = [
+    "smx_version", "smx_last_error", "smx_type_block_elems", "smx_type_block_bytes",
+    "smx_type_row_bytes", "smx_dequant", "smx_quantize", "smx_fill_normal",
+    "smx_weight_create", "smx_weight_info", "smx_weight_matmul", "smx_weight_to_float32",
+    "smx_weight_destroy", "smx_rmsnorm", "smx_layernorm", "smx_rope_tables", "smx_rope",
+    "smx_scale_mask_softmax", "smx_attention_decode", "smx_silu_mul", "smx_gelu", "smx_argmax",
+    "smx_context_create", "smx_context_destroy", "smx_model_create", "smx_model_upload_tensor",
+    "smx_model_finalize", "smx_model_weight_bytes", "smx_model_destroy", "smx_session_create",
+    "smx_session_forward", "smx_session_generate", "smx_session_reset", "smx_session_destroy",
+]
+
+
+class SmxError(RuntimeError):
+    def __init__(self, func: str, code: int, msg: str):
+        super().__init__(f"{func} -> {STATUS.get(code, code)}: {msg}")
+        self.code = code
+
+
+class ModelConfigC(ctypes.Structure):
+    _fields_ = [("arch", ctypes.c_int32), ("vocab", ctypes.c_int32), ("ctx", ctypes.c_int32),
+                ("d_model", ctypes.c_int32), ("n_layer", ctypes.c_int32),
+                ("n_head", ctypes.c_int32), ("n_kv_head", ctypes.c_int32),
+                ("d_ff", ctypes.c_int32), ("rope_theta", ctypes.c_float),
+                ("norm_eps", ctypes.c_float), ("reserved", ctypes.c_int32 * 6)]
+
+
+class GenStatsC(ctypes.Structure):
+    _fields_ = [("prefill_ms", ctypes.c_double), ("decode_ms", ctypes.c_double),
+                ("n_prefill_steps", ctypes.c_int32), ("n_decode_steps", ctypes.c_int32)]
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads libsmx.so; raises ImportError if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: the HIP backend has not been built "
+            "(run `python -c 'import __graft_entry__ as g; g.build()'`). There is no CPU fallback.")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i32, i64, f32, u64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_uint64
+    pp = ctypes.POINTER(ctypes.c_void_p)
+    sig = {
+        "smx_version": (ctypes.c_char_p, []),
+        "smx_last_error": (ctypes.c_char_p, []),
+        "smx_type_block_elems": (i32, [i32]),
+        "smx_type_block_bytes": (i32, [i32]),
+        "smx_type_row_bytes": (i64, [i32, i64]),
+        "smx_dequant": (i32, [i32, vp, i64, vp, vp]),
+        "smx_quantize": (i32, [i32, vp, i64, vp, vp]),
+        "smx_fill_normal": (i32, [u64, i64, f32, vp, vp]),
+        "smx_weight_create": (i32, [i32, i64, i64, vp, i32, pp]),
+        "smx_weight_info": (i32, [vp, ctypes.POINTER(i32), ctypes.POINTER(i64), ctypes.POINTER(i64)]),
+        "smx_weight_matmul": (i32, [vp, vp, vp, i32, i32, i32, vp]),
+        "smx_weight_to_float32": (i32, [vp, vp, vp]),
+        "smx_weight_destroy": (i32, [vp]),
+        "smx_rmsnorm": (i32, [vp, vp, vp, i32, i32, f32, vp]),
+        "smx_layernorm": (i32, [vp, vp, vp, vp, i32, i32, f32, vp]),
+        "smx_rope_tables": (i32, [i32, i32, f32, vp, vp]),
+        "smx_rope": (i32, [vp, i32, i32, i32, i32, vp, vp, vp]),
+        "smx_scale_mask_softmax": (i32, [vp, f32, i32, i32, i32, vp]),
+        "smx_attention_decode": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
+        "smx_silu_mul": (i32, [vp, vp, vp, i64, vp]),
+        "smx_gelu": (i32, [vp, vp, i64, vp]),
+        "smx_argmax": (i32, [vp, i32, vp, vp]),
+        "smx_context_create": (i32, [i32, pp]),
+        "smx_context_destroy": (i32, [vp]),
+        "smx_model_create": (i32, [vp, ctypes.POINTER(ModelConfigC), pp]),
+        "smx_model_upload_tensor": (i32, [vp, ctypes.c_char_p, i32, ctypes.POINTER(i64), i32, vp,
+                                          ctypes.c_size_t, i32]),
+        "smx_model_finalize": (i32, [vp]),
+        "smx_model_weight_bytes": (i32, [vp, ctypes.POINTER(i64)]),
+        "smx_model_destroy": (i32, [vp]),
+        "smx_session_create": (i32, [vp, i32, pp]),
+        "smx_session_forward": (i32, [vp, vp, i32, i32, vp]),
+        "smx_session_generate": (i32, [vp, vp, i32, i32, vp, vp, ctypes.POINTER(GenStatsC)]),
+        "smx_session_reset": (i32, [vp]),
+        "smx_session_destroy": (i32, [vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def call(name: str, *args) -> int:
+    """Calls a status-returning C-ABI function and raises SmxError on failure."""
+    L = load()
+    rc = getattr(L, name)(*args)
+    if rc != 0:
+        raise SmxError(name, rc, (L.smx_last_error() or b"").decode(errors="replace"))
+    return rc

@@ -1,0 +1,340 @@
+// k_ops.hip -- norms, RoPE, softmax, decode attention, activations, embedding, argmax.
+#include "smx_device.h"
+#include "smx_formats.h"
+
+namespace smx {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+// RMSNormOps.RMSNorm (RMSNormOps.cs:28-219): one workgroup per row.
+__global__ __launch_bounds__(kThreads) void k_rmsnorm(const float *__restrict__ x,
+                                                      const float *__restrict__ g,
+                                                      float *__restrict__ y, int n, float eps)
+{
+    __shared__ float red[16];
+    const float *xr = x + (int64_t)blockIdx.x * n;
+    float *yr = y + (int64_t)blockIdx.x * n;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kThreads) { float v = xr[i]; float p = v * v; ss += p; }
+    ss = block_sum<kWaves>(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += kThreads) { float t = xr[i] * inv; yr[i] = g[i] * t; }
+}
+
+// LayerNormOps.LayerNorm (LayerNormOps.cs:27-280): two-pass mean / variance, affine by FMA.
+__global__ __launch_bounds__(kThreads) void k_layernorm(const float *__restrict__ x,
+                                                        const float *__restrict__ g,
+                                                        const float *__restrict__ b,
+                                                        float *__restrict__ y, int n, float eps)
+{
+    __shared__ float red[16];
+    const float *xr = x + (int64_t)blockIdx.x * n;
+    float *yr = y + (int64_t)blockIdx.x * n;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kThreads) s += xr[i];
+    s = block_sum<kWaves>(s, red);
+    const float mean = s / (float)n;
+    float sq = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kThreads) { float dd = xr[i] - mean; float p = dd * dd; sq += p; }
+    sq = block_sum<kWaves>(sq, red);
+    const float inv = 1.0f / sqrtf(sq / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        float t = (xr[i] - mean) * inv;
+        yr[i] = __builtin_fmaf(g[i], t, b[i]);
+    }
+}
+
+// RotaryEmbedding.ApplyRotationInPlace (RotaryEmbedding.cs:85-121), data [heads][seq][hd].
+__global__ void k_rope(float *__restrict__ data, int n_heads, int seq, int hd, int pos0,
+                       const float *__restrict__ c, const float *__restrict__ sn)
+{
+    const int half = hd / 2;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)n_heads * seq * half) return;
+    const int i = (int)(idx % half);
+    const int64_t hs = idx / half;
+    const int s = (int)(hs % seq);
+    const int pos = pos0 + s;
+    float *v = data + hs * hd;
+    const float x0 = v[2 * i], x1 = v[2 * i + 1];
+    const float cc = c[(int64_t)pos * half + i], ss = sn[(int64_t)pos * half + i];
+    const float t0 = x0 * cc, t1 = x1 * ss, t2 = x0 * ss, t3 = x1 * cc;
+    v[2 * i] = t0 - t1;
+    v[2 * i + 1] = t2 + t3;
+}
+
+// OptimizedOps.FusedScaleMaskSoftmax (OptimizedOps.cs:39-93): one workgroup per row.
+__global__ __launch_bounds__(kThreads) void k_softmax(float *__restrict__ scores, float scale,
+                                                      int k_seq, int cache_off)
+{
+    __shared__ float red[16];
+    float *row = scores + (int64_t)blockIdx.x * k_seq;
+    const int valid = cache_off + (int)blockIdx.x + 1;
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < valid; j += kThreads) mx = fmaxf(mx, row[j] * scale);
+    mx = block_max<kWaves>(mx, red);
+    float sum = 0.0f;
+    for (int j = threadIdx.x; j < valid; j += kThreads) {
+        float s = row[j] * scale;
+        float e = fastexp(s - mx);
+        row[j] = e;
+        sum += e;
+    }
+    sum = block_sum<kWaves>(sum, red);
+    const float inv = 1.0f / sum;
+    for (int j = threadIdx.x; j < k_seq; j += kThreads) row[j] = j < valid ? row[j] * inv : 0.0f;
+}
+
+// One decode position of MultiHeadAttention (MultiHeadAttention.cs:676-844) per query head:
+// raw scores q.k, scale, max, FastExp(s*scale - max), normalise by 1/sum, then P.V.  The
+// softmax is two-pass (global max first) because the Pade FastExp is not multiplicative, so
+// an online rescaling would not reproduce the reference.  Scores live in LDS.
+__global__ __launch_bounds__(kThreads) void k_attention_decode(
+    const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
+    float *__restrict__ out, int n_head, int n_kv_head, int hd, int ctx_stride,
+    const int32_t *__restrict__ pos_dev, int n_pos_fixed)
+{
+    extern __shared__ float4 smem4[];
+    float *sc = (float *)smem4;              // [n_pos]
+    __shared__ float qs[256];
+    __shared__ float part[kWaves][256];
+    __shared__ float red[16];
+    const int h = blockIdx.x;
+    const int kvh = h / (n_head / n_kv_head);
+    const int n_pos = pos_dev ? *pos_dev + 1 : n_pos_fixed;
+    const float scale = 1.0f / sqrtf((float)hd);   // MultiHeadAttention.cs:686
+    for (int e = threadIdx.x; e < hd; e += kThreads) qs[e] = q[(int64_t)h * hd + e];
+    __syncthreads();
+    const float *K = kc + (int64_t)kvh * ctx_stride * hd;
+    const float *V = vc + (int64_t)kvh * ctx_stride * hd;
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < n_pos; j += kThreads) {
+        const float4 *kr = (const float4 *)(K + (int64_t)j * hd);
+        float s = 0.0f;
+        for (int e4 = 0; e4 < hd / 4; e4++) {
+            const float4 kv = kr[e4];
+            s = __builtin_fmaf(qs[4 * e4 + 0], kv.x, s);
+            s = __builtin_fmaf(qs[4 * e4 + 1], kv.y, s);
+            s = __builtin_fmaf(qs[4 * e4 + 2], kv.z, s);
+            s = __builtin_fmaf(qs[4 * e4 + 3], kv.w, s);
+        }
+        const float t = s * scale;
+        sc[j] = t;
+        mx = fmaxf(mx, t);
+    }
+    mx = block_max<kWaves>(mx, red);
+    float sum = 0.0f;
+    for (int j = threadIdx.x; j < n_pos; j += kThreads) {
+        const float e = fastexp(sc[j] - mx);
+        sc[j] = e;
+        sum += e;
+    }
+    sum = block_sum<kWaves>(sum, red);
+    const float inv = 1.0f / sum;
+    for (int j = threadIdx.x; j < n_pos; j += kThreads) sc[j] = sc[j] * inv;
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int e = lane; e < hd; e += 64) {
+        float acc = 0.0f;
+        for (int j = wave; j < n_pos; j += kWaves) acc = __builtin_fmaf(sc[j], V[(int64_t)j * hd + e], acc);
+        part[wave][e] = acc;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < hd; e += kThreads) {
+        float o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) o += part[w][e];
+        out[(int64_t)h * hd + e] = o;
+    }
+}
+
+__global__ void k_silu_mul(const float *__restrict__ g, const float *__restrict__ u,
+                           float *__restrict__ y, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = silu_mul(g[i], u[i]);
+}
+
+__global__ void k_gelu(const float *__restrict__ x, float *__restrict__ y, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = gelu_pade(x[i]);
+}
+
+// Argmax with the lowest index on ties.  With `tokens`/`pos` set it also appends the token to
+// the device token array and advances the device position (end of a decode step).
+__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ x, int n,
+                                                 int32_t *__restrict__ out,
+                                                 int32_t *__restrict__ tokens,
+                                                 int32_t *__restrict__ pos)
+{
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    float best = -INFINITY;
+    int idx = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i];
+        if (v > best) { best = v; idx = i; }   // strided ascending scan: keeps the lowest index
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (ov > best || (ov == best && oi < idx)) { best = ov; idx = oi; }
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { bv[w] = best; bi[w] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int nw = blockDim.x >> 6;
+        best = bv[0];
+        idx = bi[0];
+        for (int i = 1; i < nw; i++)
+            if (bv[i] > best || (bv[i] == best && bi[i] < idx)) { best = bv[i]; idx = bi[i]; }
+        if (idx == 0x7FFFFFFF) idx = 0;
+        if (out) *out = idx;
+        if (tokens && pos) {
+            const int p = *pos;
+            tokens[p + 1] = idx;
+            *pos = p + 1;
+        }
+    }
+}
+
+__global__ void k_advance(int32_t *pos)
+{
+    if (threadIdx.x == 0) *pos = *pos + 1;
+}
+
+// Embedding gather (NeuralNet.cs:376-391, row copies :576-592) with the row dequantised
+// exactly, plus the learned position row for GPT-2 (TransformerModel.cs:299-326).
+template <int F>
+__device__ void embed_row(const WView &w, int64_t row, float *y, const WView *pw, int64_t prow)
+{
+    const int nch = (int)(w.cols / 32);
+    for (int c = threadIdx.x; c < nch; c += blockDim.x) {
+        float v[32];
+        decode_chunk_exact<F>(w, row, c, v);
+        if (pw) {
+            float p[32];
+            switch (pw->fmt) {
+            case FMT_Q4_0: decode_chunk_exact<FMT_Q4_0>(*pw, prow, c, p); break;
+            case FMT_Q8_0: decode_chunk_exact<FMT_Q8_0>(*pw, prow, c, p); break;
+            case FMT_Q4_K: decode_chunk_exact<FMT_Q4_K>(*pw, prow, c, p); break;
+            case FMT_Q5_K: decode_chunk_exact<FMT_Q5_K>(*pw, prow, c, p); break;
+            default: decode_chunk_exact<FMT_Q6_K>(*pw, prow, c, p); break;
+            }
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = v[i] + p[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 32; i++) y[c * 32 + i] = v[i];
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_embed(WView w, WView pw, int has_pos,
+                                                    const int32_t *__restrict__ tokens,
+                                                    const int32_t *__restrict__ pos,
+                                                    float *__restrict__ x)
+{
+    const int p = *pos;
+    int64_t tok = tokens[p];
+    if (tok < 0 || tok >= w.rows) tok = 0;   // the host validates tokens; never read out of bounds
+    const WView *pp = has_pos ? &pw : nullptr;
+    switch (w.fmt) {
+    case FMT_Q4_0: embed_row<FMT_Q4_0>(w, tok, x, pp, p); break;
+    case FMT_Q8_0: embed_row<FMT_Q8_0>(w, tok, x, pp, p); break;
+    case FMT_Q4_K: embed_row<FMT_Q4_K>(w, tok, x, pp, p); break;
+    case FMT_Q5_K: embed_row<FMT_Q5_K>(w, tok, x, pp, p); break;
+    default: embed_row<FMT_Q6_K>(w, tok, x, pp, p); break;
+    }
+}
+
+unsigned grid_for(int64_t n, int t = kThreads) { return (unsigned)((n + t - 1) / t); }
+
+}  // namespace
+
+hipError_t launch_rmsnorm(const float *x, const float *g, float *y, int rows, int n, float eps, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(kThreads), 0, s, x, g, y, n, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_layernorm(const float *x, const float *g, const float *b, float *y, int rows, int n,
+                            float eps, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_layernorm, dim3(rows), dim3(kThreads), 0, s, x, g, b, y, n, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(float *data, int n_heads, int seq, int hd, int pos0, const float *c,
+                       const float *sn, hipStream_t s)
+{
+    const int64_t total = (int64_t)n_heads * seq * (hd / 2);
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rope, dim3(grid_for(total)), dim3(kThreads), 0, s, data, n_heads, seq, hd,
+                       pos0, c, sn);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax(float *scores, float scale, int seq, int k_seq, int cache_off, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_softmax, dim3(seq), dim3(kThreads), 0, s, scores, scale, k_seq, cache_off);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_decode(const float *q, const float *kc, const float *vc, float *out,
+                                   int n_head, int n_kv_head, int hd, int ctx_stride,
+                                   const int32_t *pos_dev, int n_pos_fixed, int max_pos,
+                                   hipStream_t s)
+{
+    const size_t lds = (size_t)max_pos * 4;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_attention_decode,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(k_attention_decode, dim3(n_head), dim3(kThreads), lds, s, q, kc, vc, out,
+                       n_head, n_kv_head, hd, ctx_stride, pos_dev, n_pos_fixed);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const float *g, const float *u, float *y, int64_t n, hipStream_t s)
+{
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_silu_mul, dim3(grid_for(n)), dim3(kThreads), 0, s, g, u, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_gelu(const float *x, float *y, int64_t n, hipStream_t s)
+{
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_gelu, dim3(grid_for(n)), dim3(kThreads), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float *x, int n, int32_t *out, int32_t *tokens, int32_t *pos,
+                         hipStream_t s)
+{
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, x, n, out, tokens, pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(const WView &tok, const WView *posw, const int32_t *tokens,
+                        const int32_t *pos, float *x, hipStream_t s)
+{
+    WView pw = posw ? *posw : tok;
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(kThreads), 0, s, tok, pw, posw ? 1 : 0, tokens, pos, x);
+    return hipGetLastError();
+}
+
+hipError_t launch_advance(int32_t *pos, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, pos);
+    return hipGetLastError();
+}
+
+}  // namespace smx

@@ -1,0 +1,916 @@
+// runtime.cpp -- host runtime and C-ABI of libsmx.so.
+//
+// Model-level boundary: TransformerModel.Forward + KV cache (TransformerModel.cs:272-344,
+// :476-506) and the per-token driver InferenceSession.GenerateNextTokenAsync
+// (InferenceSession.cs:478-607).  A decode step is one pass of fused kernels:
+//
+//   embed -> per layer [ norm+QKV GEMV (+RoPE, K/V append) -> attention -> O GEMV (+residual)
+//                        -> norm+gate/up GEMV (+SwiGLU | GELU) -> down GEMV (+residual) ]
+//         -> final norm + head GEMV -> argmax (token appended, position advanced on device)
+//
+// The token array and the position live in device memory, so a step is captured once as a
+// hipGraph per session and replayed without host round trips.
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <atomic>
+#include <string>
+#include <vector>
+
+#include "smx_internal.h"
+
+namespace smx {
+
+static thread_local std::string g_err;
+void set_error(const std::string &msg) { g_err = msg; }
+const char *last_error() { return g_err.c_str(); }
+
+}  // namespace smx
+
+using namespace smx;
+
+#define SMX_FAIL(code, ...)                                          \
+    do {                                                             \
+        char _b[512];                                                \
+        snprintf(_b, sizeof(_b), __VA_ARGS__);                       \
+        set_error(_b);                                               \
+        return (code);                                               \
+    } while (0)
+
+#define SMX_HIP(expr)                                                                       \
+    do {                                                                                    \
+        hipError_t _e = (expr);                                                             \
+        if (_e != hipSuccess) SMX_FAIL(_e == hipErrorOutOfMemory ? SMX_ENOMEM : SMX_EDEVICE, \
+                                       "%s: %s", #expr, hipGetErrorString(_e));             \
+    } while (0)
+
+namespace {
+
+int type_block_elems(int type)
+{
+    switch (type) {
+    case SMX_TYPE_F32: case SMX_TYPE_F16: return 1;
+    case SMX_TYPE_Q4_0: case SMX_TYPE_Q8_0: return 32;
+    case SMX_TYPE_Q4_K: case SMX_TYPE_Q5_K: case SMX_TYPE_Q6_K: return 256;
+    default: return 0;
+    }
+}
+
+int type_block_bytes(int type)
+{
+    switch (type) {
+    case SMX_TYPE_F32: return 4;
+    case SMX_TYPE_F16: return 2;
+    case SMX_TYPE_Q4_0: return 18;
+    case SMX_TYPE_Q8_0: return 34;
+    case SMX_TYPE_Q4_K: return 144;
+    case SMX_TYPE_Q5_K: return 176;
+    case SMX_TYPE_Q6_K: return 210;
+    default: return 0;
+    }
+}
+
+// A weight matrix in the backend layout.
+struct Mat {
+    int fmt = -1;
+    int64_t rows = 0, cols = 0;
+    uint8_t *q = nullptr;
+    uint16_t *d = nullptr;
+    uint64_t rows_loaded = 0;   // bitmask of uploaded row groups (QKV: 1,2,4; gate/up: 1,2)
+
+    WView view() const
+    {
+        WView v;
+        v.fmt = fmt;
+        v.q = q;
+        v.d = d;
+        v.rows = rows;
+        v.cols = cols;
+        v.nb = fmt < 0 ? 0 : (int)(cols / fmt_block_elems(fmt));
+        return v;
+    }
+    int64_t bytes() const
+    {
+        if (fmt < 0) return 0;
+        const int64_t nb = cols / fmt_block_elems(fmt);
+        return rows * nb * (fmt_main_bytes(fmt) + (fmt_has_d(fmt) ? 2 : 0));
+    }
+    void release()
+    {
+        if (q) (void)hipFree(q);
+        if (d) (void)hipFree(d);
+        q = nullptr;
+        d = nullptr;
+        fmt = -1;
+    }
+};
+
+// Allocates m as [rows][cols] of fmt; no-op when already allocated with the same geometry.
+int mat_alloc(Mat &m, int fmt, int64_t rows, int64_t cols)
+{
+    if (m.fmt >= 0) {
+        if (m.fmt != fmt || m.rows != rows || m.cols != cols)
+            SMX_FAIL(SMX_EUNSUPPORTED, "fused matrix parts must share one quantization type "
+                                       "(have type fmt %d, got fmt %d)", m.fmt, fmt);
+        return SMX_OK;
+    }
+    const int64_t nb = cols / fmt_block_elems(fmt);
+    SMX_HIP(hipMalloc((void **)&m.q, (size_t)(rows * nb * fmt_main_bytes(fmt))));
+    if (fmt_has_d(fmt)) SMX_HIP(hipMalloc((void **)&m.d, (size_t)(rows * nb * 2)));
+    m.fmt = fmt;
+    m.rows = rows;
+    m.cols = cols;
+    return SMX_OK;
+}
+
+// Copies GGUF rows (host or device) into rows row_off + r*row_step of m.
+int mat_upload(Mat &m, const void *bytes, int64_t rows, int64_t cols, int on_device,
+               int64_t row_off, int64_t row_step, hipStream_t s)
+{
+    const size_t nbytes = (size_t)(rows * (cols / fmt_block_elems(m.fmt)) * fmt_gguf_bytes(m.fmt));
+    const uint8_t *src = (const uint8_t *)bytes;
+    uint8_t *staging = nullptr;
+    if (!on_device) {
+        SMX_HIP(hipMalloc((void **)&staging, nbytes));
+        hipError_t e = hipMemcpyAsync(staging, bytes, nbytes, hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) { (void)hipFree(staging); SMX_HIP(e); }
+        src = staging;
+    }
+    hipError_t e = launch_repack(m.fmt, src, rows, cols, m.q, m.d, m.rows, row_off, row_step, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (staging) (void)hipFree(staging);
+    SMX_HIP(e);
+    return SMX_OK;
+}
+
+}  // namespace
+
+struct smx_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+};
+
+struct smx_weight {
+    int type = 0;
+    Mat mat;
+};
+
+struct Layer {
+    Mat qkv, o, gu, down;
+    std::vector<float> attn_g, attn_b, ffn_g, ffn_b, bqkv, bo, bgu, bdown;
+    bool has_bqkv = false, has_bgu = false;
+    float *d_attn_g = nullptr, *d_attn_b = nullptr, *d_ffn_g = nullptr, *d_ffn_b = nullptr;
+    float *d_bqkv = nullptr, *d_bo = nullptr, *d_bgu = nullptr, *d_bdown = nullptr;
+};
+
+struct smx_model {
+    smx_context *ctx = nullptr;
+    smx_model_config cfg{};
+    int hd = 0, kvdim = 0, nqkv = 0, hidden = 0;
+    bool llama = true;
+    Mat tok, pos, head;
+    bool head_tied = false;
+    std::vector<float> out_g, out_b;
+    float *d_out_g = nullptr, *d_out_b = nullptr;
+    std::vector<Layer> layers;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    bool finalized = false;
+    std::atomic<int> sessions{0};
+};
+
+struct smx_session {
+    smx_model *m = nullptr;
+    int max_ctx = 0;
+    float *kc = nullptr, *vc = nullptr;
+    float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
+    int32_t *tokens = nullptr, *pos = nullptr, *amax = nullptr;
+    hipGraphExec_t g_prefill = nullptr, g_decode = nullptr;
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    std::atomic<int> busy{0};
+};
+
+namespace {
+
+void free_dev(void *p)
+{
+    if (p) (void)hipFree(p);
+}
+
+int upload_floats(float **dst, const std::vector<float> &v, hipStream_t s)
+{
+    if (v.empty()) return SMX_OK;
+    SMX_HIP(hipMalloc((void **)dst, v.size() * 4));
+    SMX_HIP(hipMemcpyAsync(*dst, v.data(), v.size() * 4, hipMemcpyHostToDevice, s));
+    return SMX_OK;
+}
+
+// Parses "blk.N.rest" -> N and rest; returns -1 for non-layer names.
+int parse_layer(const char *name, std::string &rest)
+{
+    int li = -1, consumed = 0;
+    if (sscanf(name, "blk.%d.%n", &li, &consumed) == 1 && consumed > 0) {
+        rest = name + consumed;
+        return li;
+    }
+    rest = name;
+    return -1;
+}
+
+// Builds the step's kernel sequence on stream s (captured into a graph by the caller).
+int enqueue_step(smx_session *S, bool with_head, hipStream_t s)
+{
+    smx_model *m = S->m;
+    const smx_model_config &c = m->cfg;
+    const int Hkv = c.n_kv_head, hd = m->hd;
+    const size_t layer_cache = (size_t)Hkv * S->max_ctx * hd;
+    WView posw = m->pos.view();
+    SMX_HIP(launch_embed(m->tok.view(), m->llama ? nullptr : &posw, S->tokens, S->pos, S->x, s));
+    for (int l = 0; l < c.n_layer; l++) {
+        Layer &L = m->layers[l];
+        GemvArgs a{};
+        a.w = L.qkv.view();
+        a.x = S->x;
+        a.out = S->q;
+        a.bias = L.d_bqkv;
+        a.gamma = L.d_attn_g;
+        a.beta = L.d_attn_b;
+        a.eps = c.norm_eps;
+        a.pro = m->llama ? PRO_RMS : PRO_LN;
+        a.epi = EPI_QKV;
+        a.d_model = c.d_model;
+        a.kv_dim = m->kvdim;
+        a.head_dim = hd;
+        a.ctx_stride = S->max_ctx;
+        a.use_rope = m->llama ? 1 : 0;
+        a.k_cache = S->kc + l * layer_cache;
+        a.v_cache = S->vc + l * layer_cache;
+        a.rope_cos = m->rope_cos;
+        a.rope_sin = m->rope_sin;
+        a.pos = S->pos;
+        SMX_HIP(launch_gemv(a, 1, s));
+
+        SMX_HIP(launch_attention_decode(S->q, a.k_cache, a.v_cache, S->att, c.n_head, Hkv, hd,
+                                        S->max_ctx, S->pos, 0, S->max_ctx, s));
+
+        GemvArgs o{};
+        o.w = L.o.view();
+        o.x = S->att;
+        o.out = S->x;
+        o.resid = S->x;
+        o.bias = L.d_bo;
+        o.pro = PRO_NONE;
+        o.epi = EPI_RESID;
+        SMX_HIP(launch_gemv(o, 1, s));
+
+        GemvArgs g{};
+        g.w = L.gu.view();
+        g.x = S->x;
+        g.out = S->h;
+        g.bias = L.d_bgu;
+        g.gamma = L.d_ffn_g;
+        g.beta = L.d_ffn_b;
+        g.eps = c.norm_eps;
+        g.pro = m->llama ? PRO_RMS : PRO_LN;
+        g.epi = m->llama ? EPI_SILU : EPI_GELU;
+        SMX_HIP(launch_gemv(g, 1, s));
+
+        GemvArgs dn{};
+        dn.w = L.down.view();
+        dn.x = S->h;
+        dn.out = S->x;
+        dn.resid = S->x;
+        dn.bias = L.d_bdown;
+        dn.pro = PRO_NONE;
+        dn.epi = EPI_RESID;
+        SMX_HIP(launch_gemv(dn, 1, s));
+    }
+    if (with_head) {
+        GemvArgs hgt{};
+        hgt.w = m->head.view();
+        hgt.x = S->x;
+        hgt.out = S->logits;
+        hgt.gamma = m->d_out_g;
+        hgt.beta = m->d_out_b;
+        hgt.eps = c.norm_eps;
+        hgt.pro = m->llama ? PRO_RMS : PRO_LN;
+        hgt.epi = EPI_STORE;
+        SMX_HIP(launch_gemv(hgt, 1, s));
+        SMX_HIP(launch_argmax(S->logits, c.vocab, S->amax, S->tokens, S->pos, s));
+    } else {
+        SMX_HIP(launch_advance(S->pos, s));
+    }
+    return SMX_OK;
+}
+
+int capture_step(smx_session *S, bool with_head, hipGraphExec_t *out)
+{
+    hipStream_t s = S->m->ctx->stream;
+    hipGraph_t graph = nullptr;
+    SMX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(S, with_head, s);
+    hipError_t e = hipStreamEndCapture(s, &graph);
+    if (rc != SMX_OK) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc;
+    }
+    SMX_HIP(e);
+    e = hipGraphInstantiate(out, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    SMX_HIP(e);
+    return SMX_OK;
+}
+
+struct BusyGuard {
+    std::atomic<int> &flag;
+    bool ok;
+    explicit BusyGuard(std::atomic<int> &f) : flag(f)
+    {
+        int expected = 0;
+        ok = flag.compare_exchange_strong(expected, 1);
+    }
+    ~BusyGuard()
+    {
+        if (ok) flag.store(0);
+    }
+};
+
+}  // namespace
+
+// =============================================================================================
+// C-ABI
+// =============================================================================================
+extern "C" {
+
+SMX_API const char *smx_version(void) { return "smx 0.1.0 (gfx950)"; }
+SMX_API const char *smx_last_error(void) { return smx::last_error(); }
+SMX_API int smx_type_block_elems(int type) { return type_block_elems(type); }
+SMX_API int smx_type_block_bytes(int type) { return type_block_bytes(type); }
+
+SMX_API int64_t smx_type_row_bytes(int type, int64_t k)
+{
+    const int be = type_block_elems(type);
+    if (!be || k < 0 || k % be) return -1;
+    return k / be * type_block_bytes(type);
+}
+
+SMX_API int smx_dequant(int type, const void *blocks_dev, int64_t n, float *out_dev, void *stream)
+{
+    if (!type_block_elems(type)) SMX_FAIL(SMX_EUNSUPPORTED, "smx_dequant: unsupported type %d", type);
+    if (n < 0 || (n > 0 && (!blocks_dev || !out_dev))) SMX_FAIL(SMX_EINVAL, "smx_dequant: bad arguments");
+    SMX_HIP(launch_dequant_gguf(type, blocks_dev, n, out_dev, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+SMX_API int smx_quantize(int type, const float *x_dev, int64_t n, void *blocks_dev, void *stream)
+{
+    const int be = type_block_elems(type);
+    if (!be || type == SMX_TYPE_F32) SMX_FAIL(SMX_EUNSUPPORTED, "smx_quantize: unsupported type %d", type);
+    if (n < 0 || n % be) SMX_FAIL(SMX_EINVAL, "smx_quantize: n=%lld is not a multiple of %d", (long long)n, be);
+    if (n > 0 && (!x_dev || !blocks_dev)) SMX_FAIL(SMX_EINVAL, "smx_quantize: null pointer");
+    SMX_HIP(launch_quantize_gguf(type, x_dev, n, blocks_dev, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+SMX_API int smx_fill_normal(uint64_t seed, int64_t n, float std, float *out_dev, void *stream)
+{
+    if (n < 0 || (n > 0 && !out_dev)) SMX_FAIL(SMX_EINVAL, "smx_fill_normal: bad arguments");
+    SMX_HIP(launch_fill_normal(seed, n, std, out_dev, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+// ---- IWeightTensor --------------------------------------------------------------------------
+SMX_API int smx_weight_create(int type, int64_t rows, int64_t cols, const void *blocks,
+                              int blocks_on_device, smx_weight **out)
+{
+    if (!out || !blocks) SMX_FAIL(SMX_EINVAL, "smx_weight_create: null argument");
+    *out = nullptr;
+    const int fmt = fmt_from_type(type);
+    if (fmt < 0) SMX_FAIL(SMX_EUNSUPPORTED, "smx_weight_create: type %d has no quantized GEMV", type);
+    if (rows <= 0 || cols <= 0 || cols % fmt_block_elems(fmt))
+        SMX_FAIL(SMX_EINVAL, "smx_weight_create: cols=%lld must be a positive multiple of %d",
+                 (long long)cols, fmt_block_elems(fmt));
+    if (cols > 16384) SMX_FAIL(SMX_EUNSUPPORTED, "smx_weight_create: cols=%lld exceeds 16384", (long long)cols);
+    smx_weight *w = new smx_weight();
+    w->type = type;
+    int rc = mat_alloc(w->mat, fmt, rows, cols);
+    if (rc == SMX_OK) rc = mat_upload(w->mat, blocks, rows, cols, blocks_on_device, 0, 1, nullptr);
+    if (rc != SMX_OK) {
+        w->mat.release();
+        delete w;
+        return rc;
+    }
+    *out = w;
+    return SMX_OK;
+}
+
+SMX_API int smx_weight_info(const smx_weight *w, int *type, int64_t *rows, int64_t *cols)
+{
+    if (!w) SMX_FAIL(SMX_EINVAL, "smx_weight_info: null weight");
+    if (type) *type = w->type;
+    if (rows) *rows = w->mat.rows;
+    if (cols) *cols = w->mat.cols;
+    return SMX_OK;
+}
+
+SMX_API int smx_weight_matmul(const smx_weight *w, const float *act_dev, float *out_dev, int m,
+                              int k, int n, void *stream)
+{
+    if (!w || !act_dev || !out_dev) SMX_FAIL(SMX_EINVAL, "smx_weight_matmul: null argument");
+    if (k != w->mat.cols || n != w->mat.rows)
+        SMX_FAIL(SMX_EINVAL, "smx_weight_matmul: k=%d must equal cols=%lld and n=%d rows=%lld", k,
+                 (long long)w->mat.cols, n, (long long)w->mat.rows);
+    if (m <= 0 || m > 65535) SMX_FAIL(SMX_EINVAL, "smx_weight_matmul: m=%d out of range", m);
+    GemvArgs a{};
+    a.w = w->mat.view();
+    a.x = act_dev;
+    a.x_stride = k;
+    a.out = out_dev;
+    a.out_stride = n;
+    a.pro = PRO_NONE;
+    a.epi = EPI_STORE;
+    SMX_HIP(launch_gemv(a, m, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+SMX_API int smx_weight_to_float32(const smx_weight *w, float *out_dev, void *stream)
+{
+    if (!w || !out_dev) SMX_FAIL(SMX_EINVAL, "smx_weight_to_float32: null argument");
+    SMX_HIP(launch_dequant_smx(w->mat.view(), 0, w->mat.rows, out_dev, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+SMX_API int smx_weight_destroy(smx_weight *w)
+{
+    if (!w) return SMX_OK;
+    w->mat.release();
+    delete w;
+    return SMX_OK;
+}
+
+// ---- elementwise / attention operators -------------------------------------------------------
+SMX_API int smx_rmsnorm(const float *x, const float *g, float *y, int rows, int n, float eps, void *stream)
+{
+    if (!x || !g || !y || rows <= 0 || n <= 0) SMX_FAIL(SMX_EINVAL, "smx_rmsnorm: bad arguments");
+    SMX_HIP(launch_rmsnorm(x, g, y, rows, n, eps, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+SMX_API int smx_layernorm(const float *x, const float *g, const float *b, float *y, int rows, int n,
+                          float eps, void *stream)
+{
+    if (!x || !g || !b || !y || rows <= 0 || n <= 0) SMX_FAIL(SMX_EINVAL, "smx_layernorm: bad arguments");
+    SMX_HIP(launch_layernorm(x, g, b, y, rows, n, eps, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+SMX_API int smx_rope_tables(int max_pos, int head_dim, float theta, float *cos_host, float *sin_host)
+{
+    if (max_pos <= 0 || head_dim <= 0 || head_dim % 2 || !cos_host || !sin_host)
+        SMX_FAIL(SMX_EINVAL, "smx_rope_tables: head_dim must be even and positive");
+    const int half = head_dim / 2;
+    for (int pos = 0; pos < max_pos; pos++)
+        for (int i = 0; i < half; i++) {
+            const float expo = (2.0f * (float)i) / (float)head_dim;
+            const float freq = 1.0f / powf(theta, expo);   // RotaryEmbedding.cs:52
+            const float angle = (float)pos * freq;
+            sin_host[pos * half + i] = sinf(angle);
+            cos_host[pos * half + i] = cosf(angle);
+        }
+    return SMX_OK;
+}
+
+SMX_API int smx_rope(float *data, int n_heads, int seq, int head_dim, int pos0, const float *c,
+                     const float *sn, void *stream)
+{
+    if (!data || !c || !sn || n_heads <= 0 || seq <= 0 || head_dim <= 0 || head_dim % 2 || pos0 < 0)
+        SMX_FAIL(SMX_EINVAL, "smx_rope: bad arguments");
+    SMX_HIP(launch_rope(data, n_heads, seq, head_dim, pos0, c, sn, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+SMX_API int smx_scale_mask_softmax(float *scores, float scale, int seq, int k_seq, int cache_offset,
+                                   void *stream)
+{
+    if (!scores || seq <= 0 || k_seq <= 0 || cache_offset < 0 || cache_offset + seq > k_seq)
+        SMX_FAIL(SMX_EINVAL, "smx_scale_mask_softmax: need 0 <= cache_offset and cache_offset+seq <= k_seq");
+    SMX_HIP(launch_softmax(scores, scale, seq, k_seq, cache_offset, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+SMX_API int smx_attention_decode(const float *q, const float *kc, const float *vc, float *out,
+                                 int n_head, int n_kv_head, int head_dim, int ctx_stride, int n_pos,
+                                 void *stream)
+{
+    if (!q || !kc || !vc || !out) SMX_FAIL(SMX_EINVAL, "smx_attention_decode: null pointer");
+    if (n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head)
+        SMX_FAIL(SMX_EINVAL, "smx_attention_decode: n_head must be a multiple of n_kv_head");
+    if (head_dim <= 0 || head_dim > 256 || head_dim % 4)
+        SMX_FAIL(SMX_EUNSUPPORTED, "smx_attention_decode: head_dim must be a multiple of 4 in [4, 256]");
+    if (n_pos <= 0 || n_pos > ctx_stride || ctx_stride > 40000)
+        SMX_FAIL(SMX_EINVAL, "smx_attention_decode: need 1 <= n_pos <= ctx_stride <= 40000");
+    SMX_HIP(launch_attention_decode(q, kc, vc, out, n_head, n_kv_head, head_dim, ctx_stride, nullptr,
+                                    n_pos, n_pos, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+SMX_API int smx_silu_mul(const float *g, const float *u, float *y, int64_t n, void *stream)
+{
+    if (!g || !u || !y || n < 0) SMX_FAIL(SMX_EINVAL, "smx_silu_mul: bad arguments");
+    SMX_HIP(launch_silu_mul(g, u, y, n, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+SMX_API int smx_gelu(const float *x, float *y, int64_t n, void *stream)
+{
+    if (!x || !y || n < 0) SMX_FAIL(SMX_EINVAL, "smx_gelu: bad arguments");
+    SMX_HIP(launch_gelu(x, y, n, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+SMX_API int smx_argmax(const float *x, int n, int32_t *out, void *stream)
+{
+    if (!x || !out || n <= 0) SMX_FAIL(SMX_EINVAL, "smx_argmax: bad arguments");
+    SMX_HIP(launch_argmax(x, n, out, nullptr, nullptr, (hipStream_t)stream));
+    return SMX_OK;
+}
+
+// ---- context / model ----------------------------------------------------------------------------
+SMX_API int smx_context_create(int device, smx_context **out)
+{
+    if (!out) SMX_FAIL(SMX_EINVAL, "smx_context_create: null out");
+    *out = nullptr;
+    int count = 0;
+    SMX_HIP(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count) SMX_FAIL(SMX_EINVAL, "smx_context_create: device %d of %d", device, count);
+    SMX_HIP(hipSetDevice(device));
+    smx_context *c = new smx_context();
+    c->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        SMX_HIP(e);
+    }
+    *out = c;
+    return SMX_OK;
+}
+
+SMX_API int smx_context_destroy(smx_context *c)
+{
+    if (!c) return SMX_OK;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+    return SMX_OK;
+}
+
+SMX_API int smx_model_create(smx_context *ctx, const smx_model_config *cfg, smx_model **out)
+{
+    if (!ctx || !cfg || !out) SMX_FAIL(SMX_EINVAL, "smx_model_create: null argument");
+    *out = nullptr;
+    const smx_model_config &c = *cfg;
+    if (c.arch != SMX_ARCH_LLAMA && c.arch != SMX_ARCH_GPT2)
+        SMX_FAIL(SMX_EUNSUPPORTED, "smx_model_create: arch %d", c.arch);
+    if (c.vocab <= 0 || c.ctx <= 0 || c.d_model <= 0 || c.n_layer <= 0 || c.n_head <= 0 || c.n_kv_head <= 0)
+        SMX_FAIL(SMX_EINVAL, "smx_model_create: non-positive dimension");
+    if (c.d_model % c.n_head) SMX_FAIL(SMX_EINVAL, "smx_model_create: d_model %% n_head != 0");
+    if (c.n_head % c.n_kv_head) SMX_FAIL(SMX_EINVAL, "smx_model_create: n_head %% n_kv_head != 0");
+    const int hd = c.d_model / c.n_head;
+    if (hd % 4 || hd > 256) SMX_FAIL(SMX_EUNSUPPORTED, "smx_model_create: head_dim %d", hd);
+    if (c.arch == SMX_ARCH_LLAMA && c.d_ff <= 0) SMX_FAIL(SMX_EINVAL, "smx_model_create: d_ff");
+    for (int i = 0; i < 6; i++) if (c.reserved[i]) SMX_FAIL(SMX_EINVAL, "smx_model_create: reserved fields must be 0");
+    smx_model *m = new smx_model();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->hd = hd;
+    m->kvdim = c.n_kv_head * hd;
+    m->nqkv = c.d_model + 2 * m->kvdim;
+    m->llama = c.arch == SMX_ARCH_LLAMA;
+    m->hidden = m->llama ? c.d_ff : 4 * c.d_model;   // MLP.cs:25-26
+    m->layers.resize(c.n_layer);
+    *out = m;
+    return SMX_OK;
+}
+
+static int model_upload_vec(smx_model *m, std::vector<float> &dst, int64_t n, int64_t off,
+                            int64_t step, int64_t total, int type, const int64_t *dims, int ndims,
+                            const void *bytes, size_t nbytes, int on_device)
+{
+    if (type != SMX_TYPE_F32) SMX_FAIL(SMX_EUNSUPPORTED, "1-D tensors must be F32 (got type %d)", type);
+    if (ndims != 1 || dims[0] != n) SMX_FAIL(SMX_EINVAL, "1-D tensor has %lld elements, expected %lld",
+                                             (long long)(ndims >= 1 ? dims[0] : -1), (long long)n);
+    if (nbytes != (size_t)n * 4) SMX_FAIL(SMX_EINVAL, "1-D tensor byte size %zu != %lld", nbytes, (long long)n * 4);
+    std::vector<float> tmp((size_t)n);
+    if (on_device) {
+        SMX_HIP(hipMemcpy(tmp.data(), bytes, nbytes, hipMemcpyDeviceToHost));
+    } else {
+        memcpy(tmp.data(), bytes, nbytes);
+    }
+    if (dst.empty()) dst.assign((size_t)total, 0.0f);
+    for (int64_t i = 0; i < n; i++) dst[(size_t)(off + i * step)] = tmp[(size_t)i];
+    (void)m;
+    return SMX_OK;
+}
+
+SMX_API int smx_model_upload_tensor(smx_model *m, const char *name, int type, const int64_t *dims,
+                                    int ndims, const void *bytes, size_t nbytes, int bytes_on_device)
+{
+    if (!m || !name || !dims || !bytes) SMX_FAIL(SMX_EINVAL, "smx_model_upload_tensor: null argument");
+    if (m->finalized) SMX_FAIL(SMX_ESTATE, "smx_model_upload_tensor: model already finalized");
+    SMX_HIP(hipSetDevice(m->ctx->device));
+    const smx_model_config &c = m->cfg;
+    const int64_t d = c.d_model, kv = m->kvdim, hid = m->hidden;
+    std::string rest;
+    const int li = parse_layer(name, rest);
+    if (li >= c.n_layer) SMX_FAIL(SMX_EINVAL, "%s: layer index out of range", name);
+
+    // 1-D tensors (norm weights and biases).
+    if (ndims == 1) {
+        if (li < 0) {
+            if (rest == "output_norm.weight") return model_upload_vec(m, m->out_g, d, 0, 1, d, type, dims, ndims, bytes, nbytes, bytes_on_device);
+            if (rest == "output_norm.bias") return model_upload_vec(m, m->out_b, d, 0, 1, d, type, dims, ndims, bytes, nbytes, bytes_on_device);
+            SMX_FAIL(SMX_EINVAL, "%s: unknown 1-D tensor", name);
+        }
+        Layer &L = m->layers[li];
+        const int64_t nq = m->nqkv;
+        if (rest == "attn_norm.weight") return model_upload_vec(m, L.attn_g, d, 0, 1, d, type, dims, ndims, bytes, nbytes, bytes_on_device);
+        if (rest == "attn_norm.bias") return model_upload_vec(m, L.attn_b, d, 0, 1, d, type, dims, ndims, bytes, nbytes, bytes_on_device);
+        if (rest == "ffn_norm.weight") return model_upload_vec(m, L.ffn_g, d, 0, 1, d, type, dims, ndims, bytes, nbytes, bytes_on_device);
+        if (rest == "ffn_norm.bias") return model_upload_vec(m, L.ffn_b, d, 0, 1, d, type, dims, ndims, bytes, nbytes, bytes_on_device);
+        if (rest == "attn_q.bias") { L.has_bqkv = true; return model_upload_vec(m, L.bqkv, d, 0, 1, nq, type, dims, ndims, bytes, nbytes, bytes_on_device); }
+        if (rest == "attn_k.bias") { L.has_bqkv = true; return model_upload_vec(m, L.bqkv, kv, d, 1, nq, type, dims, ndims, bytes, nbytes, bytes_on_device); }
+        if (rest == "attn_v.bias") { L.has_bqkv = true; return model_upload_vec(m, L.bqkv, kv, d + kv, 1, nq, type, dims, ndims, bytes, nbytes, bytes_on_device); }
+        if (rest == "attn_qkv.bias") { L.has_bqkv = true; return model_upload_vec(m, L.bqkv, nq, 0, 1, nq, type, dims, ndims, bytes, nbytes, bytes_on_device); }
+        if (rest == "attn_output.bias") return model_upload_vec(m, L.bo, d, 0, 1, d, type, dims, ndims, bytes, nbytes, bytes_on_device);
+        if (rest == "ffn_down.bias") return model_upload_vec(m, L.bdown, d, 0, 1, d, type, dims, ndims, bytes, nbytes, bytes_on_device);
+        if (m->llama) {
+            if (rest == "ffn_gate.bias") { L.has_bgu = true; return model_upload_vec(m, L.bgu, hid, 0, 2, 2 * hid, type, dims, ndims, bytes, nbytes, bytes_on_device); }
+            if (rest == "ffn_up.bias") { L.has_bgu = true; return model_upload_vec(m, L.bgu, hid, 1, 2, 2 * hid, type, dims, ndims, bytes, nbytes, bytes_on_device); }
+        } else if (rest == "ffn_up.bias") {
+            L.has_bgu = true;
+            return model_upload_vec(m, L.bgu, hid, 0, 1, hid, type, dims, ndims, bytes, nbytes, bytes_on_device);
+        }
+        SMX_FAIL(SMX_EINVAL, "%s: unknown 1-D tensor", name);
+    }
+
+    // 2-D weights: dims = {cols (ne0), rows}.
+    if (ndims != 2) SMX_FAIL(SMX_EINVAL, "%s: expected 1 or 2 dims, got %d", name, ndims);
+    const int64_t cols = dims[0], rows = dims[1];
+    const int fmt = fmt_from_type(type);
+    if (fmt < 0) SMX_FAIL(SMX_EUNSUPPORTED, "%s: weight type %d is not a supported block format", name, type);
+    if (cols <= 0 || rows <= 0 || cols % fmt_block_elems(fmt))
+        SMX_FAIL(SMX_EINVAL, "%s: ne0=%lld is not a multiple of the block size %d", name, (long long)cols, fmt_block_elems(fmt));
+    const size_t expect = (size_t)(rows * (cols / fmt_block_elems(fmt)) * fmt_gguf_bytes(fmt));
+    if (nbytes != expect) SMX_FAIL(SMX_EINVAL, "%s: %zu bytes, expected %zu", name, nbytes, expect);
+    hipStream_t s = m->ctx->stream;
+
+    struct Target { Mat *mat; int64_t rows_total, cols, rows, off, step; uint64_t bit; };
+    Target t{nullptr, 0, 0, 0, 0, 1, 1};
+    if (li < 0) {
+        if (rest == "token_embd.weight") t = {&m->tok, c.vocab, d, c.vocab, 0, 1, 1};
+        else if (rest == "position_embd.weight") t = {&m->pos, c.ctx, d, c.ctx, 0, 1, 1};
+        else if (rest == "output.weight") t = {&m->head, c.vocab, d, c.vocab, 0, 1, 1};
+        else SMX_FAIL(SMX_EINVAL, "%s: unknown tensor", name);
+    } else {
+        Layer &L = m->layers[li];
+        if (rest == "attn_q.weight") t = {&L.qkv, m->nqkv, d, d, 0, 1, 1};
+        else if (rest == "attn_k.weight") t = {&L.qkv, m->nqkv, d, kv, d, 1, 2};
+        else if (rest == "attn_v.weight") t = {&L.qkv, m->nqkv, d, kv, d + kv, 1, 4};
+        else if (rest == "attn_qkv.weight") t = {&L.qkv, m->nqkv, d, m->nqkv, 0, 1, 7};
+        else if (rest == "attn_output.weight") t = {&L.o, d, d, d, 0, 1, 1};
+        else if (rest == "ffn_down.weight") t = {&L.down, d, hid, d, 0, 1, 1};
+        else if (m->llama && rest == "ffn_gate.weight") t = {&L.gu, 2 * hid, d, hid, 0, 2, 1};
+        else if (m->llama && rest == "ffn_up.weight") t = {&L.gu, 2 * hid, d, hid, 1, 2, 2};
+        else if (!m->llama && rest == "ffn_up.weight") t = {&L.gu, hid, d, hid, 0, 1, 3};
+        else SMX_FAIL(SMX_EINVAL, "%s: unknown tensor", name);
+    }
+    if (cols != t.cols || rows != t.rows)
+        SMX_FAIL(SMX_EINVAL, "%s: shape [%lld x %lld], expected [%lld x %lld]", name, (long long)rows,
+                 (long long)cols, (long long)t.rows, (long long)t.cols);
+    if (cols > 16384) SMX_FAIL(SMX_EUNSUPPORTED, "%s: ne0=%lld exceeds 16384", name, (long long)cols);
+    int rc = mat_alloc(*t.mat, fmt, t.rows_total, t.cols);
+    if (rc != SMX_OK) return rc;
+    rc = mat_upload(*t.mat, bytes, rows, cols, bytes_on_device, t.off, t.step, s);
+    if (rc != SMX_OK) return rc;
+    t.mat->rows_loaded |= t.bit;
+    return SMX_OK;
+}
+
+SMX_API int smx_model_finalize(smx_model *m)
+{
+    if (!m) SMX_FAIL(SMX_EINVAL, "smx_model_finalize: null model");
+    if (m->finalized) return SMX_OK;
+    SMX_HIP(hipSetDevice(m->ctx->device));
+    const smx_model_config &c = m->cfg;
+    hipStream_t s = m->ctx->stream;
+    if (m->tok.fmt < 0) SMX_FAIL(SMX_ESTATE, "finalize: token_embd.weight missing");
+    if (m->out_g.empty()) SMX_FAIL(SMX_ESTATE, "finalize: output_norm.weight missing");
+    if (!m->llama && (m->pos.fmt < 0 || m->out_b.empty()))
+        SMX_FAIL(SMX_ESTATE, "finalize: gpt2 needs position_embd.weight and output_norm.bias");
+    if (m->head.fmt < 0) {   // GgufModelLoader.HandleWeightTying (GgufModelLoader.cs:1126-1147)
+        m->head = m->tok;
+        m->head_tied = true;
+    }
+    for (int l = 0; l < c.n_layer; l++) {
+        Layer &L = m->layers[l];
+        if (L.qkv.rows_loaded != 7) SMX_FAIL(SMX_ESTATE, "finalize: layer %d Q/K/V incomplete", l);
+        if (L.o.fmt < 0 || L.down.fmt < 0) SMX_FAIL(SMX_ESTATE, "finalize: layer %d attn_output/ffn_down missing", l);
+        if (L.gu.rows_loaded != 3) SMX_FAIL(SMX_ESTATE, "finalize: layer %d ffn gate/up incomplete", l);
+        if (L.attn_g.empty() || L.ffn_g.empty()) SMX_FAIL(SMX_ESTATE, "finalize: layer %d norm weights missing", l);
+        if (!m->llama && (L.attn_b.empty() || L.ffn_b.empty()))
+            SMX_FAIL(SMX_ESTATE, "finalize: layer %d LayerNorm biases missing", l);
+        int rc;
+        if ((rc = upload_floats(&L.d_attn_g, L.attn_g, s)) || (rc = upload_floats(&L.d_attn_b, L.attn_b, s)) ||
+            (rc = upload_floats(&L.d_ffn_g, L.ffn_g, s)) || (rc = upload_floats(&L.d_ffn_b, L.ffn_b, s)) ||
+            (rc = upload_floats(&L.d_bqkv, L.bqkv, s)) || (rc = upload_floats(&L.d_bo, L.bo, s)) ||
+            (rc = upload_floats(&L.d_bgu, L.bgu, s)) || (rc = upload_floats(&L.d_bdown, L.bdown, s)))
+            return rc;
+    }
+    int rc;
+    if ((rc = upload_floats(&m->d_out_g, m->out_g, s)) || (rc = upload_floats(&m->d_out_b, m->out_b, s)))
+        return rc;
+    if (m->llama) {
+        const size_t half = (size_t)m->hd / 2;
+        std::vector<float> cs((size_t)c.ctx * half), sn((size_t)c.ctx * half);
+        smx_rope_tables(c.ctx, m->hd, c.rope_theta, cs.data(), sn.data());
+        if ((rc = upload_floats(&m->rope_cos, cs, s)) || (rc = upload_floats(&m->rope_sin, sn, s))) return rc;
+    }
+    SMX_HIP(hipStreamSynchronize(s));
+    m->finalized = true;
+    return SMX_OK;
+}
+
+SMX_API int smx_model_weight_bytes(const smx_model *m, int64_t *bytes)
+{
+    if (!m || !bytes) SMX_FAIL(SMX_EINVAL, "smx_model_weight_bytes: null argument");
+    int64_t b = m->tok.bytes() + m->pos.bytes() + (m->head_tied ? 0 : m->head.bytes());
+    for (const Layer &L : m->layers) b += L.qkv.bytes() + L.o.bytes() + L.gu.bytes() + L.down.bytes();
+    *bytes = b;
+    return SMX_OK;
+}
+
+SMX_API int smx_model_destroy(smx_model *m)
+{
+    if (!m) return SMX_OK;
+    if (m->sessions.load() != 0) SMX_FAIL(SMX_ESTATE, "smx_model_destroy: sessions still open");
+    (void)hipSetDevice(m->ctx->device);
+    if (!m->head_tied) m->head.release();
+    m->tok.release();
+    m->pos.release();
+    for (Layer &L : m->layers) {
+        L.qkv.release(); L.o.release(); L.gu.release(); L.down.release();
+        free_dev(L.d_attn_g); free_dev(L.d_attn_b); free_dev(L.d_ffn_g); free_dev(L.d_ffn_b);
+        free_dev(L.d_bqkv); free_dev(L.d_bo); free_dev(L.d_bgu); free_dev(L.d_bdown);
+    }
+    free_dev(m->d_out_g); free_dev(m->d_out_b); free_dev(m->rope_cos); free_dev(m->rope_sin);
+    delete m;
+    return SMX_OK;
+}
+
+// ---- session ------------------------------------------------------------------------------------
+SMX_API int smx_session_destroy(smx_session *S);
+
+SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out)
+{
+    if (!m || !out) SMX_FAIL(SMX_EINVAL, "smx_session_create: null argument");
+    *out = nullptr;
+    if (!m->finalized) SMX_FAIL(SMX_ESTATE, "smx_session_create: model not finalized");
+    if (max_ctx <= 0 || max_ctx > m->cfg.ctx)
+        SMX_FAIL(SMX_EINVAL, "smx_session_create: max_ctx %d not in [1, %d]", max_ctx, m->cfg.ctx);
+    SMX_HIP(hipSetDevice(m->ctx->device));
+    smx_session *S = new smx_session();
+    S->m = m;
+    S->max_ctx = max_ctx;
+    m->sessions.fetch_add(1);
+    const smx_model_config &c = m->cfg;
+    const size_t cache = (size_t)c.n_layer * c.n_kv_head * max_ctx * m->hd * 4;
+    const size_t maxv = (size_t)(m->hidden > c.d_model ? m->hidden : c.d_model);
+    hipError_t e = hipSuccess;
+    auto A = [&](void **p, size_t n) { if (e == hipSuccess) e = hipMalloc(p, n); };
+    A((void **)&S->kc, cache);
+    A((void **)&S->vc, cache);
+    A((void **)&S->x, (size_t)c.d_model * 4);
+    A((void **)&S->q, (size_t)m->nqkv * 4);
+    A((void **)&S->att, (size_t)c.d_model * 4);
+    A((void **)&S->h, maxv * 4);
+    A((void **)&S->logits, (size_t)c.vocab * 4);
+    A((void **)&S->tokens, (size_t)(max_ctx + 1) * 4);
+    A((void **)&S->pos, 4);
+    A((void **)&S->amax, 4);
+    for (int i = 0; i < 3 && e == hipSuccess; i++) e = hipEventCreate(&S->ev[i]);
+    if (e == hipSuccess) e = hipMemsetAsync(S->tokens, 0, (size_t)(max_ctx + 1) * 4, m->ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(S->pos, 0, 4, m->ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->ctx->stream);
+    if (e != hipSuccess) {
+        smx_session_destroy(S);
+        SMX_HIP(e);
+    }
+    int rc = capture_step(S, false, &S->g_prefill);
+    if (rc == SMX_OK) rc = capture_step(S, true, &S->g_decode);
+    if (rc != SMX_OK) {
+        std::string msg = smx::last_error();
+        smx_session_destroy(S);
+        SMX_FAIL(rc, "%s", msg.c_str());
+    }
+    *out = S;
+    return SMX_OK;
+}
+
+static int check_tokens(const smx_session *S, const int32_t *t, int n)
+{
+    for (int i = 0; i < n; i++)
+        if (t[i] < 0 || t[i] >= S->m->cfg.vocab)
+            SMX_FAIL(SMX_ERANGE, "token %d at index %d outside [0, %d)", t[i], i, S->m->cfg.vocab);
+    return SMX_OK;
+}
+
+SMX_API int smx_session_forward(smx_session *S, const int32_t *tokens, int n_tokens, int pos_offset,
+                                float *logits_out)
+{
+    if (!S || !tokens || n_tokens <= 0 || pos_offset < 0) SMX_FAIL(SMX_EINVAL, "smx_session_forward: bad arguments");
+    BusyGuard guard(S->busy);
+    if (!guard.ok) SMX_FAIL(SMX_EBUSY, "smx_session_forward: session in use on another thread");
+    if ((int64_t)pos_offset + n_tokens > S->max_ctx)
+        SMX_FAIL(SMX_ERANGE, "sequence length %d + offset %d exceeds block size %d", n_tokens, pos_offset, S->max_ctx);
+    int rc = check_tokens(S, tokens, n_tokens);
+    if (rc != SMX_OK) return rc;
+    SMX_HIP(hipSetDevice(S->m->ctx->device));
+    hipStream_t s = S->m->ctx->stream;
+    const int32_t p0 = pos_offset;
+    SMX_HIP(hipMemcpyAsync(S->tokens + pos_offset, tokens, (size_t)n_tokens * 4, hipMemcpyHostToDevice, s));
+    SMX_HIP(hipMemcpyAsync(S->pos, &p0, 4, hipMemcpyHostToDevice, s));
+    for (int i = 0; i + 1 < n_tokens; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
+    SMX_HIP(hipGraphLaunch(S->g_decode, s));
+    if (logits_out)
+        SMX_HIP(hipMemcpyAsync(logits_out, S->logits, (size_t)S->m->cfg.vocab * 4, hipMemcpyDeviceToHost, s));
+    SMX_HIP(hipStreamSynchronize(s));
+    return SMX_OK;
+}
+
+SMX_API int smx_session_generate(smx_session *S, const int32_t *prompt, int n_prompt, int n_new,
+                                 int32_t *out_tokens, float *logits_out, smx_gen_stats *stats)
+{
+    if (!S || !prompt || !out_tokens || n_prompt <= 0 || n_new <= 0)
+        SMX_FAIL(SMX_EINVAL, "smx_session_generate: bad arguments");
+    BusyGuard guard(S->busy);
+    if (!guard.ok) SMX_FAIL(SMX_EBUSY, "smx_session_generate: session in use on another thread");
+    if ((int64_t)n_prompt + n_new - 1 > S->max_ctx)
+        SMX_FAIL(SMX_ERANGE, "prompt %d + new tokens %d exceed the session context %d", n_prompt, n_new, S->max_ctx);
+    int rc = check_tokens(S, prompt, n_prompt);
+    if (rc != SMX_OK) return rc;
+    SMX_HIP(hipSetDevice(S->m->ctx->device));
+    hipStream_t s = S->m->ctx->stream;
+    const int V = S->m->cfg.vocab;
+    const int32_t zero = 0;
+    SMX_HIP(hipMemcpyAsync(S->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s));
+    SMX_HIP(hipMemcpyAsync(S->pos, &zero, 4, hipMemcpyHostToDevice, s));
+    SMX_HIP(hipEventRecord(S->ev[0], s));
+    for (int i = 0; i + 1 < n_prompt; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
+    SMX_HIP(hipEventRecord(S->ev[1], s));
+    for (int i = 0; i < n_new; i++) {
+        SMX_HIP(hipGraphLaunch(S->g_decode, s));
+        if (logits_out)
+            SMX_HIP(hipMemcpyAsync(logits_out + (size_t)i * V, S->logits, (size_t)V * 4, hipMemcpyDeviceToHost, s));
+    }
+    SMX_HIP(hipEventRecord(S->ev[2], s));
+    SMX_HIP(hipMemcpyAsync(out_tokens, S->tokens + n_prompt, (size_t)n_new * 4, hipMemcpyDeviceToHost, s));
+    SMX_HIP(hipStreamSynchronize(s));
+    if (stats) {
+        float a = 0.0f, b = 0.0f;
+        SMX_HIP(hipEventElapsedTime(&a, S->ev[0], S->ev[1]));
+        SMX_HIP(hipEventElapsedTime(&b, S->ev[1], S->ev[2]));
+        stats->prefill_ms = a;
+        stats->decode_ms = b;
+        stats->n_prefill_steps = n_prompt - 1;
+        stats->n_decode_steps = n_new;
+    }
+    return SMX_OK;
+}
+
+SMX_API int smx_session_reset(smx_session *S)
+{
+    if (!S) SMX_FAIL(SMX_EINVAL, "smx_session_reset: null session");
+    BusyGuard guard(S->busy);
+    if (!guard.ok) SMX_FAIL(SMX_EBUSY, "smx_session_reset: session in use on another thread");
+    SMX_HIP(hipSetDevice(S->m->ctx->device));
+    const int32_t zero = 0;
+    SMX_HIP(hipMemcpyAsync(S->pos, &zero, 4, hipMemcpyHostToDevice, S->m->ctx->stream));
+    SMX_HIP(hipStreamSynchronize(S->m->ctx->stream));
+    return SMX_OK;
+}
+
+SMX_API int smx_session_destroy(smx_session *S)
+{
+    if (!S) return SMX_OK;
+    (void)hipSetDevice(S->m->ctx->device);
+    if (S->g_prefill) (void)hipGraphExecDestroy(S->g_prefill);
+    if (S->g_decode) (void)hipGraphExecDestroy(S->g_decode);
+    for (hipEvent_t e : S->ev) if (e) (void)hipEventDestroy(e);
+    free_dev(S->kc); free_dev(S->vc); free_dev(S->x); free_dev(S->q); free_dev(S->att);
+    free_dev(S->h); free_dev(S->logits); free_dev(S->tokens); free_dev(S->pos); free_dev(S->amax);
+    S->m->sessions.fetch_sub(1);
+    delete S;
+    return SMX_OK;
+}
+
+}  // extern "C"

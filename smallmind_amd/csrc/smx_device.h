@@ -1,0 +1,153 @@
+// smx_device.h -- device helpers shared by the HIP kernels of libsmx.so.
+//
+// Everything here is compiled with -ffp-contract=off: a*b+c is never fused unless written
+// as __builtin_fmaf, so the scalar formulas below round exactly like the C# reference.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace smx {
+
+// fp16 bits -> fp32, bit-identical to GgufModelLoader.HalfToFloat (GgufModelLoader.cs:919-956)
+// for every pattern: subnormals are exact (m * 2^-24 is a normal fp32), Inf/NaN keep payload.
+__device__ __forceinline__ float h2f_exact(uint32_t h)
+{
+    uint32_t sign = (h >> 15) & 1u, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    if (e == 0) {
+        float v = (float)m * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    }
+    uint32_t r = e == 0x1F ? ((sign << 31) | 0x7F800000u | (m << 13))
+                           : ((sign << 31) | ((e + 112u) << 23) | (m << 13));
+    return __uint_as_float(r);
+}
+
+// fp16 bits -> fp32 with the hardware conversion (exact for all finite values; used in the
+// GEMV hot loops where NaN payloads do not matter).
+__device__ __forceinline__ float h2f(uint32_t h)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// fp32 -> fp16 bits, round to nearest even; the same integer routine as the oracle's
+// smxo_float_to_half, so CPU and GPU encoders store identical scales.
+__device__ __forceinline__ uint32_t f2h_rne(float f)
+{
+    uint32_t x = __float_as_uint(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return sign | (ax > 0x7F800000u ? 0x7E00u : 0x7C00u);
+    if (ax >= 0x47800000u) return sign | 0x7C00u;
+    if (ax < 0x38800000u) {
+        if (ax < 0x33000000u) return sign;
+        uint32_t e = ax >> 23;
+        uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+        uint32_t shift = 126u - e;
+        uint32_t hm = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t halfway = 1u << (shift - 1u);
+        if (rem > halfway || (rem == halfway && (hm & 1u))) hm++;
+        return sign | hm;
+    }
+    uint32_t h = (((ax >> 23) - 112u) << 10) | ((ax & 0x7FFFFFu) >> 13);
+    uint32_t rem = ax & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return sign | h;
+}
+
+// MathUtils.FastExp (src/SmallMind.Core/Utilities/MathUtils.cs:20-32).
+__device__ __forceinline__ float fastexp(float x)
+{
+    x = fmaxf(-87.3f, fminf(x, 88.7f));
+    float x2 = x * x;
+    float h = x * 0.5f, q = x2 * 0.08333333f;
+    float num = 1.0f + h;
+    num = num + q;
+    float den = 1.0f - h;
+    den = den + q;
+    return num / den;
+}
+
+// ActivationOps.GELU vector form (src/SmallMind.Core/Simd/ActivationOps.cs:262-276).
+__device__ __forceinline__ float gelu_pade(float x)
+{
+    float x2 = x * x;
+    float x3 = x2 * x;
+    float t3 = 0.044715f * x3;
+    float inner = 0.7978845608f * (x + t3);
+    inner = fmaxf(-10.0f, fminf(10.0f, inner));
+    float inner2 = inner * inner;
+    float num = inner * (27.0f + inner2);
+    float den = 27.0f + 9.0f * inner2;
+    float th = num / den;
+    float hx = 0.5f * x;
+    return hx * (1.0f + th);
+}
+
+// ActivationOps.FusedSiLUMul element (ActivationOps.cs:565-580, FastSigmoid :304-309).
+__device__ __forceinline__ float silu_mul(float x, float u)
+{
+    float c = fmaxf(-20.0f, fminf(x, 20.0f));
+    float sig = 1.0f / (1.0f + expf(-c));
+    float silu = x * sig;
+    return silu * u;
+}
+
+// ---- wave64 / block reductions ------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Block-wide sum for blockDim.x == 64 * nw (nw <= 16); red must hold 16 floats.  Every
+// thread receives the same value; the order of additions is fixed, so every block that sums
+// the same data gets the same bits.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float *red)
+{
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NW; i++) t += red[i];
+    return t;
+}
+
+template <int NW>
+__device__ __forceinline__ float block_max(float v, float *red)
+{
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int i = 1; i < NW; i++) t = fmaxf(t, red[i]);
+    return t;
+}
+
+__device__ __forceinline__ uint32_t ld_u32_unaligned(const uint8_t *p)
+{
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p)
+{
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8);
+}
+
+}  // namespace smx

@@ -1,0 +1,120 @@
+// smx_internal.h -- definitions shared by the kernels and the host runtime of libsmx.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/smx.h"
+
+namespace smx {
+
+// ---- backend ("smx") weight layouts -------------------------------------------------------
+//
+// All layouts are row-major over the [rows][cols] weight; every row is an integral number of
+// blocks.  Each row's main-stream bytes are a multiple of 16, so every 16-byte load is aligned.
+//
+//  Q4_0  main: [row][blk][16]   nibbles as in GGUF (element 2i low, 2i+1 high)
+//        d   : [row][blk] fp16
+//  Q8_0  main: [row][blk][32]   int8 as in GGUF
+//        d   : [row][blk] fp16
+//  Q4_K  main: [row][sb][144]   the GGUF super-block unchanged (16 B header + 128 B qs)
+//  Q5_K  main: [row][sb][176]   header 16 B | qh' 32 B | ql 128 B.  qh' is a bit permutation of
+//                               GGUF qh: dword j (elements 32j..32j+31), byte k, bit (2g+p)
+//                               holds the high bit of element 32j + 8g + 2k + p.
+//  Q6_K  main: [row][sb][208]   ql 128 B | qh' 64 B | int8 scales 16 B;  d: [row][sb] fp16.
+//                               qh' chunk c = dwords (D0, D1) at 128 + 8c; D_p byte k bits
+//                               (2g, 2g+1) hold the two high bits of element 32c + 8g + 2k + p.
+//
+// The permutations put the high bits of the four elements that share one byte position of a
+// 4-byte group of ql at the same bit offset of four consecutive bytes, so one shift and one
+// and-or rebuild four 5-/6-bit codes.
+
+enum Fmt { FMT_Q4_0 = 0, FMT_Q8_0 = 1, FMT_Q4_K = 2, FMT_Q5_K = 3, FMT_Q6_K = 4, FMT_COUNT = 5 };
+
+__host__ __device__ constexpr int fmt_block_elems(int f) { return f <= FMT_Q8_0 ? 32 : 256; }
+__host__ __device__ constexpr int fmt_main_bytes(int f)
+{
+    return f == FMT_Q4_0 ? 16 : f == FMT_Q8_0 ? 32 : f == FMT_Q4_K ? 144 : f == FMT_Q5_K ? 176 : 208;
+}
+__host__ __device__ constexpr bool fmt_has_d(int f) { return f == FMT_Q4_0 || f == FMT_Q8_0 || f == FMT_Q6_K; }
+__host__ __device__ constexpr int fmt_gguf_bytes(int f)
+{
+    return f == FMT_Q4_0 ? 18 : f == FMT_Q8_0 ? 34 : f == FMT_Q4_K ? 144 : f == FMT_Q5_K ? 176 : 210;
+}
+
+int fmt_from_type(int type);   // -1 if not a block-quantized type
+
+struct WView {
+    int fmt;              // Fmt
+    const uint8_t *q;     // main stream
+    const uint16_t *d;    // fp16 scale stream or nullptr
+    int64_t rows, cols;
+    int nb;               // blocks per row
+};
+
+// ---- GEMV prologue / epilogue selectors ---------------------------------------------------
+enum Pro { PRO_NONE = 0, PRO_RMS = 1, PRO_LN = 2 };
+enum Epi {
+    EPI_STORE = 0,   // out[r] = acc + bias
+    EPI_RESID = 1,   // out[r] = resid[r] + (acc + bias)
+    EPI_SILU = 2,    // rows interleaved gate/up: out[i] = silu(g) * u
+    EPI_GELU = 3,    // out[r] = gelu(acc + bias)
+    EPI_QKV = 4      // rows [Q | K | V]: RoPE on Q/K, Q -> out, K/V -> caches at *pos
+};
+
+struct GemvArgs {
+    WView w;
+    const float *x;        // [m][cols]
+    int64_t x_stride;
+    float *out;            // [m][out_stride]
+    int64_t out_stride;
+    const float *bias;     // [rows] or nullptr (interleaved like the rows for EPI_SILU)
+    const float *resid;    // EPI_RESID
+    const float *gamma;    // PRO_RMS / PRO_LN
+    const float *beta;     // PRO_LN
+    float eps;
+    int pro, epi;
+    // EPI_QKV
+    int d_model, kv_dim, head_dim, ctx_stride, use_rope;
+    float *k_cache, *v_cache;   // [n_kv_head][ctx_stride][head_dim] of this layer
+    const float *rope_cos, *rope_sin;   // [ctx][head_dim/2]
+    const int32_t *pos;         // device position
+};
+
+hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s);
+
+// ---- other kernels -------------------------------------------------------------------------
+hipError_t launch_dequant_gguf(int type, const void *blocks, int64_t n, float *out, hipStream_t s);
+hipError_t launch_quantize_gguf(int type, const float *x, int64_t n, void *blocks, hipStream_t s);
+hipError_t launch_fill_normal(uint64_t seed, int64_t n, float std, float *out, hipStream_t s);
+// GGUF rows [rows][cols] -> smx layout rows dst_row = row_off + r * row_step.
+hipError_t launch_repack(int fmt, const uint8_t *gguf, int64_t rows, int64_t cols, uint8_t *dst_q,
+                         uint16_t *dst_d, int64_t dst_rows, int64_t row_off, int64_t row_step,
+                         hipStream_t s);
+hipError_t launch_dequant_smx(const WView &w, int64_t row0, int64_t nrows, float *out, hipStream_t s);
+
+hipError_t launch_rmsnorm(const float *x, const float *g, float *y, int rows, int n, float eps, hipStream_t s);
+hipError_t launch_layernorm(const float *x, const float *g, const float *b, float *y, int rows, int n,
+                            float eps, hipStream_t s);
+hipError_t launch_rope(float *data, int n_heads, int seq, int hd, int pos0, const float *c,
+                       const float *sn, hipStream_t s);
+hipError_t launch_softmax(float *scores, float scale, int seq, int k_seq, int cache_off, hipStream_t s);
+hipError_t launch_attention_decode(const float *q, const float *kc, const float *vc, float *out,
+                                   int n_head, int n_kv_head, int hd, int ctx_stride,
+                                   const int32_t *pos_dev, int n_pos_fixed, int max_pos,
+                                   hipStream_t s);
+hipError_t launch_silu_mul(const float *g, const float *u, float *y, int64_t n, hipStream_t s);
+hipError_t launch_gelu(const float *x, float *y, int64_t n, hipStream_t s);
+hipError_t launch_argmax(const float *x, int n, int32_t *out, int32_t *tokens, int32_t *pos,
+                         hipStream_t s);
+hipError_t launch_embed(const WView &tok, const WView *posw, const int32_t *tokens,
+                        const int32_t *pos, float *x, hipStream_t s);
+hipError_t launch_advance(int32_t *pos, hipStream_t s);
+
+// ---- errors --------------------------------------------------------------------------------
+void set_error(const std::string &msg);
+const char *last_error();
+
+}  // namespace smx

@@ -1,0 +1,168 @@
+"""Model / session level of the backend.
+
+GpuTransformerModel replaces TransformerModel (TransformerModel.cs:81-344) for inference:
+weights are uploaded by GGUF tensor name (as GgufModelLoader maps them, GgufModelLoader.cs:
+117-187, with the Q/K/V merge of :1027-1110 and the weight tying of :1126-1147) and stay
+quantized on the device.  GpuInferenceSession mirrors the KV-cached Forward(idx,
+positionOffset) calls InferenceSession makes (InferenceSession.cs:478-546) and adds greedy
+generation that runs entirely on the device.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import ARCH_GPT2, ARCH_LLAMA, GenStatsC, ModelConfigC, call, load
+
+
+@dataclass
+class ModelConfig:
+    """Fields of SmallMind's ModelConfig (ModelConfig.cs:142-258) the forward path reads."""
+    architecture: str            # "llama" (RoPE, RMSNorm, SwiGLU) or "gpt2" (learned pos, LayerNorm, GELU)
+    vocab_size: int
+    context_length: int
+    embedding_length: int
+    block_count: int
+    head_count: int
+    head_count_kv: int
+    feed_forward_length: int
+    rope_freq_base: float = 10000.0
+    norm_eps: float = 1e-5
+
+    @property
+    def head_dim(self) -> int:
+        return self.embedding_length // self.head_count
+
+    @property
+    def kv_dim(self) -> int:
+        return self.head_count_kv * self.head_dim
+
+    @property
+    def hidden_dim(self) -> int:
+        return 4 * self.embedding_length if self.architecture == "gpt2" else self.feed_forward_length
+
+    def to_c(self) -> ModelConfigC:
+        c = ModelConfigC()
+        c.arch = ARCH_GPT2 if self.architecture == "gpt2" else ARCH_LLAMA
+        c.vocab = self.vocab_size
+        c.ctx = self.context_length
+        c.d_model = self.embedding_length
+        c.n_layer = self.block_count
+        c.n_head = self.head_count
+        c.n_kv_head = self.head_count_kv
+        c.d_ff = self.feed_forward_length
+        c.rope_theta = self.rope_freq_base
+        c.norm_eps = self.norm_eps
+        return c
+
+
+class GpuContext:
+    def __init__(self, device: int = 0):
+        load()
+        self._h = ctypes.c_void_p()
+        call("smx_context_create", device, ctypes.byref(self._h))
+        self.device = device
+
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            call("smx_context_destroy", self._h)
+            self._h = ctypes.c_void_p()
+
+
+class GpuTransformerModel:
+    """TransformerModel for the GPU backend (weights stay quantized on the device)."""
+
+    def __init__(self, config: ModelConfig, context: GpuContext | None = None, device: int = 0):
+        self.config = config
+        self.context = context or GpuContext(device)
+        self._own_ctx = context is None
+        self._cfg = config.to_c()
+        self._h = ctypes.c_void_p()
+        call("smx_model_create", self.context._h, ctypes.byref(self._cfg), ctypes.byref(self._h))
+        self._sessions = []
+
+    def load_tensor(self, name: str, qtype: int, dims, data):
+        """Uploads one GGUF tensor.  dims are GGUF order (ne0 first).  data is a host buffer
+        (numpy / bytes) or a device torch tensor."""
+        d = (ctypes.c_int64 * len(dims))(*[int(x) for x in dims])
+        if isinstance(data, (bytes, bytearray, np.ndarray)):
+            buf = np.ascontiguousarray(np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray)
+                                       else data).view(np.uint8).reshape(-1)
+            call("smx_model_upload_tensor", self._h, name.encode(), int(qtype), d, len(dims),
+                 buf.ctypes.data_as(ctypes.c_void_p), buf.size, 0)
+        else:
+            import torch
+            if not data.is_cuda or not data.is_contiguous():
+                raise ValueError("device tensors must be contiguous cuda tensors")
+            torch.cuda.synchronize()
+            call("smx_model_upload_tensor", self._h, name.encode(), int(qtype), d, len(dims),
+                 ctypes.c_void_p(data.data_ptr()), data.numel() * data.element_size(), 1)
+
+    def finalize(self):
+        call("smx_model_finalize", self._h)
+
+    def weight_bytes(self) -> int:
+        b = ctypes.c_int64()
+        call("smx_model_weight_bytes", self._h, ctypes.byref(b))
+        return b.value
+
+    def create_session(self, max_ctx: int | None = None) -> "GpuInferenceSession":
+        s = GpuInferenceSession(self, max_ctx or self.config.context_length)
+        self._sessions.append(s)
+        return s
+
+    def close(self):
+        for s in self._sessions:
+            s.close()
+        self._sessions = []
+        if getattr(self, "_h", None) and self._h.value:
+            call("smx_model_destroy", self._h)
+            self._h = ctypes.c_void_p()
+        if self._own_ctx:
+            self.context.close()
+
+
+class GpuInferenceSession:
+    """KV-cached decoding session (one HIP stream, one captured decode-step graph).
+
+    Not thread-safe, like InferenceSession (InferenceSession.cs:127-144): concurrent use
+    raises SmxError with SMX_EBUSY."""
+
+    def __init__(self, model: GpuTransformerModel, max_ctx: int):
+        self.model = model
+        self.max_ctx = max_ctx
+        self._h = ctypes.c_void_p()
+        call("smx_session_create", model._h, max_ctx, ctypes.byref(self._h))
+
+    def forward(self, tokens, position_offset: int, want_logits: bool = True):
+        """TransformerModel.Forward(idx[1,T], positionOffset) with the KV cache enabled;
+        returns the last row's logits."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
+        out = np.empty(self.model.config.vocab_size, np.float32) if want_logits else None
+        call("smx_session_forward", self._h, t.ctypes.data_as(ctypes.c_void_p), t.size,
+             position_offset, out.ctypes.data_as(ctypes.c_void_p) if want_logits else None)
+        return out
+
+    def generate_greedy(self, prompt, max_new_tokens: int, return_logits: bool = False):
+        """Prefill + greedy decode on the device.  Returns (tokens, stats[, logits])."""
+        p = np.ascontiguousarray(prompt, dtype=np.int32).reshape(-1)
+        toks = np.empty(max_new_tokens, np.int32)
+        logits = (np.empty((max_new_tokens, self.model.config.vocab_size), np.float32)
+                  if return_logits else None)
+        st = GenStatsC()
+        call("smx_session_generate", self._h, p.ctypes.data_as(ctypes.c_void_p), p.size,
+             max_new_tokens, toks.ctypes.data_as(ctypes.c_void_p),
+             logits.ctypes.data_as(ctypes.c_void_p) if return_logits else None, ctypes.byref(st))
+        stats = {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
+                 "prefill_steps": st.n_prefill_steps, "decode_steps": st.n_decode_steps}
+        return (toks, stats, logits) if return_logits else (toks, stats)
+
+    def reset_kv_cache(self):
+        call("smx_session_reset", self._h)
+
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            call("smx_session_destroy", self._h)
+            self._h = ctypes.c_void_p()

@@ -1,0 +1,79 @@
+"""Shared builders for the parity tests: one set of seeded GGUF bytes feeds both the CPU oracle
+and the GPU backend."""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle as O
+
+TYPES = {"Q4_0": O.Q4_0, "Q8_0": O.Q8_0, "Q4_K": O.Q4_K, "Q5_K": O.Q5_K, "Q6_K": O.Q6_K}
+
+
+def random_blocks(qtype: int, nblocks: int, seed: int) -> np.ndarray:
+    """Random bytes for every field, with the fp16 scale fields forced finite (the reference's
+    HalfToFloat keeps NaN payloads, which no fp32 product reproduces bit-for-bit)."""
+    rng = np.random.default_rng(seed)
+    bb = O.BLOCK_BYTES[qtype]
+    b = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+
+    def finite_half(col):
+        h = b[:, col].astype(np.uint16) | (b[:, col + 1].astype(np.uint16) << 8)
+        bad = (h & 0x7C00) == 0x7C00
+        h = np.where(bad, h & 0xBBFF, h)   # clear one exponent bit
+        b[:, col] = (h & 0xFF).astype(np.uint8)
+        b[:, col + 1] = (h >> 8).astype(np.uint8)
+
+    if qtype in (O.Q4_0, O.Q8_0, O.Q4_K, O.Q5_K):
+        finite_half(0)
+    if qtype in (O.Q4_K, O.Q5_K):
+        finite_half(2)
+    if qtype == O.Q6_K:
+        finite_half(208)
+    return b.reshape(-1)
+
+
+def quantized(qtype: int, shape, seed: int, std: float = 0.02):
+    x = np.random.default_rng(seed).normal(0.0, std, size=int(np.prod(shape))).astype(np.float32)
+    return O.quantize(qtype, x)
+
+
+def model_specs(cfg, layer_type, embd_type, head_type):
+    from smallmind_amd.synthetic import tensor_specs
+    return tensor_specs(cfg, layer_type, embd_type, head_type)
+
+
+def build_pair(cfg, layer_type, embd_type, head_type, seed=1234, random_norms=True, with_gpu=True):
+    """Returns (oracle_model, gpu_model or None, {name: (qtype, dims, host bytes)})."""
+    rng = np.random.default_rng(seed)
+    arch = O.ARCH_GPT2 if cfg.architecture == "gpt2" else O.ARCH_LLAMA
+    om = O.OracleModel(arch, cfg.vocab_size, cfg.context_length, cfg.embedding_length,
+                       cfg.block_count, cfg.head_count, cfg.head_count_kv, cfg.feed_forward_length,
+                       cfg.rope_freq_base, cfg.norm_eps)
+    gm = None
+    if with_gpu:
+        from smallmind_amd.model import GpuTransformerModel
+        gm = GpuTransformerModel(cfg)
+    tensors = {}
+    for s in model_specs(cfg, layer_type, embd_type, head_type):
+        if s.kind == "norm":
+            data = (rng.normal(1.0, 0.1, s.n) if random_norms else np.ones(s.n)).astype(np.float32)
+        elif s.kind == "bias0":
+            data = (rng.normal(0.0, 0.05, s.n) if random_norms else np.zeros(s.n)).astype(np.float32)
+        elif s.kind == "bias":
+            data = rng.normal(0.0, 0.02, s.n).astype(np.float32)
+        else:
+            data = O.quantize(s.qtype, rng.normal(0.0, 0.02, s.n).astype(np.float32))
+        om.set_tensor(s.name, s.qtype, data, s.n)
+        if gm is not None:
+            gm.load_tensor(s.name, s.qtype, s.dims, data)
+        tensors[s.name] = (s.qtype, s.dims, data)
+    om.finalize()
+    if gm is not None:
+        gm.finalize()
+    return om, gm, tensors
+
+
+def rel_err(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))

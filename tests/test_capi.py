@@ -1,0 +1,60 @@
+"""CPU checks of the C-ABI library: it loads, exports every function include/smx.h declares,
+and its host-only entry points behave (no device calls here)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+
+import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "smx.h")).read()
+    return sorted(set(re.findall(r"SMX_API[^;(]*?\b(smx_\w+)\s*\(", text, re.S)))
+
+
+def test_library_exports_every_declared_symbol():
+    from smallmind_amd import _lib
+    L = _lib.load()
+    declared = _declared()
+    assert len(declared) >= 30
+    for name in declared:
+        assert hasattr(L, name), name
+    assert sorted(_lib.EXPORTS) == declared
+
+
+def test_type_geometry():
+    from smallmind_amd import _lib
+    L = _lib.load()
+    for t in (O.F32, O.F16, O.Q4_0, O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K):
+        assert L.smx_type_block_elems(t) == O.BLOCK_ELEMS[t]
+        assert L.smx_type_block_bytes(t) == O.BLOCK_BYTES[t]
+    assert L.smx_type_row_bytes(O.Q4_K, 2048) == 8 * 144
+    assert L.smx_type_row_bytes(O.Q4_0, 4096) == 128 * 18
+    assert L.smx_type_row_bytes(O.Q4_K, 100) == -1
+    assert L.smx_type_block_elems(3) == 0    # Q4_1: not implemented by the backend
+
+
+def test_rope_tables_host_entry_matches_oracle():
+    from smallmind_amd.quantization import rope_tables
+    c, s = rope_tables(128, 64, 10000.0)
+    oc, os_ = O.rope_tables(128, 64, 10000.0)
+    assert np.array_equal(c, oc) and np.array_equal(s, os_)
+
+
+def test_invalid_arguments_report_errors_without_a_device():
+    from smallmind_amd import _lib
+    L = _lib.load()
+    assert L.smx_rope_tables(4, 3, 10000.0, None, None) == -1
+    assert b"even" in L.smx_last_error()
+    w = ctypes.c_void_p()
+    assert L.smx_weight_create(3, 4, 32, ctypes.c_void_p(1), 0, ctypes.byref(w)) == -5
+    assert L.smx_quantize(O.Q4_K, None, 100, None, None) == -1
+
+
+def test_model_config_struct_layout():
+    from smallmind_amd._lib import ModelConfigC
+    assert ctypes.sizeof(ModelConfigC) == 4 * 16

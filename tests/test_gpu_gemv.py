@@ -1,0 +1,118 @@
+"""GPU parity of the fused dequant-GEMV (IWeightTensor.MatMul) against the oracle's float64
+GEMV on the same blocks.  Tolerance: max|y - y_ref| / max|y_ref| <= 1e-3 (the stated bar for
+the quantized GEMV), and the kernel is additionally held to 2e-5, which fp32 accumulation of
+K <= 11008 terms meets with margin."""
+import numpy as np
+import pytest
+
+import oracle as O
+from tests.helpers import TYPES, quantized, random_blocks, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+TIGHT = 2e-5
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _gemv(qt, blocks, N, K, x, m=1):
+    import torch
+
+    from smallmind_amd.quantization import GpuWeightTensor
+    w = GpuWeightTensor(qt, N, K, blocks)
+    xd = _dev(x.reshape(m, K))
+    out = torch.empty((m, N), dtype=torch.float32, device="cuda")
+    w.mat_mul(xd, out, m, K, N)
+    y = out.cpu().numpy()
+    w.close()
+    return y
+
+
+SHAPES = [(2, 256), (48, 512), (2560, 2048), (2048, 5632), (1000, 768), (3, 3072)]
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("N,K", SHAPES)
+def test_gemv_vs_oracle_realistic(gpu, name, N, K):
+    qt = TYPES[name]
+    if K % O.BLOCK_ELEMS[qt]:
+        pytest.skip("row length not a multiple of the block")
+    W = quantized(qt, (N, K), seed=N * 7 + K)
+    x = np.random.default_rng(K).normal(0, 1, K).astype(np.float32)
+    y = _gemv(qt, W, N, K, x)[0]
+    ref = O.gemv_f64(qt, W, N, K, x)
+    err = rel_err(y, ref)
+    assert err <= TOL and err <= TIGHT, err
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_gemv_vs_oracle_random_bytes(gpu, name):
+    qt = TYPES[name]
+    N, K = 130, 2048
+    W = random_blocks(qt, N * K // O.BLOCK_ELEMS[qt], 77)
+    x = np.random.default_rng(1).normal(0, 1, K).astype(np.float32)
+    y = _gemv(qt, W, N, K, x)[0]
+    ref = O.gemv_f64(qt, W, N, K, x)
+    # per-row relative error: random fp16 scales give rows of wildly different magnitude
+    Wf = O.dequant(qt, W, N * K).reshape(N, K).astype(np.float64)
+    scale = np.abs(Wf) @ np.abs(x.astype(np.float64))
+    assert np.all(np.abs(y - ref) <= TIGHT * scale + 1e-30)
+
+
+@pytest.mark.parametrize("N,K", [(4096, 4096), (11008, 4096), (4096, 11008)])
+def test_q4_0_gemv_benchmark_shapes(gpu, N, K):
+    """the three Q4_0 GEMV shapes, reference nibble semantics."""
+    W = quantized(O.Q4_0, (N, K), seed=N + K)
+    x = np.random.default_rng(3).normal(0, 1, K).astype(np.float32)
+    y = _gemv(O.Q4_0, W, N, K, x)[0]
+    err = rel_err(y, O.gemv_f64(O.Q4_0, W, N, K, x))
+    assert err <= TOL and err <= TIGHT, err
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_matmul_m_rows_equals_gemv_rows(gpu, name):
+    qt = TYPES[name]
+    N, K, m = 300, 512, 5
+    W = quantized(qt, (N, K), seed=5)
+    X = np.random.default_rng(6).normal(0, 1, (m, K)).astype(np.float32)
+    Y = _gemv(qt, W, N, K, X, m=m)
+    for r in range(m):
+        assert np.array_equal(Y[r], _gemv(qt, W, N, K, X[r])[0])
+        assert rel_err(Y[r], O.gemv_f64(qt, W, N, K, X[r])) <= TIGHT
+
+
+def test_fused_equals_dequant_then_matmul(gpu):
+    """The reference's live equivalence check (ExpandedQuantizationTests.cs:229-250): fused
+    quantized matmul == dequantize then fp32 matmul."""
+    import torch
+
+    from smallmind_amd.quantization import GpuWeightTensor
+    for qt in TYPES.values():
+        N, K = 256, 1024
+        W = quantized(qt, (N, K), seed=qt)
+        x = np.random.default_rng(qt).normal(0, 1, K).astype(np.float32)
+        w = GpuWeightTensor(qt, N, K, W)
+        Wf = w.to_float32().double()
+        ref = (Wf @ _dev(x).double()).cpu().numpy()
+        out = torch.empty((1, N), dtype=torch.float32, device="cuda")
+        w.mat_mul(_dev(x), out, 1, K, N)
+        assert rel_err(out.cpu().numpy()[0], ref) <= 1e-5
+        w.close()
+
+
+def test_matmul_dimension_mismatch_raises(gpu):
+    import torch
+
+    from smallmind_amd.quantization import GpuWeightTensor
+    w = GpuWeightTensor(O.Q8_0, 64, 256, quantized(O.Q8_0, (64, 256), 1))
+    x = torch.zeros(256, device="cuda")
+    y = torch.zeros(64, device="cuda")
+    with pytest.raises(ValueError):
+        w.mat_mul(x, y, 1, 128, 64)
+    with pytest.raises(ValueError):
+        w.mat_mul(x, y, 1, 256, 32)
+    w.close()

@@ -1,0 +1,153 @@
+"""End-to-end parity of the GPU decode path against the oracle's reference forward.
+
+Bar (stated by the north star): logits within 1e-3 relative error (max|dl| / max|l_ref| per
+step) and greedy tokens identical for the first 64 steps, on the same seeded weights and
+prompts."""
+import numpy as np
+import pytest
+
+import oracle as O
+from smallmind_amd.model import ModelConfig
+from tests.helpers import build_pair, rel_err
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-3
+
+SMALL = {
+    # llama-style, GQA 4:1, Q4_K layers, Q6_K embedding/head (the configs[2] formats)
+    "llama-q4k": (ModelConfig("llama", 1000, 160, 256, 3, 8, 2, 640), O.Q4_K, O.Q6_K, O.Q6_K),
+    # GPT-2 style, Q8_0 everywhere, tied head, learned positions (configs[0] formats)
+    "gpt2-q8_0": (ModelConfig("gpt2", 1000, 160, 256, 3, 4, 4, 1024), O.Q8_0, O.Q8_0, None),
+    # SmolLM-style MHA, Q5_K, tied embeddings (configs[4] formats)
+    "smollm-q5k": (ModelConfig("llama", 1000, 160, 256, 2, 4, 4, 512), O.Q5_K, O.Q5_K, None),
+    # Q8_0 layers + Q6_K head (configs[3] formats), and Q4_0 layers
+    "llama-q8_0": (ModelConfig("llama", 1000, 160, 256, 2, 8, 2, 512), O.Q8_0, O.Q6_K, O.Q6_K),
+    "llama-q4_0": (ModelConfig("llama", 1000, 160, 256, 2, 8, 2, 512), O.Q4_0, O.Q8_0, O.Q4_0),
+}
+
+
+@pytest.fixture(scope="module")
+def pairs(gpu):
+    out = {}
+    yield out
+    for om, gm in out.values():
+        gm.close()
+
+
+def _pair(pairs, key):
+    if key not in pairs:
+        cfg, lt, et, ht = SMALL[key]
+        om, gm, _ = build_pair(cfg, lt, et, ht, seed=sum(map(ord, key)))
+        pairs[key] = (om, gm)
+    return pairs[key]
+
+
+@pytest.mark.parametrize("key", list(SMALL))
+def test_greedy_64_tokens_and_logits(pairs, key):
+    om, gm = _pair(pairs, key)
+    cfg = SMALL[key][0]
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, 20).astype(np.int32)
+    sess = gm.create_session(96)
+    toks, stats, logits = sess.generate_greedy(prompt, 64, return_logits=True)
+    osess = om.session(96)
+    for p, t in enumerate(prompt[:-1]):
+        osess.step(int(t), p, want_logits=False)
+    tok = int(prompt[-1])
+    for i in range(64):
+        ref = osess.step(tok, len(prompt) - 1 + i)
+        err = rel_err(logits[i], ref)
+        assert err <= LOGIT_TOL, (i, err)
+        ref_tok = int(np.argmax(ref))
+        assert int(toks[i]) == ref_tok, (i, int(toks[i]), ref_tok)
+        tok = ref_tok
+    assert stats["decode_steps"] == 64 and stats["prefill_steps"] == 19
+    sess.close()
+
+
+@pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0"])
+def test_forward_api_matches_nocache_reference(pairs, key):
+    """GpuInferenceSession.forward mirrors TransformerModel.Forward(idx, positionOffset) with the
+    cache on; compared with the reference's no-cache full-context forward."""
+    om, gm = _pair(pairs, key)
+    cfg = SMALL[key][0]
+    toks = np.random.default_rng(2).integers(0, cfg.vocab_size, 30).astype(np.int32)
+    sess = gm.create_session(64)
+    full = om.forward_nocache(toks, all_rows=True)
+    got = sess.forward(toks[:17], 0)          # prefill
+    assert rel_err(got, full[16]) <= LOGIT_TOL
+    for p in range(17, 30):                    # decode one token at a time
+        got = sess.forward(toks[p:p + 1], p)
+        assert rel_err(got, full[p]) <= LOGIT_TOL
+    sess.reset_kv_cache()
+    got = sess.forward(toks[:5], 0)            # restart after ResetKVCache
+    assert rel_err(got, full[4]) <= LOGIT_TOL
+    sess.close()
+
+
+def test_decode_is_deterministic_and_cache_equals_recompute(pairs):
+    om, gm = _pair(pairs, "llama-q4k")
+    prompt = np.arange(12, dtype=np.int32) * 7
+    s = gm.create_session(64)
+    t1, _ = s.generate_greedy(prompt, 20)
+    t2, _ = s.generate_greedy(prompt, 20)
+    assert np.array_equal(t1, t2)
+    # KV-cached decode == full recompute of the whole sequence on the GPU
+    seq = np.concatenate([prompt, t1[:-1]])
+    last = s.forward(seq, 0)
+    s2 = gm.create_session(64)
+    _, _, lg = s2.generate_greedy(prompt, 20, return_logits=True)
+    assert rel_err(last, lg[-1]) < 1e-6
+    s.close()
+    s2.close()
+
+
+def test_errors_out_of_range_and_bad_tokens(pairs):
+    from smallmind_amd.quantization import SmxError
+    om, gm = _pair(pairs, "llama-q4k")
+    s = gm.create_session(16)
+    with pytest.raises(SmxError) as e:
+        s.forward(np.zeros(10, np.int32), 10)      # 10 + 10 > 16 (TransformerModel.cs:282-285)
+    assert e.value.code == -7
+    with pytest.raises(SmxError) as e:
+        s.forward(np.array([5, 1000], np.int32), 0)
+    assert e.value.code == -7
+    with pytest.raises(SmxError):
+        s.generate_greedy(np.zeros(10, np.int32), 10)
+    s.close()
+
+
+def test_full_size_llama_q4k_short_prompt():
+    """configs[2] at full size (22 layers, d=2048, GQA 32/4, ff=5632, V=32000, Q4_K + Q6_K),
+    weights drawn and encoded on the device, checked against the oracle on a short prompt."""
+    import torch
+
+    from smallmind_amd.model import GpuTransformerModel
+    from smallmind_amd.synthetic import WORKLOADS, load_synthetic_on_device
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    wl = WORKLOADS["llama-1.1b-q4_k"]
+    cfg = wl.config
+    gm = GpuTransformerModel(cfg)
+    kept = load_synthetic_on_device(gm, wl, seed=42, keep_blocks=True)
+    om = O.OracleModel(O.ARCH_LLAMA, cfg.vocab_size, cfg.context_length, cfg.embedding_length,
+                       cfg.block_count, cfg.head_count, cfg.head_count_kv, cfg.feed_forward_length,
+                       cfg.rope_freq_base, cfg.norm_eps)
+    for name, (qt, dims, data) in kept.items():
+        om.set_tensor(name, qt, data.cpu().numpy(), int(np.prod(dims)))
+    del kept
+    om.finalize()
+    prompt = np.random.default_rng(0).integers(0, cfg.vocab_size, 4).astype(np.int32)
+    s = gm.create_session(16)
+    toks, _, logits = s.generate_greedy(prompt, 3, return_logits=True)
+    os_ = om.session(16)
+    for p, t in enumerate(prompt[:-1]):
+        os_.step(int(t), p, want_logits=False)
+    tok = int(prompt[-1])
+    for i in range(3):
+        ref = os_.step(tok, len(prompt) - 1 + i)
+        assert rel_err(logits[i], ref) <= LOGIT_TOL
+        assert int(toks[i]) == int(np.argmax(ref))
+        tok = int(toks[i])
+    s.close()
+    gm.close()

@@ -1,0 +1,97 @@
+"""GPU parity of the elementwise / attention operators against the oracle."""
+import numpy as np
+import pytest
+
+import oracle as O
+from tests.helpers import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("n", [4, 768, 2048, 5000])
+def test_rmsnorm_layernorm(gpu, n):
+    from smallmind_amd.quantization import layernorm, rmsnorm
+    rng = np.random.default_rng(n)
+    x = rng.normal(0, 2, (3, n)).astype(np.float32)
+    g = rng.normal(1, 0.2, n).astype(np.float32)
+    b = rng.normal(0, 0.2, n).astype(np.float32)
+    assert rel_err(rmsnorm(_dev(x), _dev(g)).cpu().numpy(), O.rmsnorm(x, g)) < 2e-6
+    assert rel_err(layernorm(_dev(x), _dev(g), _dev(b)).cpu().numpy(), O.layernorm(x, g, b)) < 2e-6
+
+
+def test_rmsnorm_reference_values(gpu):
+    from smallmind_amd.quantization import rmsnorm
+    x = np.array([[0.5, 1.5, 2.5, 3.5]], np.float32)
+    g = np.array([1.2, 0.8, 1.5, 0.5], np.float32)
+    inv = 1.0 / np.sqrt((0.25 + 2.25 + 6.25 + 12.25) / 4 + 1e-5)
+    assert np.allclose(rmsnorm(_dev(x), _dev(g)).cpu().numpy(), g * x * inv, atol=1e-4)
+
+
+def test_rope_tables_equal_oracle_and_apply(gpu):
+    from smallmind_amd.quantization import rope_, rope_tables
+    c, s = rope_tables(300, 64, 10000.0)
+    oc, os_ = O.rope_tables(300, 64, 10000.0)
+    assert np.array_equal(c, oc) and np.array_equal(s, os_)
+    rng = np.random.default_rng(0)
+    x = rng.normal(0, 1, (4, 6, 64)).astype(np.float32)
+    got = rope_(_dev(x), 37, _dev(c), _dev(s)).cpu().numpy()
+    assert np.array_equal(got, O.rope_apply(x, 37, oc, os_))
+    got0 = rope_(_dev(x), 0, _dev(c), _dev(s)).cpu().numpy()
+    assert np.array_equal(got0[:, 0], x[:, 0])   # position 0 is the identity
+
+
+@pytest.mark.parametrize("seq,kseq,off", [(1, 1, 0), (1, 700, 699), (5, 9, 4), (3, 3000, 2997)])
+def test_scale_mask_softmax(gpu, seq, kseq, off):
+    from smallmind_amd.quantization import scale_mask_softmax_
+    s = np.random.default_rng(kseq).normal(0, 3, (seq, kseq)).astype(np.float32)
+    got = scale_mask_softmax_(_dev(s), 0.125, off).cpu().numpy()
+    ref = O.scale_mask_softmax(s, 0.125, off)
+    assert np.abs(got - ref).max() < 1e-6
+    for i in range(seq):
+        assert np.all(got[i, off + i + 1:] == 0)
+
+
+@pytest.mark.parametrize("H,Hkv,hd,npos", [(32, 4, 64, 1), (32, 4, 64, 513), (12, 12, 64, 160),
+                                           (32, 32, 64, 300), (8, 2, 128, 1000), (32, 4, 64, 4096)])
+def test_attention_decode_vs_oracle(gpu, H, Hkv, hd, npos):
+    from smallmind_amd.quantization import attention_decode
+    rng = np.random.default_rng(npos)
+    ctx = npos + 7
+    q = rng.normal(0, 1, (H, hd)).astype(np.float32)
+    kc = rng.normal(0, 1, (Hkv, ctx, hd)).astype(np.float32)
+    vc = rng.normal(0, 1, (Hkv, ctx, hd)).astype(np.float32)
+    got = attention_decode(_dev(q), _dev(kc), _dev(vc), H, Hkv, hd, ctx, npos).cpu().numpy()
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    ref = np.empty((H, hd), np.float32)
+    for h in range(H):
+        kv = h // (H // Hkv)
+        sc = (kc[kv, :npos].astype(np.float64) @ q[h].astype(np.float64)).astype(np.float32)[None]
+        p = O.scale_mask_softmax(sc, float(scale), cache_off=npos - 1)[0]
+        ref[h] = p.astype(np.float64) @ vc[kv, :npos].astype(np.float64)
+    assert rel_err(got.reshape(H, hd), ref) < 1e-5
+
+
+def test_silu_mul_gelu(gpu):
+    from smallmind_amd.quantization import gelu, silu_mul
+    rng = np.random.default_rng(1)
+    g = rng.normal(0, 4, 10001).astype(np.float32)
+    u = rng.normal(0, 1, 10001).astype(np.float32)
+    assert np.allclose(silu_mul(_dev(g), _dev(u)).cpu().numpy(), O.silu_mul(g, u), rtol=2e-6, atol=1e-7)
+    x = rng.normal(0, 3, 10001).astype(np.float32)
+    assert np.allclose(gelu(_dev(x)).cpu().numpy(), O.gelu(x), rtol=1e-6, atol=1e-7)
+
+
+def test_argmax_lowest_index_on_ties(gpu):
+    from smallmind_amd.quantization import argmax
+    rng = np.random.default_rng(2)
+    for n in (1, 63, 32000, 50257):
+        v = rng.normal(0, 1, n).astype(np.float32)
+        assert argmax(_dev(v)) == int(np.argmax(v))
+        if n > 10:
+            v[n // 3] = v[n - 2] = v.max() + 1
+            assert argmax(_dev(v)) == n // 3
