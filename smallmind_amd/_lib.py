@@ -62,6 +62,13 @@ def load() -> ctypes.CDLL:
         raise ImportError(
             f"{LIB_PATH} is missing: the HIP backend has not been built "
             "(run `python -c 'import __graft_entry__ as g; g.build()'`). There is no CPU fallback.")
+    # torch ships its own libamdhip64 / libhsa-runtime64 with the same SONAMEs as ROCm's.  Two
+    # HIP runtimes in one process do not share the device, so when torch is present it is
+    # loaded first and libsmx.so binds to the runtime already in the process.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = ctypes.CDLL(LIB_PATH)
     vp, i32, i64, f32, u64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_uint64
     pp = ctypes.POINTER(ctypes.c_void_p)

@@ -16,7 +16,7 @@ LOGIT_TOL = 1e-3
 
 SMALL = {
     # llama-style, GQA 4:1, Q4_K layers, Q6_K embedding/head (the configs[2] formats)
-    "llama-q4k": (ModelConfig("llama", 1000, 160, 256, 3, 8, 2, 640), O.Q4_K, O.Q6_K, O.Q6_K),
+    "llama-q4k": (ModelConfig("llama", 1000, 160, 256, 3, 8, 2, 768), O.Q4_K, O.Q6_K, O.Q6_K),
     # GPT-2 style, Q8_0 everywhere, tied head, learned positions (configs[0] formats)
     "gpt2-q8_0": (ModelConfig("gpt2", 1000, 160, 256, 3, 4, 4, 1024), O.Q8_0, O.Q8_0, None),
     # SmolLM-style MHA, Q5_K, tied embeddings (configs[4] formats)
