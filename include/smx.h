@@ -111,7 +111,8 @@ SMX_API int smx_rope(float *data_dev, int n_heads, int seq, int head_dim, int po
 SMX_API int smx_scale_mask_softmax(float *scores_dev, float scale, int seq, int k_seq,
                                    int cache_offset, void *stream);
 /* One decode position of MultiHeadAttention (MultiHeadAttention.cs:676-844): q [n_head][hd],
- * caches [n_kv_head][ctx_stride][hd] holding n_pos positions, out [n_head][hd]. */
+ * k_cache [n_kv_head][hd][ctx_stride] (dimension-major), v_cache [n_kv_head][ctx_stride][hd],
+ * each holding n_pos positions, out [n_head][hd]. */
 SMX_API int smx_attention_decode(const float *q_dev, const float *k_cache_dev,
                                  const float *v_cache_dev, float *out_dev, int n_head,
                                  int n_kv_head, int head_dim, int ctx_stride, int n_pos,

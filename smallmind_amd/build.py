@@ -16,7 +16,11 @@ OUT = os.path.join(HERE, "libsmx.so")
 BUILD = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["k_quant.hip", "k_gemv.hip", "k_ops.hip", "runtime.cpp"]
+# (source, object name, extra flags); the persistent decode kernel is built once per block
+# format so its instantiations compile in parallel.
+SOURCES = [("k_quant.hip", "k_quant", []), ("k_gemv.hip", "k_gemv", []), ("k_ops.hip", "k_ops", []),
+           ("runtime.cpp", "runtime", []), ("decode_dispatch.cpp", "decode_dispatch", [])] + [
+           ("k_decode.hip", f"k_decode_f{f}", [f"-DSMX_DECODE_FMT={f}"]) for f in range(5)]
 
 FLAGS = [
     "-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-fvisibility=hidden",
@@ -28,9 +32,10 @@ FLAGS = [
 ]
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(entry) -> str:
+    src, name, extra = entry
+    obj = os.path.join(BUILD, name + ".o")
+    cmd = [HIPCC, *FLAGS, *extra, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
@@ -39,7 +44,7 @@ def _compile(src: str) -> str:
 
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 8, 16)) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = OUT + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]

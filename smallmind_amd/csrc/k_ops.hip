@@ -1,6 +1,7 @@
 // k_ops.hip -- norms, RoPE, softmax, decode attention, activations, embedding, argmax.
 #include "smx_device.h"
 #include "smx_formats.h"
+#include "smx_attn.h"
 
 namespace smx {
 
@@ -88,67 +89,21 @@ __global__ __launch_bounds__(kThreads) void k_softmax(float *__restrict__ scores
     for (int j = threadIdx.x; j < k_seq; j += kThreads) row[j] = j < valid ? row[j] * inv : 0.0f;
 }
 
-// One decode position of MultiHeadAttention (MultiHeadAttention.cs:676-844) per query head:
-// raw scores q.k, scale, max, FastExp(s*scale - max), normalise by 1/sum, then P.V.  The
-// softmax is two-pass (global max first) because the Pade FastExp is not multiplicative, so
-// an online rescaling would not reproduce the reference.  Scores live in LDS.
+// One decode position of MultiHeadAttention for every query head (one workgroup per head).
+template <int HD>
 __global__ __launch_bounds__(kThreads) void k_attention_decode(
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
-    float *__restrict__ out, int n_head, int n_kv_head, int hd, int ctx_stride,
+    float *__restrict__ out, int n_head, int n_kv_head, int ctx_stride,
     const int32_t *__restrict__ pos_dev, int n_pos_fixed)
 {
     extern __shared__ float4 smem4[];
-    float *sc = (float *)smem4;              // [n_pos]
-    __shared__ float qs[256];
-    __shared__ float part[kWaves][256];
-    __shared__ float red[16];
+    __shared__ AttnSmem<HD, kThreads> sm;
     const int h = blockIdx.x;
     const int kvh = h / (n_head / n_kv_head);
     const int n_pos = pos_dev ? *pos_dev + 1 : n_pos_fixed;
-    const float scale = 1.0f / sqrtf((float)hd);   // MultiHeadAttention.cs:686
-    for (int e = threadIdx.x; e < hd; e += kThreads) qs[e] = q[(int64_t)h * hd + e];
-    __syncthreads();
-    const float *K = kc + (int64_t)kvh * ctx_stride * hd;
-    const float *V = vc + (int64_t)kvh * ctx_stride * hd;
-    float mx = -INFINITY;
-    for (int j = threadIdx.x; j < n_pos; j += kThreads) {
-        const float4 *kr = (const float4 *)(K + (int64_t)j * hd);
-        float s = 0.0f;
-        for (int e4 = 0; e4 < hd / 4; e4++) {
-            const float4 kv = kr[e4];
-            s = __builtin_fmaf(qs[4 * e4 + 0], kv.x, s);
-            s = __builtin_fmaf(qs[4 * e4 + 1], kv.y, s);
-            s = __builtin_fmaf(qs[4 * e4 + 2], kv.z, s);
-            s = __builtin_fmaf(qs[4 * e4 + 3], kv.w, s);
-        }
-        const float t = s * scale;
-        sc[j] = t;
-        mx = fmaxf(mx, t);
-    }
-    mx = block_max<kWaves>(mx, red);
-    float sum = 0.0f;
-    for (int j = threadIdx.x; j < n_pos; j += kThreads) {
-        const float e = fastexp(sc[j] - mx);
-        sc[j] = e;
-        sum += e;
-    }
-    sum = block_sum<kWaves>(sum, red);
-    const float inv = 1.0f / sum;
-    for (int j = threadIdx.x; j < n_pos; j += kThreads) sc[j] = sc[j] * inv;
-    __syncthreads();
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int e = lane; e < hd; e += 64) {
-        float acc = 0.0f;
-        for (int j = wave; j < n_pos; j += kWaves) acc = __builtin_fmaf(sc[j], V[(int64_t)j * hd + e], acc);
-        part[wave][e] = acc;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < hd; e += kThreads) {
-        float o = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; w++) o += part[w][e];
-        out[(int64_t)h * hd + e] = o;
-    }
+    const int64_t off = (int64_t)kvh * ctx_stride * HD;
+    attention_head<HD, kThreads>(q + (int64_t)h * HD, kc + off, vc + off, out + (int64_t)h * HD, n_pos,
+                                 ctx_stride, (float *)smem4, sm);
 }
 
 __global__ void k_silu_mul(const float *__restrict__ g, const float *__restrict__ u,
@@ -292,13 +247,24 @@ hipError_t launch_attention_decode(const float *q, const float *kc, const float 
                                    hipStream_t s)
 {
     const size_t lds = (size_t)max_pos * 4;
+    const void *fn = nullptr;
+    switch (hd) {
+    case 16: fn = (const void *)k_attention_decode<16>; break;
+    case 32: fn = (const void *)k_attention_decode<32>; break;
+    case 64: fn = (const void *)k_attention_decode<64>; break;
+    case 128: fn = (const void *)k_attention_decode<128>; break;
+    default: return hipErrorInvalidValue;
+    }
     if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_attention_decode,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(k_attention_decode, dim3(n_head), dim3(kThreads), lds, s, q, kc, vc, out,
-                       n_head, n_kv_head, hd, ctx_stride, pos_dev, n_pos_fixed);
+    switch (hd) {
+    case 16: hipLaunchKernelGGL(k_attention_decode<16>, dim3(n_head), dim3(kThreads), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
+    case 32: hipLaunchKernelGGL(k_attention_decode<32>, dim3(n_head), dim3(kThreads), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
+    case 64: hipLaunchKernelGGL(k_attention_decode<64>, dim3(n_head), dim3(kThreads), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
+    default: hipLaunchKernelGGL(k_attention_decode<128>, dim3(n_head), dim3(kThreads), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
+    }
     return hipGetLastError();
 }
 

@@ -188,6 +188,22 @@ struct smx_session {
     hipGraphExec_t g_prefill = nullptr, g_decode = nullptr;
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     std::atomic<int> busy{0};
+    // persistent decode (one cooperative launch per prefill / generation)
+    bool persistent = false;
+    int grid = 0, fmt = -1;
+    size_t lds = 0;
+    DecodeArgs dargs{};
+    LayerDesc *d_layers = nullptr;
+    unsigned *bar = nullptr;
+    int *abort_flag = nullptr;
+    float *wg_val = nullptr;
+    int32_t *wg_idx = nullptr;
+    float *logits_all = nullptr;
+    size_t logits_all_cap = 0;
+    // SMX_DECODE_TRACE=<file>: barrier timestamps of the last persistent launch are appended
+    unsigned long long *trace = nullptr;
+    int trace_cap = 0;
+    std::string trace_path;
 };
 
 namespace {
@@ -318,6 +334,137 @@ int capture_step(smx_session *S, bool with_head, hipGraphExec_t *out)
     e = hipGraphInstantiate(out, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
     SMX_HIP(e);
+    return SMX_OK;
+}
+
+// Prepares the persistent decode path (one cooperative kernel per generate call) when
+// SMX_DECODE=persistent is set, the device supports cooperative launches and every layer matrix
+// shares one block format; otherwise the session uses the per-kernel graph path, which is the
+// faster of the two on MI355X (a grid-wide barrier costs about as much as a kernel boundary).
+int setup_persistent(smx_session *S)
+{
+    smx_model *m = S->m;
+    const char *mode = getenv("SMX_DECODE");
+    if (!mode || strcmp(mode, "persistent")) return SMX_OK;
+    const int fmt = m->layers[0].qkv.fmt;
+    for (const Layer &L : m->layers)
+        if (L.qkv.fmt != fmt || L.o.fmt != fmt || L.gu.fmt != fmt || L.down.fmt != fmt) return SMX_OK;
+    const size_t lds = (size_t)S->max_ctx * 4;
+    const int grid = decode_grid(fmt, m->hd, lds, m->ctx->device);
+    if (grid <= 0) return SMX_OK;
+    const smx_model_config &c = m->cfg;
+    const size_t layer_cache = (size_t)c.n_kv_head * S->max_ctx * m->hd;
+    std::vector<LayerDesc> hl((size_t)c.n_layer);
+    for (int l = 0; l < c.n_layer; l++) {
+        const Layer &L = m->layers[l];
+        LayerDesc &D = hl[(size_t)l];
+        D.qkv = L.qkv.view();
+        D.o = L.o.view();
+        D.gu = L.gu.view();
+        D.down = L.down.view();
+        D.attn_g = L.d_attn_g;
+        D.attn_b = L.d_attn_b;
+        D.ffn_g = L.d_ffn_g;
+        D.ffn_b = L.d_ffn_b;
+        D.bqkv = L.d_bqkv;
+        D.bo = L.d_bo;
+        D.bgu = L.d_bgu;
+        D.bdown = L.d_bdown;
+        D.kc = S->kc + l * layer_cache;
+        D.vc = S->vc + l * layer_cache;
+    }
+    SMX_HIP(hipMalloc((void **)&S->d_layers, sizeof(LayerDesc) * hl.size()));
+    SMX_HIP(hipMemcpy(S->d_layers, hl.data(), sizeof(LayerDesc) * hl.size(), hipMemcpyHostToDevice));
+    SMX_HIP(hipMalloc((void **)&S->bar, 256));
+    SMX_HIP(hipMalloc((void **)&S->abort_flag, 256));
+    SMX_HIP(hipMalloc((void **)&S->wg_val, (size_t)grid * 4));
+    SMX_HIP(hipMalloc((void **)&S->wg_idx, (size_t)grid * 4));
+    DecodeArgs &a = S->dargs;
+    a.layers = S->d_layers;
+    a.n_layer = c.n_layer;
+    a.llama = m->llama ? 1 : 0;
+    a.d = c.d_model;
+    a.hd = m->hd;
+    a.n_head = c.n_head;
+    a.n_kv_head = c.n_kv_head;
+    a.kv_dim = m->kvdim;
+    a.nqkv = m->nqkv;
+    a.hidden = m->hidden;
+    a.vocab = c.vocab;
+    a.max_ctx = S->max_ctx;
+    a.eps = c.norm_eps;
+    a.tok = m->tok.view();
+    a.posw = m->llama ? WView{} : m->pos.view();
+    a.head = m->head.view();
+    a.out_g = m->d_out_g;
+    a.out_b = m->d_out_b;
+    a.rope_cos = m->rope_cos;
+    a.rope_sin = m->rope_sin;
+    a.x = S->x;
+    a.q = S->q;
+    a.att = S->att;
+    a.h = S->h;
+    a.logits = S->logits;
+    a.wg_val = S->wg_val;
+    a.wg_idx = S->wg_idx;
+    a.tokens = S->tokens;
+    a.pos = S->pos;
+    a.bar = S->bar;
+    a.abort_flag = S->abort_flag;
+    S->grid = grid;
+    S->fmt = fmt;
+    S->lds = lds;
+    S->persistent = true;
+    const char *tp = getenv("SMX_DECODE_TRACE");
+    if (tp && *tp) {
+        S->trace_cap = 4096;
+        S->trace_path = tp;
+        SMX_HIP(hipMalloc((void **)&S->trace, (size_t)S->trace_cap * grid * 2 * 8));
+    }
+    return SMX_OK;
+}
+
+// Enqueues one persistent launch running steps at positions pos0 .. pos0+n_steps-1; steps
+// s >= head_from compute logits and the greedy token.
+int run_persistent(smx_session *S, int pos0, int n_steps, int head_from, float *logits_all)
+{
+    hipStream_t s = S->m->ctx->stream;
+    SMX_HIP(hipMemsetAsync(S->bar, 0, 4, s));
+    SMX_HIP(hipMemsetAsync(S->abort_flag, 0, 4, s));
+    DecodeArgs a = S->dargs;
+    a.pos0 = pos0;
+    a.n_steps = n_steps;
+    a.head_from = head_from;
+    a.logits_all = logits_all;
+    if (S->trace) {
+        SMX_HIP(hipMemsetAsync(S->trace, 0, (size_t)S->trace_cap * S->grid * 2 * 8, s));
+        a.trace = S->trace;
+        a.trace_cap = S->trace_cap;
+    }
+    SMX_HIP(launch_decode(a, S->fmt, S->grid, S->lds, s));
+    return SMX_OK;
+}
+
+// After the stream has been synchronised: reports an aborted persistent launch and, when
+// tracing, appends the last launch's barrier stamps (header: grid, events; then
+// [events][grid][arrive, release] of the 100 MHz realtime counter).
+int check_abort(smx_session *S)
+{
+    if (!S->persistent) return SMX_OK;
+    int f = 0;
+    SMX_HIP(hipMemcpy(&f, S->abort_flag, 4, hipMemcpyDeviceToHost));
+    if (f) SMX_FAIL(SMX_EDEVICE, "persistent decode aborted: a device-wide barrier wait exceeded its limit");
+    if (S->trace) {
+        std::vector<unsigned long long> t((size_t)S->trace_cap * S->grid * 2);
+        SMX_HIP(hipMemcpy(t.data(), S->trace, t.size() * 8, hipMemcpyDeviceToHost));
+        FILE *fp = fopen(S->trace_path.c_str(), "ab");
+        if (fp) {
+            const long long hdr[2] = {S->grid, S->trace_cap};
+            fwrite(hdr, 8, 2, fp);
+            fwrite(t.data(), 8, t.size(), fp);
+            fclose(fp);
+        }
+    }
     return SMX_OK;
 }
 
@@ -505,8 +652,8 @@ SMX_API int smx_attention_decode(const float *q, const float *kc, const float *v
     if (!q || !kc || !vc || !out) SMX_FAIL(SMX_EINVAL, "smx_attention_decode: null pointer");
     if (n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head)
         SMX_FAIL(SMX_EINVAL, "smx_attention_decode: n_head must be a multiple of n_kv_head");
-    if (head_dim <= 0 || head_dim > 256 || head_dim % 4)
-        SMX_FAIL(SMX_EUNSUPPORTED, "smx_attention_decode: head_dim must be a multiple of 4 in [4, 256]");
+    if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128)
+        SMX_FAIL(SMX_EUNSUPPORTED, "smx_attention_decode: head_dim must be 16, 32, 64 or 128");
     if (n_pos <= 0 || n_pos > ctx_stride || ctx_stride > 40000)
         SMX_FAIL(SMX_EINVAL, "smx_attention_decode: need 1 <= n_pos <= ctx_stride <= 40000");
     SMX_HIP(launch_attention_decode(q, kc, vc, out, n_head, n_kv_head, head_dim, ctx_stride, nullptr,
@@ -576,7 +723,8 @@ SMX_API int smx_model_create(smx_context *ctx, const smx_model_config *cfg, smx_
     if (c.d_model % c.n_head) SMX_FAIL(SMX_EINVAL, "smx_model_create: d_model %% n_head != 0");
     if (c.n_head % c.n_kv_head) SMX_FAIL(SMX_EINVAL, "smx_model_create: n_head %% n_kv_head != 0");
     const int hd = c.d_model / c.n_head;
-    if (hd % 4 || hd > 256) SMX_FAIL(SMX_EUNSUPPORTED, "smx_model_create: head_dim %d", hd);
+    if (hd != 16 && hd != 32 && hd != 64 && hd != 128)
+        SMX_FAIL(SMX_EUNSUPPORTED, "smx_model_create: head_dim %d (supported: 16, 32, 64, 128)", hd);
     if (c.arch == SMX_ARCH_LLAMA && c.d_ff <= 0) SMX_FAIL(SMX_EINVAL, "smx_model_create: d_ff");
     for (int i = 0; i < 6; i++) if (c.reserved[i]) SMX_FAIL(SMX_EINVAL, "smx_model_create: reserved fields must be 0");
     smx_model *m = new smx_model();
@@ -805,8 +953,11 @@ SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out)
         smx_session_destroy(S);
         SMX_HIP(e);
     }
-    int rc = capture_step(S, false, &S->g_prefill);
-    if (rc == SMX_OK) rc = capture_step(S, true, &S->g_decode);
+    int rc = setup_persistent(S);
+    if (rc == SMX_OK && !S->persistent) {
+        rc = capture_step(S, false, &S->g_prefill);
+        if (rc == SMX_OK) rc = capture_step(S, true, &S->g_decode);
+    }
     if (rc != SMX_OK) {
         std::string msg = smx::last_error();
         smx_session_destroy(S);
@@ -839,12 +990,17 @@ SMX_API int smx_session_forward(smx_session *S, const int32_t *tokens, int n_tok
     const int32_t p0 = pos_offset;
     SMX_HIP(hipMemcpyAsync(S->tokens + pos_offset, tokens, (size_t)n_tokens * 4, hipMemcpyHostToDevice, s));
     SMX_HIP(hipMemcpyAsync(S->pos, &p0, 4, hipMemcpyHostToDevice, s));
-    for (int i = 0; i + 1 < n_tokens; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
-    SMX_HIP(hipGraphLaunch(S->g_decode, s));
+    if (S->persistent) {
+        rc = run_persistent(S, pos_offset, n_tokens, n_tokens - 1, nullptr);
+        if (rc != SMX_OK) return rc;
+    } else {
+        for (int i = 0; i + 1 < n_tokens; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
+        SMX_HIP(hipGraphLaunch(S->g_decode, s));
+    }
     if (logits_out)
         SMX_HIP(hipMemcpyAsync(logits_out, S->logits, (size_t)S->m->cfg.vocab * 4, hipMemcpyDeviceToHost, s));
     SMX_HIP(hipStreamSynchronize(s));
-    return SMX_OK;
+    return check_abort(S);
 }
 
 SMX_API int smx_session_generate(smx_session *S, const int32_t *prompt, int n_prompt, int n_new,
@@ -864,17 +1020,36 @@ SMX_API int smx_session_generate(smx_session *S, const int32_t *prompt, int n_pr
     const int32_t zero = 0;
     SMX_HIP(hipMemcpyAsync(S->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s));
     SMX_HIP(hipMemcpyAsync(S->pos, &zero, 4, hipMemcpyHostToDevice, s));
+    if (S->persistent && logits_out && S->logits_all_cap < (size_t)n_new * V) {
+        if (S->logits_all) (void)hipFree(S->logits_all);
+        S->logits_all = nullptr;
+        S->logits_all_cap = 0;
+        SMX_HIP(hipMalloc((void **)&S->logits_all, (size_t)n_new * V * 4));
+        S->logits_all_cap = (size_t)n_new * V;
+    }
     SMX_HIP(hipEventRecord(S->ev[0], s));
-    for (int i = 0; i + 1 < n_prompt; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
+    if (S->persistent) {
+        if (n_prompt > 1 && (rc = run_persistent(S, 0, n_prompt - 1, n_prompt - 1, nullptr)) != SMX_OK) return rc;
+    } else {
+        for (int i = 0; i + 1 < n_prompt; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
+    }
     SMX_HIP(hipEventRecord(S->ev[1], s));
-    for (int i = 0; i < n_new; i++) {
-        SMX_HIP(hipGraphLaunch(S->g_decode, s));
+    if (S->persistent) {
+        if ((rc = run_persistent(S, n_prompt - 1, n_new, 0, logits_out ? S->logits_all : nullptr)) != SMX_OK)
+            return rc;
         if (logits_out)
-            SMX_HIP(hipMemcpyAsync(logits_out + (size_t)i * V, S->logits, (size_t)V * 4, hipMemcpyDeviceToHost, s));
+            SMX_HIP(hipMemcpyAsync(logits_out, S->logits_all, (size_t)n_new * V * 4, hipMemcpyDeviceToHost, s));
+    } else {
+        for (int i = 0; i < n_new; i++) {
+            SMX_HIP(hipGraphLaunch(S->g_decode, s));
+            if (logits_out)
+                SMX_HIP(hipMemcpyAsync(logits_out + (size_t)i * V, S->logits, (size_t)V * 4, hipMemcpyDeviceToHost, s));
+        }
     }
     SMX_HIP(hipEventRecord(S->ev[2], s));
     SMX_HIP(hipMemcpyAsync(out_tokens, S->tokens + n_prompt, (size_t)n_new * 4, hipMemcpyDeviceToHost, s));
     SMX_HIP(hipStreamSynchronize(s));
+    if ((rc = check_abort(S)) != SMX_OK) return rc;
     if (stats) {
         float a = 0.0f, b = 0.0f;
         SMX_HIP(hipEventElapsedTime(&a, S->ev[0], S->ev[1]));
@@ -908,6 +1083,8 @@ SMX_API int smx_session_destroy(smx_session *S)
     for (hipEvent_t e : S->ev) if (e) (void)hipEventDestroy(e);
     free_dev(S->kc); free_dev(S->vc); free_dev(S->x); free_dev(S->q); free_dev(S->att);
     free_dev(S->h); free_dev(S->logits); free_dev(S->tokens); free_dev(S->pos); free_dev(S->amax);
+    free_dev(S->d_layers); free_dev(S->bar); free_dev(S->abort_flag); free_dev(S->wg_val);
+    free_dev(S->wg_idx); free_dev(S->logits_all); free_dev(S->trace);
     S->m->sessions.fetch_sub(1);
     delete S;
     return SMX_OK;

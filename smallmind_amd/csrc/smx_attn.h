@@ -1,0 +1,110 @@
+// smx_attn.h -- decode attention of one query head, executed by one whole workgroup.
+//
+// One decode position of MultiHeadAttention (MultiHeadAttention.cs:676-844): raw scores q.k,
+// scale, max, FastExp(s*scale - max) (MathUtils.cs:20-32), normalise by 1/sum
+// (OptimizedOps.cs:39-93), then P.V (:810-844).  The softmax is two-pass (global max first)
+// because the Pade FastExp is not multiplicative, so an online rescaling would not reproduce
+// the reference.
+//
+// Cache layouts: K is dimension-major [kv_head][HD][ctx_stride] so that lanes reading
+// consecutive positions issue coalesced loads; V is position-major [kv_head][ctx_stride][HD]
+// so that lanes reading consecutive dimensions of one position are coalesced.  Every load
+// batch is a fully unrolled set of independent loads, so a thread keeps many requests in
+// flight instead of one round trip per loop iteration.
+#pragma once
+
+#include "smx_device.h"
+
+namespace smx {
+
+template <int HD, int NT>
+struct AttnSmem {
+    static constexpr int D4 = HD / 4;
+    static constexpr int NPL = NT / D4;
+    float4 qs[D4];
+    float4 part[NPL][D4];
+    float red[16];
+};
+
+// sc: LDS scratch of at least n_pos floats.  All NT threads of the workgroup must call this.
+template <int HD, int NT>
+__device__ __forceinline__ void attention_head(const float *__restrict__ qh, const float *__restrict__ K,
+                                               const float *__restrict__ V, float *__restrict__ out,
+                                               int n_pos, int ctx_stride, float *sc,
+                                               AttnSmem<HD, NT> &sm)
+{
+    constexpr int D4 = HD / 4;
+    constexpr int NPL = NT / D4;
+    constexpr int NW = NT / 64;
+    constexpr int U = 8;
+    const float scale = 1.0f / sqrtf((float)HD);   // MultiHeadAttention.cs:686
+    const int tid = opaque_tid();
+    if (tid < D4) sm.qs[tid] = ((const float4 *)qh)[tid];
+    __syncthreads();
+
+    float mx = -INFINITY;
+    for (int j = tid; j < n_pos; j += NT) {
+        const float *kcol = K + j;
+        float kv[HD];
+#pragma unroll
+        for (int e = 0; e < HD; e++) kv[e] = kcol[(int64_t)e * ctx_stride];
+        float s = 0.0f;
+#pragma unroll
+        for (int e4 = 0; e4 < D4; e4++) {
+            const float4 qv = sm.qs[e4];
+            s = __builtin_fmaf(qv.x, kv[4 * e4 + 0], s);
+            s = __builtin_fmaf(qv.y, kv[4 * e4 + 1], s);
+            s = __builtin_fmaf(qv.z, kv[4 * e4 + 2], s);
+            s = __builtin_fmaf(qv.w, kv[4 * e4 + 3], s);
+        }
+        const float t = s * scale;
+        sc[j] = t;
+        mx = fmaxf(mx, t);
+    }
+    mx = block_max<NW>(mx, sm.red);
+    float sum = 0.0f;
+    for (int j = tid; j < n_pos; j += NT) {
+        const float e = fastexp(sc[j] - mx);
+        sc[j] = e;
+        sum += e;
+    }
+    sum = block_sum<NW>(sum, sm.red);
+    const float inv = 1.0f / sum;
+    for (int j = tid; j < n_pos; j += NT) sc[j] = sc[j] * inv;
+    __syncthreads();
+
+    // P.V: thread = (position lane pl, float4 column c4); U rows in flight per thread
+    const int c4 = tid % D4, pl = tid / D4;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j0 = pl; j0 < n_pos; j0 += NPL * U) {
+        float4 vv[U];
+        float pp[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int j = j0 + u * NPL;
+            const bool ok = j < n_pos;
+            vv[u] = ok ? ((const float4 *)(V + (int64_t)j * HD))[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            pp[u] = ok ? sc[j] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            acc.x = __builtin_fmaf(pp[u], vv[u].x, acc.x);
+            acc.y = __builtin_fmaf(pp[u], vv[u].y, acc.y);
+            acc.z = __builtin_fmaf(pp[u], vv[u].z, acc.z);
+            acc.w = __builtin_fmaf(pp[u], vv[u].w, acc.w);
+        }
+    }
+    sm.part[pl][c4] = acc;
+    __syncthreads();
+    if (tid < D4) {
+        float4 o = sm.part[0][tid];
+        for (int p = 1; p < NPL; p++) {
+            const float4 v = sm.part[p][tid];
+            o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+        }
+        ((float4 *)out)[tid] = o;
+    }
+    __syncthreads();   // sm and sc may be reused by the caller right away
+}
+
+}  // namespace smx

@@ -94,6 +94,21 @@ __device__ __forceinline__ float silu_mul(float x, float u)
     return silu * u;
 }
 
+// Thread index passed through an opaque instruction.  In the persistent decode kernel every
+// phase recomputes its lane-dependent addresses from this value where it uses them, instead
+// of the compiler hoisting all of them out of the step/layer loops and keeping them live for
+// the whole kernel (which spills registers).  Costs one v_mov per call site.
+__device__ __forceinline__ int opaque_tid()
+{
+    int t;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
+    return t;
+}
+__device__ __forceinline__ int lane_id() { return opaque_tid() & 63; }
+// Wave index within the workgroup as a scalar (wave-uniform) value, so task indices and row
+// addresses derived from it live in SGPRs.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 // ---- wave64 / block reductions ------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v)
 {

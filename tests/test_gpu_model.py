@@ -43,11 +43,15 @@ def _pair(pairs, key):
     return pairs[key]
 
 
+@pytest.mark.parametrize("mode", ["graph", "persistent"])
 @pytest.mark.parametrize("key", list(SMALL))
-def test_greedy_64_tokens_and_logits(pairs, key):
+def test_greedy_64_tokens_and_logits(pairs, key, mode, monkeypatch):
+    """Both decode paths: the captured per-kernel graph (default) and the single cooperative
+    kernel per generate call (SMX_DECODE=persistent)."""
     om, gm = _pair(pairs, key)
     cfg = SMALL[key][0]
     prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, 20).astype(np.int32)
+    monkeypatch.setenv("SMX_DECODE", mode)
     sess = gm.create_session(96)
     toks, stats, logits = sess.generate_greedy(prompt, 64, return_logits=True)
     osess = om.session(96)

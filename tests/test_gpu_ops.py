@@ -65,7 +65,8 @@ def test_attention_decode_vs_oracle(gpu, H, Hkv, hd, npos):
     q = rng.normal(0, 1, (H, hd)).astype(np.float32)
     kc = rng.normal(0, 1, (Hkv, ctx, hd)).astype(np.float32)
     vc = rng.normal(0, 1, (Hkv, ctx, hd)).astype(np.float32)
-    got = attention_decode(_dev(q), _dev(kc), _dev(vc), H, Hkv, hd, ctx, npos).cpu().numpy()
+    kt = np.ascontiguousarray(kc.transpose(0, 2, 1))   # the backend keeps K dimension-major
+    got = attention_decode(_dev(q), _dev(kt), _dev(vc), H, Hkv, hd, ctx, npos).cpu().numpy()
     scale = np.float32(1.0) / np.sqrt(np.float32(hd))
     ref = np.empty((H, hd), np.float32)
     for h in range(H):
