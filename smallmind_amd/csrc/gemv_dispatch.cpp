@@ -1,0 +1,30 @@
+// gemv_dispatch.cpp -- routes a fused GEMV to the instantiation compiled for its block format
+// (k_gemv.hip is built once per format) after checking the shape limits the kernels assume.
+#include "smx_internal.h"
+
+namespace smx {
+
+hipError_t launch_gemv_fmt0(const GemvArgs &a, int m, hipStream_t s);
+hipError_t launch_gemv_fmt1(const GemvArgs &a, int m, hipStream_t s);
+hipError_t launch_gemv_fmt2(const GemvArgs &a, int m, hipStream_t s);
+hipError_t launch_gemv_fmt3(const GemvArgs &a, int m, hipStream_t s);
+hipError_t launch_gemv_fmt4(const GemvArgs &a, int m, hipStream_t s);
+
+hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s)
+{
+    // Weight offsets are 32-bit inside the kernels; columns come in whole 32-element chunks.
+    if (a.w.rows <= 0 || a.w.cols <= 0 || a.w.cols % 32 != 0 || m <= 0 || m > 65535)
+        return hipErrorInvalidValue;
+    if ((uint64_t)a.w.rows * (uint64_t)a.w.nb * (uint64_t)fmt_main_bytes(a.w.fmt) >= (1ull << 32))
+        return hipErrorInvalidValue;
+    switch (a.w.fmt) {
+    case FMT_Q4_0: return launch_gemv_fmt0(a, m, s);
+    case FMT_Q8_0: return launch_gemv_fmt1(a, m, s);
+    case FMT_Q4_K: return launch_gemv_fmt2(a, m, s);
+    case FMT_Q5_K: return launch_gemv_fmt3(a, m, s);
+    case FMT_Q6_K: return launch_gemv_fmt4(a, m, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace smx

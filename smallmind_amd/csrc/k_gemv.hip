@@ -5,62 +5,442 @@
 // (NeuralNet.cs:145-298) and the fused C# kernels (MatMulF32Q8.cs, MatMulF32Q4.cs,
 // FusedQ4KMatMul.cs, FusedQ6KMatMul.cs), computing y = x W^T as the GGUF loader path does.
 //
-// Work decomposition: a wave64 owns R consecutive weight rows and is independent of every
-// other wave (no LDS, no workgroup barrier).  Lane l walks the 32-element chunks l, l+64, ...
-//   1. the weight loads of the wave's first chunk are issued before anything else, so HBM
-//      latency overlaps the activation prologue;
-//   2. the activation chunk is read from global memory (L1/L2 resident: every wave reads the
-//      same vector); a RMSNorm / LayerNorm prologue is computed by the wave itself with
-//      shuffles (deterministic, identical in every wave), so the norm never takes its own
-//      kernel or HBM round trip;
-//   3. codes are unpacked with and/shift into bytes and converted with v_cvt_f32_ubyte*, and
-//      block scales are factored out of the 32-term sums (sum (sc*q - m) x =
-//      sc * sum q x - m * sum x);
-//   4. the R partial sums are reduce-scattered across the wave and one lane applies the
-//      epilogue (bias, residual, SwiGLU, GELU, or RoPE + KV-cache append).
+// Work decomposition.  A workgroup is 4 wave64s.  A "row group" of R consecutive rows is owned
+// by S waves (S = 1, 2 or 4) that split the 32-element chunks of K between them; lane l of wave
+// ws takes chunks (ws + S*j)*64 + l for j < C, so one pass ("round") covers 64*S*C chunks and
+// every lane holds at most C chunks of x and C*R chunks of weights in registers.
+//
+// Latency is the budget at decode sizes (a 3 MB matrix is 0.4 us of HBM time), so each wave
+// issues all of its loads before it consumes any of them, in the order in which it needs them:
+//   1. the activation vector (+ gamma / beta of a fused RMSNorm / LayerNorm), loaded by the
+//      whole workgroup with coalesced 16-byte loads (L2-resident);
+//   2. the weight chunks of all R rows (HBM);
+//   3. the epilogue operands (bias, residual, RoPE table entries, KV position) as scalar loads.
+// Vector-memory loads complete in issue order, so (1) is consumed while (2) is in flight: the
+// norm statistic is reduced across the workgroup (DPP within waves, LDS across them), the
+// normalised vector is staged in LDS with a bank-conflict-free swizzle, and each lane reads
+// its 32-element chunks from there -- one copy of the activations per workgroup instead of
+// one strided copy per wave.
+// Codes are unpacked with and/shift into bytes and converted with v_cvt_f32_ubyte*; block
+// scales are factored out of each 32-term sum (sum (sc*q - m) x = sc * sum q x - m * sum x).
+// The R per-lane partials are summed across the wave with DPP, combined across the S waves in
+// LDS in a fixed order, and one lane applies the epilogue.
+//
+// Compiled once per block format (SMX_GEMV_FMT) so the instantiations build in parallel.
 #include "smx_device.h"
 #include "smx_formats.h"
 #include "smx_gemv.h"
+
+#ifndef SMX_GEMV_FMT
+#error "compile with -DSMX_GEMV_FMT=<Fmt>"
+#endif
 
 namespace smx {
 
 namespace {
 
-template <int F, int R>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
+// Epilogue classes: EC_SIMPLE covers EPI_STORE / EPI_RESID / EPI_GELU (selected at run time).
+enum { EC_SIMPLE = 0, EC_SILU = 1, EC_QKV = 2, EC_ARGMAX = 3 };
+
+// Epilogue operands of one row group, loaded before the dot products (wave-uniform values).
+template <int R, int EC>
+struct EpiIn {
+    float bias[R];
+    float res[R];
+    float cs[R / 2], sn[R / 2];
+    int pos;
+};
+
+template <int R, int EC>
+__device__ __forceinline__ void epi_load(const GemvArgs &a, uint32_t row0, uint32_t N, int my,
+                                         EpiIn<R, EC> &e)
 {
-    const int64_t wave = ((int64_t)blockIdx.x * (blockDim.x >> 6)) + wave_id();
-    gemv_wave<F, R>(a, wave * R, blockIdx.y);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t row = row0 + r < N ? row0 + r : N - 1;
+        e.bias[r] = a.bias ? ld_uniform(a.bias + row) : 0.0f;
+        e.res[r] = 0.0f;
+        if constexpr (EC == EC_SIMPLE)
+            if (a.epi == EPI_RESID) e.res[r] = ld_uniform(a.resid + (int64_t)my * a.out_stride + row);
+    }
+    e.pos = 0;
+    if constexpr (EC == EC_QKV) {
+        e.pos = a.pos ? ld_uniform(a.pos) : a.pos_val;
+        const int half = a.head_dim / 2, d = a.d_model, kv = a.kv_dim;
+#pragma unroll
+        for (int p = 0; p < R / 2; p++) {
+            const int row = (int)row0 + 2 * p;
+            int pair = -1;
+            if (a.use_rope && row < d) pair = (row % a.head_dim) / 2;
+            else if (a.use_rope && row < d + kv) pair = ((row - d) % a.head_dim) / 2;
+            e.cs[p] = pair >= 0 ? ld_uniform(a.rope_cos + (int64_t)e.pos * half + pair) : 1.0f;
+            e.sn[p] = pair >= 0 ? ld_uniform(a.rope_sin + (int64_t)e.pos * half + pair) : 0.0f;
+        }
+    }
 }
 
-template <int F, int R>
-hipError_t launch_fr(const GemvArgs &a, int m, hipStream_t s)
+template <int R, int EC>
+__device__ __forceinline__ void epi_store(const GemvArgs &a, const float *t, const EpiIn<R, EC> &e,
+                                          uint32_t row0, uint32_t N, int my)
 {
-    const int64_t waves = (a.w.rows + R - 1) / R;
-    const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)m);
-    hipLaunchKernelGGL((k_gemv<F, R>), grid, dim3(256), 0, s, a);
+    float *out = a.out + (int64_t)my * a.out_stride;
+    float v[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) v[r] = a.bias ? t[r] + e.bias[r] : t[r];
+    if constexpr (EC == EC_ARGMAX) {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (row0 + r < N) out[row0 + r] = v[r];
+    } else if constexpr (EC == EC_SIMPLE) {
+        const int epi = a.epi;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if (row0 + r >= N) break;
+            float y = v[r];
+            if (epi == EPI_RESID) y = e.res[r] + v[r];
+            else if (epi == EPI_GELU) y = gelu_pade(v[r]);
+            out[row0 + r] = y;
+        }
+    } else if constexpr (EC == EC_SILU) {
+        // rows interleave gate / up: out[i] = silu(gate_i) * up_i
+#pragma unroll
+        for (int r = 0; r < R; r += 2)
+            if (row0 + r + 1 < N) out[(row0 + r) / 2] = silu_mul(v[r], v[r + 1]);
+    } else {
+        // rows [Q | K | V]: RoPE on Q and K pairs (RotaryEmbedding.cs:115-116); Q -> out,
+        // K -> k_cache [kv_head][head_dim][ctx_stride] (dimension-major), V -> v_cache
+        // [kv_head][ctx_stride][head_dim].
+        const int d = a.d_model, kv = a.kv_dim, hd = a.head_dim, pos = e.pos;
+#pragma unroll
+        for (int p = 0; p < R / 2; p++) {
+            const int row = (int)row0 + 2 * p;
+            if (row + 1 >= (int)N) break;
+            float v0 = v[2 * p], v1 = v[2 * p + 1];
+            if (a.use_rope && row < d + kv) {
+                const float c = e.cs[p], s = e.sn[p];
+                const float t0 = v0 * c, t1 = v1 * s, t2 = v0 * s, t3 = v1 * c;
+                v0 = t0 - t1;
+                v1 = t2 + t3;
+            }
+            if (row < d) {
+                out[row] = v0;
+                out[row + 1] = v1;
+            } else if (row < d + kv) {
+                float *dst = a.k_cache + (int64_t)(row - d) * a.ctx_stride + pos;
+                dst[0] = v0;
+                dst[a.ctx_stride] = v1;
+            } else {
+                const int vr = row - d - kv;
+                float *dst = a.v_cache + ((int64_t)(vr / hd) * a.ctx_stride + pos) * hd + (vr % hd);
+                dst[0] = v0;
+                dst[1] = v1;
+            }
+        }
+    }
+}
+
+// Wave-uniform totals of R per-lane partials (DPP row sums + lane reads, no LDS).
+template <int R>
+__device__ __forceinline__ void wave_totals(const float *acc, float *t)
+{
+#pragma unroll
+    for (int r = 0; r < R; r++) t[r] = wave_sum_uniform(acc[r]);
+}
+
+// (v, i) beats (bv, bi): larger value, or equal value and lower index (NaN never wins).
+__device__ __forceinline__ bool am_better(float v, int i, float bv, int bi)
+{
+    return v > bv || (v == bv && i < bi);
+}
+
+// Workgroup-wide sum (4 waves), the same bits in every thread.
+__device__ __forceinline__ float wg_sum(float v, float *slot, int w)
+{
+    v = wave_sum_uniform(v);
+    if (lane_id() == 0) slot[w] = v;
+    __syncthreads();
+    return (slot[0] + slot[1]) + (slot[2] + slot[3]);
+}
+
+// Position of float4 i4 of the activation vector in the staged LDS copy: float4 i of chunk c
+// sits at 8c + (i ^ (c & 7)), so the eight 16-byte reads of a lane's 128-byte chunk fall on
+// distinct banks across consecutive lanes.
+__device__ __forceinline__ int xs_pos(int c, int i) { return 8 * c + (i ^ (c & 7)); }
+
+// STG = 1 (K <= 8192) / 2 (K <= 16384, no norm): the workgroup loads the activation vector
+// with coalesced loads (thread t: float4 t, t+256, ...), applies the fused norm and stages it
+// in LDS; lanes then read their chunks from LDS.  STG = 0 (no norm, K > 16384): lanes read
+// their chunks from global memory.
+template <int F, int R, int S, int C, int PRO, int EC, int STG>
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
+{
+    static_assert(STG || PRO == PRO_NONE, "a fused norm needs the staged activation path");
+    constexpr int G = 4 / S;    // row groups per workgroup
+    constexpr int KPT = STG == 2 ? 16 : 8;   // staged float4 per thread: K <= 1024*KPT
+    static_assert(STG < 2 || PRO == PRO_NONE, "the wide staging is for plain GEMVs");
+    __shared__ float s_red[4][R];
+    __shared__ float s_st[2][4];
+    extern __shared__ float4 xs[];
+    const int w = wave_id();
+    const int grp = w / S, ws = w % S;
+    const int lane = lane_id();
+    const uint32_t N = (uint32_t)a.w.rows;
+    const int K = (int)a.w.cols, nch = K >> 5, K4 = K >> 2;
+    const uint32_t row0 = (blockIdx.x * G + grp) * R;
+    const int my = blockIdx.y;
+    const float *x = a.x + (int64_t)my * a.x_stride;
+    uint32_t rb[R];   // row * blocks-per-row (rows past the end re-read the last row)
+#pragma unroll
+    for (int r = 0; r < R; r++) rb[r] = (row0 + r < N ? row0 + r : N - 1) * (uint32_t)a.w.nb;
+
+    // 1. activations (+ norm parameters): coalesced, issued first
+    const int tid = STG ? opaque_tid() : 0;
+    float4 xr[STG ? KPT : 1], gr[PRO != PRO_NONE ? KPT : 1], br[PRO == PRO_LN ? KPT : 1];
+    if constexpr (STG) {
+#pragma unroll
+        for (int k = 0; k < KPT; k++) {
+            const int i4 = tid + 256 * k;
+            if (i4 < K4) {
+                xr[k] = ((const float4 *)x)[i4];
+                if constexpr (PRO != PRO_NONE) gr[k] = ((const float4 *)a.gamma)[i4];
+                if constexpr (PRO == PRO_LN) br[k] = ((const float4 *)a.beta)[i4];
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. weights of the first round
+    int cj[C];
+    bool on[C];
+    Raw<F> wr[C][R];
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+        const int c = (ws + S * j) * 64 + lane;
+        on[j] = c < nch;
+        cj[j] = on[j] ? c : nch - 1;
+#pragma unroll
+        for (int r = 0; r < R; r++) wr[j][r].load32(a.w, rb[r], cj[j]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. epilogue operands
+    EpiIn<R, EC> e;
+    epi_load<R, EC>(a, row0, N, my, e);
+    __builtin_amdgcn_sched_barrier(0);
+    // 4. norm statistic over the workgroup, normalise, stage in LDS
+    if constexpr (STG) {
+        float sc = 1.0f, mean = 0.0f;
+        if constexpr (PRO == PRO_RMS) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KPT; k++)
+                if (tid + 256 * k < K4) {
+                    float q;
+                    q = xr[k].x * xr[k].x; ss += q;
+                    q = xr[k].y * xr[k].y; ss += q;
+                    q = xr[k].z * xr[k].z; ss += q;
+                    q = xr[k].w * xr[k].w; ss += q;
+                }
+            ss = wg_sum(ss, s_st[0], w);
+            sc = 1.0f / sqrtf(ss / (float)K + a.eps);   // RMSNormOps.cs:114
+        } else if constexpr (PRO == PRO_LN) {
+            float t = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KPT; k++)
+                if (tid + 256 * k < K4) { t += xr[k].x; t += xr[k].y; t += xr[k].z; t += xr[k].w; }
+            mean = wg_sum(t, s_st[0], w) / (float)K;     // LayerNormOps.cs:92-101
+            float sq = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KPT; k++)
+                if (tid + 256 * k < K4) {
+                    float dd, q;
+                    dd = xr[k].x - mean; q = dd * dd; sq += q;
+                    dd = xr[k].y - mean; q = dd * dd; sq += q;
+                    dd = xr[k].z - mean; q = dd * dd; sq += q;
+                    dd = xr[k].w - mean; q = dd * dd; sq += q;
+                }
+            sq = wg_sum(sq, s_st[1], w);
+            sc = 1.0f / sqrtf(sq / (float)K + a.eps);     // LayerNormOps.cs:103-119
+        }
+#pragma unroll
+        for (int k = 0; k < KPT; k++) {
+            const int i4 = tid + 256 * k;
+            if (i4 < K4) {
+                float4 v = xr[k];
+                if constexpr (PRO == PRO_RMS) {   // RMSNormOps.cs:137-139: gamma * (x * invRms)
+                    const float4 g = gr[k];
+                    v.x = g.x * (v.x * sc); v.y = g.y * (v.y * sc);
+                    v.z = g.z * (v.z * sc); v.w = g.w * (v.w * sc);
+                } else if constexpr (PRO == PRO_LN) {   // LayerNormOps.cs:185
+                    const float4 g = gr[k], b = br[k];
+                    v.x = __builtin_fmaf(g.x, (v.x - mean) * sc, b.x);
+                    v.y = __builtin_fmaf(g.y, (v.y - mean) * sc, b.y);
+                    v.z = __builtin_fmaf(g.z, (v.z - mean) * sc, b.z);
+                    v.w = __builtin_fmaf(g.w, (v.w - mean) * sc, b.w);
+                }
+                xs[xs_pos(i4 >> 3, i4 & 7)] = v;
+            }
+        }
+        __syncthreads();
+    }
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    // 5. activation chunks (LDS or global) and dot products.  A staged launch covers K in one
+    // round; only the unstaged fallback (K > 16384) loops, which keeps the loop's register
+    // cost out of the common instances.
+    auto round = [&]() {
+#pragma unroll
+        for (int j = 0; j < C; j++) {
+            float4 xv[8];
+            if constexpr (STG) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) xv[i] = xs[xs_pos(cj[j], i)];
+            } else {
+                const float4 *xp = (const float4 *)(x + 32 * cj[j]);
+#pragma unroll
+                for (int i = 0; i < 8; i++) xv[i] = xp[i];
+            }
+            float xa = 0.0f, xb = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                xa += (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
+                xb += (xv[i + 4].x + xv[i + 4].y) + (xv[i + 4].z + xv[i + 4].w);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const float p = wr[j][r].dot(xv, xa, xb, cj[j]);
+                acc[r] += on[j] ? p : 0.0f;
+            }
+        }
+    };
+    round();
+    if constexpr (!STG) {
+        for (int base = 64 * S * C; base < nch; base += 64 * S * C) {
+#pragma unroll
+            for (int j = 0; j < C; j++) {
+                const int c = base + (ws + S * j) * 64 + lane;
+                on[j] = c < nch;
+                cj[j] = on[j] ? c : nch - 1;
+#pragma unroll
+                for (int r = 0; r < R; r++) wr[j][r].load32(a.w, rb[r], cj[j]);
+            }
+            round();
+        }
+    }
+
+    // 6. reduction across the wave, then across the S waves of the row group
+    float t[R];
+    wave_totals<R>(acc, t);
+    if constexpr (S > 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; r++) s_red[w][r] = t[r];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float v = s_red[grp * S][r];
+#pragma unroll
+            for (int s = 1; s < S; s++) v += s_red[grp * S + s][r];
+            t[r] = v;
+        }
+    }
+    if (ws == 0 && lane == 0 && row0 < N) epi_store<R, EC>(a, t, e, row0, N, my);
+    if constexpr (EC == EC_ARGMAX) {
+        __shared__ float s_bv[4];
+        __shared__ int s_bi[4];
+        if (ws == 0 && lane == 0) {
+            float bv = -INFINITY;
+            int bi = 0x7FFFFFFF;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const float v = a.bias ? t[r] + e.bias[r] : t[r];
+                if (row0 + r < N && am_better(v, (int)(row0 + r), bv, bi)) { bv = v; bi = (int)(row0 + r); }
+            }
+            s_bv[grp] = bv;
+            s_bi[grp] = bi;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float bv = s_bv[0];
+            int bi = s_bi[0];
+#pragma unroll
+            for (int g = 1; g < G; g++)
+                if (am_better(s_bv[g], s_bi[g], bv, bi)) { bv = s_bv[g]; bi = s_bi[g]; }
+            a.wg_val[blockIdx.x] = bv;
+            a.wg_idx[blockIdx.x] = bi;
+        }
+    }
+}
+
+template <int R, int S, int C, int PRO, int EC, int STG>
+hipError_t launch_v(const GemvArgs &a, int m, hipStream_t s)
+{
+    constexpr int F = SMX_GEMV_FMT;
+    const int64_t groups = (a.w.rows + R - 1) / R;
+    const dim3 grid((unsigned)((groups + (4 / S) - 1) / (4 / S)), (unsigned)m);
+    const size_t lds = STG ? (size_t)a.w.cols * 4 : 0;
+    hipLaunchKernelGGL((k_gemv<F, R, S, C, PRO, EC, STG>), grid, dim3(256), lds, s, a);
+    if constexpr (EC == EC_ARGMAX) {
+        // the per-workgroup partials are reduced by a one-workgroup kernel; the kernel boundary
+        // makes them visible without a device-scope fence in each of the many workgroups
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_argmax_pairs(a.wg_val, a.wg_idx, (int)grid.x, a.amax_out, a.tokens, a.tok_pos, s);
+    }
     return hipGetLastError();
 }
 
-template <int F>
-hipError_t launch_f(const GemvArgs &a, int m, hipStream_t s)
+// Shape selection: S waves split K so that one round covers it (up to 4 waves x 64 lanes x C
+// chunks); R = 4 rows per wave for tall matrices with short rows, else 2.  The activation
+// vector is staged in LDS (up to 8192 floats with a fused norm, 16384 without).
+template <int PRO, int EC>
+hipError_t launch_pe(const GemvArgs &a, int m, hipStream_t s)
 {
-    // Pairs of rows must share a wave for the SwiGLU and RoPE epilogues, so R >= 2.
-    if (a.w.rows >= 8192) return launch_fr<F, 4>(a, m, s);
-    return launch_fr<F, 2>(a, m, s);
+    const int64_t K = a.w.cols, nch = K / 32;
+    if (K > 8192) {
+        if constexpr (PRO == PRO_NONE && EC == EC_SIMPLE) {
+            if (K <= 16384) return launch_v<2, 4, 2, PRO, EC, 2>(a, m, s);
+            return launch_v<2, 4, 2, PRO, EC, 0>(a, m, s);
+        }
+        return hipErrorInvalidValue;
+    }
+    if (nch <= 64) {
+        if (a.w.rows >= 8192) return launch_v<4, 1, 1, PRO, EC, 1>(a, m, s);
+        return launch_v<2, 1, 1, PRO, EC, 1>(a, m, s);
+    }
+    if (nch <= 128) return launch_v<2, 2, 1, PRO, EC, 1>(a, m, s);
+    return launch_v<2, 4, 1, PRO, EC, 1>(a, m, s);   // nch <= 256
 }
 
 }  // namespace
 
-hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s)
+#define SMX_CAT2(a, b) a##b
+#define SMX_CAT(a, b) SMX_CAT2(a, b)
+
+hipError_t SMX_CAT(launch_gemv_fmt, SMX_GEMV_FMT)(const GemvArgs &a, int m, hipStream_t s)
 {
-    switch (a.w.fmt) {
-    case FMT_Q4_0: return launch_f<FMT_Q4_0>(a, m, s);
-    case FMT_Q8_0: return launch_f<FMT_Q8_0>(a, m, s);
-    case FMT_Q4_K: return launch_f<FMT_Q4_K>(a, m, s);
-    case FMT_Q5_K: return launch_f<FMT_Q5_K>(a, m, s);
-    case FMT_Q6_K: return launch_f<FMT_Q6_K>(a, m, s);
-    default: return hipErrorInvalidValue;
+    switch (a.epi) {
+    case EPI_STORE:
+    case EPI_RESID:
+    case EPI_GELU:
+        if (a.pro == PRO_NONE) return launch_pe<PRO_NONE, EC_SIMPLE>(a, m, s);
+        if (a.pro == PRO_RMS) return launch_pe<PRO_RMS, EC_SIMPLE>(a, m, s);
+        return launch_pe<PRO_LN, EC_SIMPLE>(a, m, s);
+    case EPI_SILU:
+        if (a.pro == PRO_RMS) return launch_pe<PRO_RMS, EC_SILU>(a, m, s);
+        return hipErrorInvalidValue;
+    case EPI_QKV:
+        if (a.pro == PRO_RMS) return launch_pe<PRO_RMS, EC_QKV>(a, m, s);
+        if (a.pro == PRO_LN) return launch_pe<PRO_LN, EC_QKV>(a, m, s);
+        return hipErrorInvalidValue;
+    case EPI_ARGMAX:
+        if (m != 1 || !a.wg_val || !a.wg_idx) return hipErrorInvalidValue;
+        if (a.pro == PRO_RMS) return launch_pe<PRO_RMS, EC_ARGMAX>(a, m, s);
+        if (a.pro == PRO_LN) return launch_pe<PRO_LN, EC_ARGMAX>(a, m, s);
+        return hipErrorInvalidValue;
+    default:
+        return hipErrorInvalidValue;
     }
 }
 

@@ -90,20 +90,35 @@ __global__ __launch_bounds__(kThreads) void k_softmax(float *__restrict__ scores
 }
 
 // One decode position of MultiHeadAttention for every query head (one workgroup per head).
+// The softmax needs the exact maximum over all positions before any exponential (the Pade
+// FastExp is not multiplicative), so a head is not split across workgroups; instead the
+// workgroup is wide (512 threads) and, for head_dim 64, the score pass (one position per
+// thread) and the P.V pass (16 positions per thread) each cover 512 positions per round of
+// loads.
+template <int HD> struct AttnCfg {
+    static constexpr int NT = 512;
+    static constexpr int U = HD <= 64 ? 16 : 8;
+};
+
 template <int HD>
-__global__ __launch_bounds__(kThreads) void k_attention_decode(
+__global__ __launch_bounds__(AttnCfg<HD>::NT) void k_attention_decode(
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
     float *__restrict__ out, int n_head, int n_kv_head, int ctx_stride,
     const int32_t *__restrict__ pos_dev, int n_pos_fixed)
 {
+    constexpr int NT = AttnCfg<HD>::NT;
     extern __shared__ float4 smem4[];
-    __shared__ AttnSmem<HD, kThreads> sm;
-    const int h = blockIdx.x;
+    __shared__ AttnSmem<HD, NT> sm;
+    // Workgroups are dealt to the 8 XCDs round-robin (workgroup b -> XCD b % 8); ordering the
+    // heads so that XCD x gets heads x*H/8 .. x*H/8 + H/8 - 1 keeps the query heads of one KV
+    // head on one XCD, whose L2 then serves their shared K/V rows.
+    const int b = blockIdx.x;
+    const int h = (n_head % 8 == 0) ? (b % 8) * (n_head / 8) + b / 8 : b;
     const int kvh = h / (n_head / n_kv_head);
-    const int n_pos = pos_dev ? *pos_dev + 1 : n_pos_fixed;
+    const int n_pos = pos_dev ? ld_uniform(pos_dev) + 1 : n_pos_fixed;
     const int64_t off = (int64_t)kvh * ctx_stride * HD;
-    attention_head<HD, kThreads>(q + (int64_t)h * HD, kc + off, vc + off, out + (int64_t)h * HD, n_pos,
-                                 ctx_stride, (float *)smem4, sm);
+    attention_head<HD, NT, AttnCfg<HD>::U>(q + (int64_t)h * HD, kc + off, vc + off, out + (int64_t)h * HD,
+                                           n_pos, ctx_stride, (float *)smem4, sm);
 }
 
 __global__ void k_silu_mul(const float *__restrict__ g, const float *__restrict__ u,
@@ -154,6 +169,47 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ x, in
         if (tokens && pos) {
             const int p = *pos;
             tokens[p + 1] = idx;
+            *pos = p + 1;
+        }
+    }
+}
+
+// Argmax over (value, index) pairs (per-workgroup partials of the head GEMV), lowest index on
+// ties; same outputs as k_argmax.
+__global__ __launch_bounds__(256) void k_argmax_pairs(const float *__restrict__ val,
+                                                      const int32_t *__restrict__ idx, int n,
+                                                      int32_t *__restrict__ out,
+                                                      int32_t *__restrict__ tokens,
+                                                      int32_t *__restrict__ pos)
+{
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    float best = -INFINITY;
+    int bidx = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = val[i];
+        const int ix = idx[i];
+        if (v > best || (v == best && ix < bidx)) { best = v; bidx = ix; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bidx, o, 64);
+        if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { bv[w] = best; bi[w] = bidx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        best = bv[0];
+        bidx = bi[0];
+        for (int k = 1; k < 4; k++)
+            if (bv[k] > best || (bv[k] == best && bi[k] < bidx)) { best = bv[k]; bidx = bi[k]; }
+        if (bidx == 0x7FFFFFFF) bidx = 0;
+        if (out) *out = bidx;
+        if (tokens && pos) {
+            const int p = *pos;
+            tokens[p + 1] = bidx;
             *pos = p + 1;
         }
     }
@@ -260,10 +316,10 @@ hipError_t launch_attention_decode(const float *q, const float *kc, const float 
         if (e != hipSuccess) return e;
     }
     switch (hd) {
-    case 16: hipLaunchKernelGGL(k_attention_decode<16>, dim3(n_head), dim3(kThreads), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
-    case 32: hipLaunchKernelGGL(k_attention_decode<32>, dim3(n_head), dim3(kThreads), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
-    case 64: hipLaunchKernelGGL(k_attention_decode<64>, dim3(n_head), dim3(kThreads), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
-    default: hipLaunchKernelGGL(k_attention_decode<128>, dim3(n_head), dim3(kThreads), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
+    case 16: hipLaunchKernelGGL(k_attention_decode<16>, dim3(n_head), dim3(AttnCfg<16>::NT), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
+    case 32: hipLaunchKernelGGL(k_attention_decode<32>, dim3(n_head), dim3(AttnCfg<32>::NT), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
+    case 64: hipLaunchKernelGGL(k_attention_decode<64>, dim3(n_head), dim3(AttnCfg<64>::NT), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
+    default: hipLaunchKernelGGL(k_attention_decode<128>, dim3(n_head), dim3(AttnCfg<128>::NT), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
     }
     return hipGetLastError();
 }
@@ -286,6 +342,13 @@ hipError_t launch_argmax(const float *x, int n, int32_t *out, int32_t *tokens, i
                          hipStream_t s)
 {
     hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, x, n, out, tokens, pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_pairs(const float *val, const int32_t *idx, int n, int32_t *out,
+                               int32_t *tokens, int32_t *pos, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_argmax_pairs, dim3(1), dim3(256), 0, s, val, idx, n, out, tokens, pos);
     return hipGetLastError();
 }
 

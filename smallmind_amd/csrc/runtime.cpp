@@ -185,6 +185,9 @@ struct smx_session {
     float *kc = nullptr, *vc = nullptr;
     float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
     int32_t *tokens = nullptr, *pos = nullptr, *amax = nullptr;
+    // argmax fused into the head GEMV: per-workgroup partials
+    float *head_val = nullptr;
+    int32_t *head_idx = nullptr;
     hipGraphExec_t g_prefill = nullptr, g_decode = nullptr;
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     std::atomic<int> busy{0};
@@ -310,9 +313,13 @@ int enqueue_step(smx_session *S, bool with_head, hipStream_t s)
         hgt.beta = m->d_out_b;
         hgt.eps = c.norm_eps;
         hgt.pro = m->llama ? PRO_RMS : PRO_LN;
-        hgt.epi = EPI_STORE;
+        hgt.epi = EPI_ARGMAX;
+        hgt.wg_val = S->head_val;
+        hgt.wg_idx = S->head_idx;
+        hgt.amax_out = S->amax;
+        hgt.tokens = S->tokens;
+        hgt.tok_pos = S->pos;
         SMX_HIP(launch_gemv(hgt, 1, s));
-        SMX_HIP(launch_argmax(S->logits, c.vocab, S->amax, S->tokens, S->pos, s));
     } else {
         SMX_HIP(launch_advance(S->pos, s));
     }
@@ -945,6 +952,9 @@ SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out)
     A((void **)&S->tokens, (size_t)(max_ctx + 1) * 4);
     A((void **)&S->pos, 4);
     A((void **)&S->amax, 4);
+    // the head GEMV has at most one workgroup per two vocabulary rows
+    A((void **)&S->head_val, (size_t)(c.vocab / 2 + 1) * 4);
+    A((void **)&S->head_idx, (size_t)(c.vocab / 2 + 1) * 4);
     for (int i = 0; i < 3 && e == hipSuccess; i++) e = hipEventCreate(&S->ev[i]);
     if (e == hipSuccess) e = hipMemsetAsync(S->tokens, 0, (size_t)(max_ctx + 1) * 4, m->ctx->stream);
     if (e == hipSuccess) e = hipMemsetAsync(S->pos, 0, 4, m->ctx->stream);
@@ -1083,6 +1093,7 @@ SMX_API int smx_session_destroy(smx_session *S)
     for (hipEvent_t e : S->ev) if (e) (void)hipEventDestroy(e);
     free_dev(S->kc); free_dev(S->vc); free_dev(S->x); free_dev(S->q); free_dev(S->att);
     free_dev(S->h); free_dev(S->logits); free_dev(S->tokens); free_dev(S->pos); free_dev(S->amax);
+    free_dev(S->head_val); free_dev(S->head_idx);
     free_dev(S->d_layers); free_dev(S->bar); free_dev(S->abort_flag); free_dev(S->wg_val);
     free_dev(S->wg_idx); free_dev(S->logits_all); free_dev(S->trace);
     S->m->sessions.fetch_sub(1);

@@ -27,7 +27,8 @@ struct AttnSmem {
 };
 
 // sc: LDS scratch of at least n_pos floats.  All NT threads of the workgroup must call this.
-template <int HD, int NT>
+// U: positions per thread per P.V load batch (one batch = one round trip to memory).
+template <int HD, int NT, int U = 8>
 __device__ __forceinline__ void attention_head(const float *__restrict__ qh, const float *__restrict__ K,
                                                const float *__restrict__ V, float *__restrict__ out,
                                                int n_pos, int ctx_stride, float *sc,
@@ -36,22 +37,27 @@ __device__ __forceinline__ void attention_head(const float *__restrict__ qh, con
     constexpr int D4 = HD / 4;
     constexpr int NPL = NT / D4;
     constexpr int NW = NT / 64;
-    constexpr int U = 8;
     const float scale = 1.0f / sqrtf((float)HD);   // MultiHeadAttention.cs:686
     const int tid = opaque_tid();
     if (tid < D4) sm.qs[tid] = ((const float4 *)qh)[tid];
     __syncthreads();
 
+    // K and V of one KV head span less than 4 GiB, so every load is a uniform base plus a
+    // 32-bit byte offset (no 64-bit address per load held in registers).
+    const char *Kb = (const char *)K, *Vb = (const char *)V;
     float mx = -INFINITY;
     for (int j = tid; j < n_pos; j += NT) {
-        const float *kcol = K + j;
         float kv[HD];
 #pragma unroll
-        for (int e = 0; e < HD; e++) kv[e] = kcol[(int64_t)e * ctx_stride];
+        for (int e = 0; e < HD; e++) kv[e] = *(const float *)(Kb + 4u * ((uint32_t)e * (uint32_t)ctx_stride + (uint32_t)j));
+        // q is read from LDS (broadcast) at each use: held in registers across the position
+        // loop it would take HD VGPRs and, at 1024 threads, force the K loads to serialize.
+        int z = 0;
+        asm volatile("" : "+s"(z));
         float s = 0.0f;
 #pragma unroll
         for (int e4 = 0; e4 < D4; e4++) {
-            const float4 qv = sm.qs[e4];
+            const float4 qv = sm.qs[e4 + z];
             s = __builtin_fmaf(qv.x, kv[4 * e4 + 0], s);
             s = __builtin_fmaf(qv.y, kv[4 * e4 + 1], s);
             s = __builtin_fmaf(qv.z, kv[4 * e4 + 2], s);
@@ -83,7 +89,8 @@ __device__ __forceinline__ void attention_head(const float *__restrict__ qh, con
         for (int u = 0; u < U; u++) {
             const int j = j0 + u * NPL;
             const bool ok = j < n_pos;
-            vv[u] = ok ? ((const float4 *)(V + (int64_t)j * HD))[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            vv[u] = ok ? *(const float4 *)(Vb + 16u * ((uint32_t)j * (HD / 4) + (uint32_t)c4))
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             pp[u] = ok ? sc[j] : 0.0f;
         }
 #pragma unroll

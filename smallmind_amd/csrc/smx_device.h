@@ -109,12 +109,49 @@ __device__ __forceinline__ int lane_id() { return opaque_tid() & 63; }
 // addresses derived from it live in SGPRs.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
+// Load of a wave-uniform value through the scalar data cache (s_load, counted by lgkmcnt), so
+// it neither waits for nor delays the vector-memory loads in flight.  The address must be the
+// same in every lane, and the data must not be written by the running kernel before the load.
+template <typename T>
+__device__ __forceinline__ T ld_uniform(const T *p)
+{
+    return *(const __attribute__((address_space(4))) T *)p;
+}
+
 // ---- wave64 / block reductions ------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v)
 {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
+}
+
+// Sum over each row of 16 lanes with DPP (quad swaps, half-row and row mirrors): no LDS
+// traffic.  Every lane of a row ends with the same bits (each step adds a commuted pair).
+// All 64 lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v)
+{
+    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);   // row_half_mirror
+    v += dpp_mov<0x140>(v);   // row_mirror
+    return v;
+}
+// Wave-uniform total of v over all 64 lanes (all lanes active): row sums, then the four row
+// totals read into scalars and added in a fixed order.
+__device__ __forceinline__ float wave_sum_uniform(float v)
+{
+    v = row16_sum(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
 __device__ __forceinline__ float wave_max(float v)

@@ -14,9 +14,14 @@ namespace smx {
 // as one little-endian bit stream per half (GgufModelLoader.cs:688-705).
 __device__ __forceinline__ uint32_t kq_scale6(uint32_t h1, uint32_t h2, uint32_t h3, int j, int sel)
 {
-    // h1 = bytes 4..7, h2 = bytes 8..11, h3 = bytes 12..15 of the super-block.
-    uint64_t s = sel == 0 ? (((uint64_t)h2 << 32) | h1) : (((uint64_t)h3 << 16) | (h2 >> 16));
-    return (uint32_t)(s >> (6 * j)) & 63u;
+    // h1 = bytes 4..7, h2 = bytes 8..11, h3 = bytes 12..15 of the super-block: the scales sit
+    // at bits 6j, the mins at bits 48 + 6j of the 96-bit stream h3:h2:h1.  One funnel shift
+    // (v_alignbit_b32) of the two words holding the field extracts it without 64-bit values.
+    const uint32_t b = 6u * (uint32_t)j + (sel ? 48u : 0u);
+    const uint32_t wd = b >> 5;
+    const uint32_t lo = wd == 0 ? h1 : wd == 1 ? h2 : h3;
+    const uint32_t hi = wd == 0 ? h2 : wd == 1 ? h3 : 0u;
+    return __builtin_amdgcn_alignbit(hi, lo, b & 31u) & 63u;
 }
 
 template <int F>

@@ -70,6 +70,13 @@ template <> struct Raw<FMT_Q4_0> {
         q = *(const uint4 *)(w.q + blk * 16);
         d = w.d[blk];
     }
+    // 32-bit offsets (the whole matrix is below 4 GiB): `row_blk` = row * blocks per row.
+    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    {
+        const uint32_t blk = row_blk + (uint32_t)c;
+        q = *(const uint4 *)(w.q + blk * 16u);
+        d = w.d[blk];
+    }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int) const
     {
         const uint32_t v[4] = {q.x ^ 0x88888888u, q.y ^ 0x88888888u, q.z ^ 0x88888888u, q.w ^ 0x88888888u};
@@ -93,6 +100,13 @@ template <> struct Raw<FMT_Q8_0> {
         q1 = p[1];
         d = w.d[blk];
     }
+    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    {
+        const uint32_t blk = row_blk + (uint32_t)c;
+        q0 = *(const uint4 *)(w.q + blk * 32u);
+        q1 = *(const uint4 *)(w.q + blk * 32u + 16u);
+        d = w.d[blk];
+    }
     __device__ __forceinline__ float dot(const float4 *xv, float, float, int) const
     {
         const uint32_t v[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
@@ -113,6 +127,12 @@ template <> struct Raw<FMT_Q4_K> {
         const uint8_t *base = w.q + (row * w.nb + (c >> 3)) * 144;
         h = *(const uint4 *)base;
         q = *(const uint4 *)(base + 16 + 16 * (c & 7));
+    }
+    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    {
+        const uint32_t off = (row_blk + ((uint32_t)c >> 3)) * 144u;
+        h = *(const uint4 *)(w.q + off);
+        q = *(const uint4 *)(w.q + off + 16u + 16u * ((uint32_t)c & 7u));
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int c) const
     {
@@ -138,6 +158,13 @@ template <> struct Raw<FMT_Q5_K> {
         h = *(const uint4 *)base;
         H = *(const uint32_t *)(base + 16 + 4 * j);
         q = *(const uint4 *)(base + 48 + 16 * j);
+    }
+    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    {
+        const uint32_t off = (row_blk + ((uint32_t)c >> 3)) * 176u, j = (uint32_t)c & 7u;
+        h = *(const uint4 *)(w.q + off);
+        H = *(const uint32_t *)(w.q + off + 16u + 4u * j);
+        q = *(const uint4 *)(w.q + off + 48u + 16u * j);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int c) const
     {
@@ -172,6 +199,14 @@ template <> struct Raw<FMT_Q6_K> {
         D = *(const uint2 *)(base + 128 + 8 * cc);
         scw = *(const uint16_t *)(base + 192 + 2 * cc);
         d = w.d[sbi];
+    }
+    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    {
+        const uint32_t sb = row_blk + ((uint32_t)c >> 3), off = sb * 208u, cc = (uint32_t)c & 7u;
+        q = *(const uint4 *)(w.q + off + 16u * cc);
+        D = *(const uint2 *)(w.q + off + 128u + 8u * cc);
+        scw = *(const uint16_t *)(w.q + off + 192u + 2u * cc);
+        d = w.d[sb];
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int) const
     {

@@ -61,7 +61,10 @@ enum Epi {
     EPI_RESID = 1,   // out[r] = resid[r] + (acc + bias)
     EPI_SILU = 2,    // rows interleaved gate/up: out[i] = silu(g) * u
     EPI_GELU = 3,    // out[r] = gelu(acc + bias)
-    EPI_QKV = 4      // rows [Q | K | V]: RoPE on Q/K, Q -> out, K/V -> caches at *pos
+    EPI_QKV = 4,     // rows [Q | K | V]: RoPE on Q/K, Q -> out, K/V -> caches at *pos
+    EPI_ARGMAX = 5   // out[r] = acc + bias; each workgroup's best row -> wg_val/wg_idx, then a
+                     // one-workgroup kernel takes the argmax over them (lowest index on ties)
+                     // -> *amax_out and, with `tokens`, tokens[*tok_pos + 1], ++*tok_pos
 };
 
 struct GemvArgs {
@@ -88,6 +91,10 @@ struct GemvArgs {
     int x_embed;
     WView emb, embp;
     int64_t emb_row, embp_row;
+    // EPI_ARGMAX (m == 1): per-workgroup partials [grid] and the outputs
+    float *wg_val;
+    int32_t *wg_idx;
+    int32_t *amax_out, *tokens, *tok_pos;
 };
 
 hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s);
@@ -150,6 +157,9 @@ hipError_t launch_silu_mul(const float *g, const float *u, float *y, int64_t n, 
 hipError_t launch_gelu(const float *x, float *y, int64_t n, hipStream_t s);
 hipError_t launch_argmax(const float *x, int n, int32_t *out, int32_t *tokens, int32_t *pos,
                          hipStream_t s);
+// Argmax over n (value, index) pairs, lowest index on ties; same outputs as launch_argmax.
+hipError_t launch_argmax_pairs(const float *val, const int32_t *idx, int n, int32_t *out,
+                               int32_t *tokens, int32_t *pos, hipStream_t s);
 hipError_t launch_embed(const WView &tok, const WView *posw, const int32_t *tokens,
                         const int32_t *pos, float *x, hipStream_t s);
 hipError_t launch_advance(int32_t *pos, hipStream_t s);
