@@ -2,9 +2,10 @@
 
 One step = one request of the configs[2] workload: a 512-token seeded prompt (prefilled
 through the KV cache) and 256 greedy tokens, all on the device.  `value` is decode tokens/s
-(GPU-event time of the token-producing steps).  The dominant kernel -- the fused gate/up
-Q4_K GEMV (k_gemv<Q4_K,R=4>, 11264 x 2048) -- is then timed on its own with HIP events over
-rotating weight copies larger than the 256 MB MALL, giving the roofline figure.  The CPU
+(GPU-event time of the token-producing steps).  The dominant kernel -- the fused Q4_K GEMV at
+the gate/up shape (11264 x 2048) -- is then timed on its own with HIP events around replays of
+a captured graph of launches over rotating weight copies larger than the 256 MB MALL, giving
+the roofline figure; the configs[1] Q4_0 GEMV shapes are timed the same way.  The CPU
 baseline is the oracle's reference-faithful path (fp32 weights dequantized at load, one
 thread) timed on a bounded sample of the same model.
 """
@@ -28,35 +29,92 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def gemv_roofline(n_iter: int = 200):
-    """Times the gate/up-shaped fused Q4_K GEMV (11264 x 2048, x in LDS, RMSNorm-free store
-    epilogue -- the same kernel instance) on the current stream over >512 MB of weights."""
+def gemv_timing(qt: int, N: int, K: int, seed: int, min_bytes: int = 600 << 20, reps: int = 10):
+    """Average launch duration of the fused GEMV y = W x (smx_weight_matmul) for one [N, K]
+    weight of block type `qt`, on the current torch stream, with HIP events around replays of a
+    captured graph of back-to-back launches that cycle over enough distinct weight copies
+    (>= 600 MB) to defeat the 256 MB MALL: every launch streams its weights from HBM."""
     import torch
 
-    from smallmind_amd.quantization import GpuWeightTensor, fill_normal, quantize
-    N, K = 2 * 5632, 2048
-    wbytes = N * (K // 256) * 144
-    copies = max(2, (600 << 20) // wbytes + 1)
-    blocks = quantize(12, fill_normal(3, N * K, 0.02))
-    ws = [GpuWeightTensor(12, N, K, blocks) for _ in range(copies)]
+    from smallmind_amd.quantization import GpuWeightTensor, fill_normal, quantize, row_bytes
+    wbytes = N * row_bytes(qt, K)
+    copies = max(2, min_bytes // wbytes + 1)
+    blocks = quantize(qt, fill_normal(seed, N * K, 0.02))
+    ws = [GpuWeightTensor(qt, N, K, blocks) for _ in range(copies)]
     del blocks
     x = torch.randn(K, device="cuda")
     y = torch.empty(N, device="cuda")
-    for w in ws:
-        w.mat_mul(x, y, 1, K, N)
+    n_launch = max(copies, 64)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        for w in ws:
+            w.mat_mul(x, y, 1, K, N)
+        with torch.cuda.graph(g, stream=s):
+            for i in range(n_launch):
+                ws[i % copies].mat_mul(x, y, 1, K, N)
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            g.replay()
+        e1.record(s)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(n_iter):
-        ws[i % copies].mat_mul(x, y, 1, K, N)
-    e1.record()
-    torch.cuda.synchronize()
-    avg_s = e0.elapsed_time(e1) * 1e-3 / n_iter
+    avg_s = e0.elapsed_time(e1) * 1e-3 / (reps * n_launch)
     alg = wbytes + K * 4 + N * 4          # weights + activations in + outputs
+    del g
     for w in ws:
         w.close()
-    return {"kernel": "k_gemv<Q4_K,R=4> (fused dequant-GEMV, 11264x2048)", "avg_us": avg_s * 1e6,
-            "bytes": alg, "gbs": alg / avg_s / 1e9, "copies": copies}
+    return {"avg_us": avg_s * 1e6, "bytes": alg, "gbs": alg / avg_s / 1e9, "copies": copies,
+            "launches": reps * n_launch}
+
+
+def gemv_roofline():
+    """The dominant decode kernel: the fused Q4_K GEMV at the gate/up shape (11264 x 2048)."""
+    g = gemv_timing(12, 2 * 5632, 2048, seed=3)
+    g["kernel"] = "k_gemv<Q4_K,R=4,S=1> (fused dequant-GEMV, gate/up shape 11264x2048)"
+    return g
+
+
+def c2_gemv_lines():
+    """configs[1] (C2): Q4_0 GEMV at the three reference shapes."""
+    from smallmind_amd.synthetic import GEMV_SHAPES
+    out = []
+    for i, (N, K) in enumerate(GEMV_SHAPES):
+        g = gemv_timing(2, N, K, seed=10 + i)
+        out.append({"shape": [N, K], "avg_us": round(g["avg_us"], 3), "bytes": g["bytes"],
+                    "gbs": round(g["gbs"], 1), "frac": round(g["gbs"] / HBM_PEAK_GBS, 4)})
+    return out
+
+
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemv_q4k_11264x2048_pmc.md")
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the roofline kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by what the counter reads for a plain
+    copy kernel of known size), or None when no summary is present."""
+    if not os.path.exists(PMC_SUMMARY):
+        return None
+    with open(PMC_SUMMARY) as f:
+        for line in f:
+            if line.startswith("hbm_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    return None
+
+
+def copy_calibration(n_bytes: int = 1 << 30, reps: int = 5):
+    """A plain device copy of known size (reads n_bytes, writes n_bytes per launch), run under
+    rocprofv3 --pmc to scale FETCH_SIZE / WRITE_SIZE to bytes."""
+    import torch
+    a = torch.empty(n_bytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n_bytes, "copy_bytes_written": n_bytes, "launches": reps}),
+          flush=True)
 
 
 def cpu_baseline(kept, wl, budget_s: float = 15.0):
@@ -90,6 +148,10 @@ def main():
     ap.add_argument("--workload", default="llama-1.1b-q4_k")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="time only the dominant GEMV kernel (for rocprofv3 --pmc passes)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each box has one "
@@ -98,6 +160,16 @@ def main():
 
     import numpy as np
     import torch
+
+    if args.copy_calibration:
+        copy_calibration()
+        return
+    if args.roofline_only:
+        g = gemv_roofline()
+        print(json.dumps({"roofline_kernel": g["kernel"], "avg_us": round(g["avg_us"], 3),
+                          "bytes_per_launch": g["bytes"], "gbs": round(g["gbs"], 1),
+                          "launches": g["launches"]}), flush=True)
+        return
 
     from smallmind_amd.model import GpuTransformerModel
     from smallmind_amd.synthetic import WORKLOADS, load_synthetic_on_device, prompt_tokens
@@ -149,9 +221,12 @@ def main():
         log("timing the dominant GEMV kernel")
         g = gemv_roofline()
         out["roofline"] = {"bound": "hbm", "achieved": round(g["gbs"], 1), "peak": HBM_PEAK_GBS,
-                           "unit": "GB/s", "frac": round(g["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                           "unit": "GB/s", "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
+                           "traffic": traffic_from_profiles(),
                            "kernel": g["kernel"], "avg_us": round(g["avg_us"], 3),
                            "bytes_per_launch": g["bytes"]}
+        log("timing the configs[1] Q4_0 GEMV shapes")
+        out["c2_q4_0_gemv"] = c2_gemv_lines()
     sess.close()
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle, one thread)")
