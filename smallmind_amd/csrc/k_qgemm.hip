@@ -1,0 +1,453 @@
+// k_qgemm.hip -- quantized GEMM Y[M][N] = X[M][K] . W[N][K]^T on the bf16 matrix cores, for
+// several activation rows at once (m >= 16: batched decode of many sessions, prefill chunks,
+// IWeightTensor.MatMul with m > 1; NeuralNet.cs:145-298, MatMulF32Q8.cs:23-80).
+//
+// Exactness.  The MFMA inputs are bf16, the reference computes in fp32.  Both sides are made
+// exact:
+//   * weights enter as their integer codes, which bf16 represents exactly: 128 + q is built
+//     with one and-or per pair of codes (bf16 0x4300 | q; Q8_0 codes go through a conversion),
+//     and the block scales are applied to the fp32 result of each 32-element sub-block;
+//   * activations enter as three bf16 parts, x = hi + mid + lo (8 + 8 + 8 significant bits),
+//     so every product code x part is exact and the MFMA accumulates in fp32.
+// A fourth product with an all-ones weight operand gives sum(x) per sub-block, which removes
+// the +128 code offset and supplies the min term of Q4_K/Q5_K:
+//   y += sc * (C - off * sum x) - m * sum x        (C = sum (128 + q) x over the sub-block).
+//
+// MFMA v_mfma_f32_16x16x32_bf16: A = activation parts (16 tokens x 32 k), B = weight codes
+// (32 k x 16 weight rows), D[token][row].  Lane l supplies token / weight row l % 16 and the
+// 8 k-values of group l / 16; D lane l holds tokens 4*(l/16)+0..3 of weight row l % 16.  The
+// order of the 8 k-values inside a group is free as long as A and B agree; both use
+// element order {0,4,1,5,2,6,3,7}, the order in which ((v >> 4p) & 0x000F000F) lays out two
+// nibble codes per 32-bit pair.
+//
+// Work decomposition: a workgroup is 4 waves that split the sub-blocks of K between them
+// (wave w takes sub-blocks w, w+4, ...) for RT row tiles of 16 weight rows and TT token tiles
+// of 16 tokens; the four partial tiles are summed in LDS in a fixed order.
+//
+// Activation parts come from k_qprep: Xp[tt][s][p][g][t][8 bf16] (1 KB per (token tile,
+// sub-block, part), lane l reads 16 bytes at l*16).
+#include "smx_device.h"
+#include "smx_formats.h"
+#include "smx_internal.h"
+
+namespace smx {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v)
+{
+    bf16x8 r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+}
+
+__device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// bf16 of an fp32 holding an integer of at most 8 significant bits (exact: the low 16 bits are 0)
+__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi)
+{
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// ---- per-format weight operand --------------------------------------------------------------
+// load(): the raw words of (row, sub-block s, k-group g) -- codes and scale fields -- issued
+// one sub-block ahead of use; codes(): 4 bf16 pairs (element p, element p + 4) of the group's
+// 8 codes; scale(): the per-(row, sub-block) scale terms.
+struct RawQ {
+    uint4 h;          // K-quant super-block header
+    uint32_t v, v2;   // code bytes of the group
+    uint32_t H, H2;   // high bits (Q5_K: qh'; Q6_K: D0, D1)
+    uint32_t d;       // fp16 scale (Q4_0, Q8_0, Q6_K) / Q6_K int8 scale pair in the high half
+};
+struct Scl {
+    float sc, sc2, m;   // Q6_K uses sc (first 16 elements) and sc2 (second 16)
+};
+
+template <int F> struct QW;
+
+// Q4_0: block = sub-block of 32; codes n ^ 8 (value = code - 8): offset 128 + 8.
+template <> struct QW<FMT_Q4_0> {
+    static constexpr float kOff = 136.0f;
+    static constexpr bool kHalves = false;
+    __device__ __forceinline__ static RawQ load(const WView &w, uint32_t row, int s, int g)
+    {
+        RawQ r{};
+        const uint32_t blk = row * (uint32_t)w.nb + (uint32_t)s;
+        r.v = *(const uint32_t *)(w.q + blk * 16u + 4u * g);
+        r.d = w.d[blk];
+        return r;
+    }
+    __device__ __forceinline__ static uint4 codes(const RawQ &r, int)
+    {
+        const uint32_t v = r.v ^ 0x88888888u;
+        return make_uint4((v & 0x000F000Fu) | 0x43004300u, ((v >> 4) & 0x000F000Fu) | 0x43004300u,
+                          ((v >> 8) & 0x000F000Fu) | 0x43004300u, ((v >> 12) & 0x000F000Fu) | 0x43004300u);
+    }
+    __device__ __forceinline__ static Scl scale(const RawQ &r, int) { return {h2f(r.d), 0.0f, 0.0f}; }
+};
+
+// Q8_0: int8 codes; bf16(b ^ 0x80) = value + 128 (exact integers up to 255).
+template <> struct QW<FMT_Q8_0> {
+    static constexpr float kOff = 128.0f;
+    static constexpr bool kHalves = false;
+    __device__ __forceinline__ static RawQ load(const WView &w, uint32_t row, int s, int g)
+    {
+        RawQ r{};
+        const uint32_t blk = row * (uint32_t)w.nb + (uint32_t)s;
+        const uint2 v = *(const uint2 *)(w.q + blk * 32u + 8u * g);
+        r.v = v.x;
+        r.v2 = v.y;
+        r.d = w.d[blk];
+        return r;
+    }
+    __device__ __forceinline__ static uint4 codes(const RawQ &r, int)
+    {
+        const uint32_t a = r.v ^ 0x80808080u, b = r.v2 ^ 0x80808080u;
+        // pair p = (element p, element p + 4) = (byte p of a, byte p of b)
+        float a0, a1, a2, a3, b0, b1, b2, b3;
+        asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(a0) : "v"(a));
+        asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(a1) : "v"(a));
+        asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(a2) : "v"(a));
+        asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(a3) : "v"(a));
+        asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(b0) : "v"(b));
+        asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(b1) : "v"(b));
+        asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(b2) : "v"(b));
+        asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(b3) : "v"(b));
+        return make_uint4(pack_hi16(a0, b0), pack_hi16(a1, b1), pack_hi16(a2, b2), pack_hi16(a3, b3));
+    }
+    __device__ __forceinline__ static Scl scale(const RawQ &r, int) { return {h2f(r.d), 0.0f, 0.0f}; }
+};
+
+// Q4_K: sub-block s = qs bytes 16 + 16*(s % 8) of super-block s / 8.
+template <> struct QW<FMT_Q4_K> {
+    static constexpr float kOff = 128.0f;
+    static constexpr bool kHalves = false;
+    __device__ __forceinline__ static RawQ load(const WView &w, uint32_t row, int s, int g)
+    {
+        RawQ r{};
+        const uint32_t base = (row * (uint32_t)w.nb + ((uint32_t)s >> 3)) * 144u;
+        r.h = *(const uint4 *)(w.q + base);
+        r.v = *(const uint32_t *)(w.q + base + 16u + 16u * ((uint32_t)s & 7u) + 4u * g);
+        return r;
+    }
+    __device__ __forceinline__ static uint4 codes(const RawQ &r, int)
+    {
+        const uint32_t v = r.v;
+        return make_uint4((v & 0x000F000Fu) | 0x43004300u, ((v >> 4) & 0x000F000Fu) | 0x43004300u,
+                          ((v >> 8) & 0x000F000Fu) | 0x43004300u, ((v >> 12) & 0x000F000Fu) | 0x43004300u);
+    }
+    __device__ __forceinline__ static Scl scale(const RawQ &r, int s)
+    {
+        const int j = s & 7;
+        return {h2f(r.h.x & 0xFFFFu) * (float)kq_scale6(r.h.y, r.h.z, r.h.w, j, 0), 0.0f,
+                h2f(r.h.x >> 16) * (float)kq_scale6(r.h.y, r.h.z, r.h.w, j, 1)};
+    }
+};
+
+// Q5_K: codes = ql nibble | high bit (bit-permuted qh'), value = q - 16: offset 128 + 16.
+template <> struct QW<FMT_Q5_K> {
+    static constexpr float kOff = 144.0f;
+    static constexpr bool kHalves = false;
+    __device__ __forceinline__ static RawQ load(const WView &w, uint32_t row, int s, int g)
+    {
+        RawQ r{};
+        const uint32_t base = (row * (uint32_t)w.nb + ((uint32_t)s >> 3)) * 176u;
+        const uint32_t j = (uint32_t)s & 7u;
+        r.h = *(const uint4 *)(w.q + base);
+        r.v = *(const uint32_t *)(w.q + base + 48u + 16u * j + 4u * g);
+        r.H = *(const uint32_t *)(w.q + base + 16u + 4u * j);
+        return r;
+    }
+    __device__ __forceinline__ static uint4 codes(const RawQ &r, int g)
+    {
+        // the high bit of element 8g + 2k + p sits at bit 8k + 2g + p of H
+        const uint32_t v = r.v, H = r.H;
+        const uint32_t h0 = H >> (2 * g), h1 = H >> (2 * g + 1), h2 = H >> (2 * g + 8), h3 = H >> (2 * g + 9);
+        return make_uint4((v & 0x000F000Fu) | ((h0 & 0x00010001u) << 4) | 0x43004300u,
+                          ((v >> 4) & 0x000F000Fu) | ((h1 & 0x00010001u) << 4) | 0x43004300u,
+                          ((v >> 8) & 0x000F000Fu) | ((h2 & 0x00010001u) << 4) | 0x43004300u,
+                          ((v >> 12) & 0x000F000Fu) | ((h3 & 0x00010001u) << 4) | 0x43004300u);
+    }
+    __device__ __forceinline__ static Scl scale(const RawQ &r, int s)
+    {
+        const int j = s & 7;
+        return {h2f(r.h.x & 0xFFFFu) * (float)kq_scale6(r.h.y, r.h.z, r.h.w, j, 0), 0.0f,
+                h2f(r.h.x >> 16) * (float)kq_scale6(r.h.y, r.h.z, r.h.w, j, 1)};
+    }
+};
+
+// Q6_K: 6-bit codes, value = q - 32: offset 128 + 32; two 16-element scales per sub-block.
+template <> struct QW<FMT_Q6_K> {
+    static constexpr float kOff = 160.0f;
+    static constexpr bool kHalves = true;
+    __device__ __forceinline__ static RawQ load(const WView &w, uint32_t row, int s, int g)
+    {
+        RawQ r{};
+        const uint32_t sb = row * (uint32_t)w.nb + ((uint32_t)s >> 3);
+        const uint32_t base = sb * 208u, cc = (uint32_t)s & 7u;
+        r.v = *(const uint32_t *)(w.q + base + 16u * cc + 4u * g);
+        const uint2 D = *(const uint2 *)(w.q + base + 128u + 8u * cc);
+        r.H = D.x;
+        r.H2 = D.y;
+        r.d = (uint32_t)w.d[sb] | ((uint32_t)*(const uint16_t *)(w.q + base + 192u + 2u * cc) << 16);
+        return r;
+    }
+    __device__ __forceinline__ static uint4 codes(const RawQ &r, int g)
+    {
+        // the two high bits of element 8g + 2k + p sit at bits 8k + 2g of D_p
+        const uint32_t v = r.v;
+        const uint32_t e0 = r.H >> (2 * g), e1 = r.H2 >> (2 * g), e2 = r.H >> (2 * g + 8), e3 = r.H2 >> (2 * g + 8);
+        return make_uint4((v & 0x000F000Fu) | ((e0 & 0x00030003u) << 4) | 0x43004300u,
+                          ((v >> 4) & 0x000F000Fu) | ((e1 & 0x00030003u) << 4) | 0x43004300u,
+                          ((v >> 8) & 0x000F000Fu) | ((e2 & 0x00030003u) << 4) | 0x43004300u,
+                          ((v >> 12) & 0x000F000Fu) | ((e3 & 0x00030003u) << 4) | 0x43004300u);
+    }
+    __device__ __forceinline__ static Scl scale(const RawQ &r, int)
+    {
+        const float d = h2f(r.d & 0xFFFFu);
+        return {d * (float)(int8_t)((r.d >> 16) & 0xFFu), d * (float)(int8_t)(r.d >> 24), 0.0f};
+    }
+};
+
+constexpr uint4 kZero4 = {0u, 0u, 0u, 0u};
+constexpr uint32_t kOnes = 0x3F803F80u;   // bf16 1.0 pair
+
+template <int F, int RT, int TT>
+__global__ __launch_bounds__(256) void k_qgemm(WView w, const uint8_t *__restrict__ xp, int M,
+                                               float *__restrict__ y, int64_t y_stride)
+{
+    using Q = QW<F>;
+    constexpr int NW = 4;
+    __shared__ f32x4 s_part[NW - 1][RT * TT][64];
+    const int wv = wave_id();
+    const int lane = lane_id();
+    const int g = lane >> 4, li = lane & 15;
+    const uint32_t N = (uint32_t)w.rows;
+    const int nsb = (int)(w.cols >> 5);
+    const uint32_t row_base = blockIdx.x * (16 * RT);
+    const int tt0 = blockIdx.y * TT;
+    const int ntt = (M + 15) >> 4;
+
+    f32x4 acc[RT][TT];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int t = 0; t < TT; t++) acc[r][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // weight rows of this lane (B operand column l % 16), clamped to the matrix
+    uint32_t wrow[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        const uint32_t rr = row_base + 16 * r + li;
+        wrow[r] = rr < N ? rr : N - 1;
+    }
+    const uint4 ones_a = Q::kHalves ? (g < 2 ? make_uint4(kOnes, kOnes, kOnes, kOnes) : kZero4)
+                                    : make_uint4(kOnes, kOnes, kOnes, kOnes);
+    const uint4 ones_b = g >= 2 ? make_uint4(kOnes, kOnes, kOnes, kOnes) : kZero4;
+
+    // one sub-block ahead: raw weight words and activation parts of the next sub-block are in
+    // flight while the current one is multiplied
+    RawQ raw[RT];
+    uint4 xa[TT][3];
+    auto load = [&](int s, RawQ *rq, uint4 (*xq)[3]) {
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const int tt = tt0 + t < ntt ? tt0 + t : ntt - 1;
+#pragma unroll
+            for (int p = 0; p < 3; p++)
+                xq[t][p] = *(const uint4 *)(xp + (((size_t)tt * nsb + s) * 3 + p) * 1024 + lane * 16);
+        }
+#pragma unroll
+        for (int r = 0; r < RT; r++) rq[r] = Q::load(w, wrow[r], s, g);
+    };
+    if (wv < nsb) load(wv, raw, xa);
+    for (int s = wv; s < nsb; s += NW) {
+        RawQ rawn[RT];
+        uint4 xan[TT][3];
+        const bool more = s + NW < nsb;
+        if (more) load(s + NW, rawn, xan);
+        uint4 wc[RT];
+        Scl sc[RT];
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            wc[r] = Q::codes(raw[r], g);
+            sc[r] = Q::scale(raw[r], s);
+        }
+        // sum(x) per token (and per half for Q6_K): the same for every weight row
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            f32x4 sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                sa = mfma(xa[t][p], ones_a, sa);
+                if constexpr (Q::kHalves) sb = mfma(xa[t][p], ones_b, sb);
+            }
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                if constexpr (Q::kHalves) {
+                    const uint4 ca = g < 2 ? wc[r] : kZero4, cb = g >= 2 ? wc[r] : kZero4;
+                    f32x4 da = {0.0f, 0.0f, 0.0f, 0.0f}, db = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int p = 0; p < 3; p++) {
+                        da = mfma(xa[t][p], ca, da);
+                        db = mfma(xa[t][p], cb, db);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        acc[r][t][i] += sc[r].sc * (da[i] - Q::kOff * sa[i]) + sc[r].sc2 * (db[i] - Q::kOff * sb[i]);
+                } else {
+                    f32x4 dc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int p = 0; p < 3; p++) dc = mfma(xa[t][p], wc[r], dc);
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        acc[r][t][i] += sc[r].sc * (dc[i] - Q::kOff * sa[i]) - sc[r].m * sa[i];
+                }
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int r = 0; r < RT; r++) raw[r] = rawn[r];
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int p = 0; p < 3; p++) xa[t][p] = xan[t][p];
+        }
+    }
+
+    // sum the four waves' partial tiles in a fixed order; wave 0 stores
+    if (wv > 0) {
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int t = 0; t < TT; t++) s_part[wv - 1][r * TT + t][lane] = acc[r][t];
+    }
+    __syncthreads();
+    if (wv != 0) return;
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            f32x4 v = acc[r][t];
+#pragma unroll
+            for (int k = 0; k < NW - 1; k++) {
+                const f32x4 o = s_part[k][r * TT + t][lane];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] += o[i];
+            }
+            const uint32_t row = row_base + 16 * r + li;
+            if (row >= N) continue;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tok = (tt0 + t) * 16 + 4 * g + i;
+                if (tok < M) y[(int64_t)tok * y_stride + row] = v[i];
+            }
+        }
+}
+
+// Activation parts: token m, sub-block s, part p -> Xp[m/16][s][p][g][m%16][perm] (bf16).
+// x = hi + mid + lo with hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid), each
+// rounded to nearest even; tokens beyond M (tile padding) are zero.
+__device__ __forceinline__ uint32_t bf16_rne(float f)
+{
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__global__ __launch_bounds__(256) void k_qprep(const float *__restrict__ x, int64_t x_stride, int M,
+                                               int K, uint8_t *__restrict__ xp)
+{
+    // one thread per (token, sub-block, group): 8 elements
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int nsb = K >> 5;
+    const int64_t Mp = ((int64_t)M + 15) & ~(int64_t)15;
+    if (id >= Mp * nsb * 4) return;
+    const int g = (int)(id & 3);
+    const int64_t r = id >> 2;
+    const int s = (int)(r % nsb);
+    const int m = (int)(r / nsb);
+    float v[8];
+    if (m < M) {
+        const float4 *src = (const float4 *)(x + (int64_t)m * x_stride + 32 * s + 8 * g);
+        const float4 a = src[0], b = src[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = 0.0f;
+    }
+    uint32_t part[3][8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float f = v[i];
+        const uint32_t h = bf16_rne(f);
+        const float r1 = f - __uint_as_float(h << 16);
+        const uint32_t mm = bf16_rne(r1);
+        const float r2 = r1 - __uint_as_float(mm << 16);
+        part[0][i] = h;
+        part[1][i] = mm;
+        part[2][i] = bf16_rne(r2);
+    }
+    const int tt = m >> 4, t = m & 15;
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+        // pair q = (element q, element q + 4)
+        uint4 o;
+        o.x = part[p][0] | (part[p][4] << 16);
+        o.y = part[p][1] | (part[p][5] << 16);
+        o.z = part[p][2] | (part[p][6] << 16);
+        o.w = part[p][3] | (part[p][7] << 16);
+        *(uint4 *)(xp + (((size_t)tt * nsb + s) * 3 + p) * 1024 + (g * 16 + t) * 16) = o;
+    }
+}
+
+template <int F, int RT, int TT>
+hipError_t launch_frt(const WView &w, const uint8_t *xp, int M, float *y, int64_t ys, hipStream_t s)
+{
+    const dim3 grid((unsigned)((w.rows + 16 * RT - 1) / (16 * RT)), (unsigned)(((M + 15) / 16 + TT - 1) / TT));
+    hipLaunchKernelGGL((k_qgemm<F, RT, TT>), grid, dim3(256), 0, s, w, xp, M, y, ys);
+    return hipGetLastError();
+}
+
+template <int F>
+hipError_t launch_f(const WView &w, const uint8_t *xp, int M, float *y, int64_t ys, hipStream_t s)
+{
+    // Token tiles per workgroup: 4 for prefill-sized M (weights reused across 64 tokens), else
+    // 1; row tiles: enough workgroups to fill the chip.
+    if (M > 32) return launch_frt<F, 1, 4>(w, xp, M, y, ys, s);
+    if (w.rows >= 16 * 4 * 256) return launch_frt<F, 4, 1>(w, xp, M, y, ys, s);
+    if (w.rows >= 16 * 2 * 256) return launch_frt<F, 2, 1>(w, xp, M, y, ys, s);
+    return launch_frt<F, 1, 1>(w, xp, M, y, ys, s);
+}
+
+}  // namespace
+
+size_t qgemm_xp_bytes(int M, int K) { return (size_t)((M + 15) / 16) * (K / 32) * 3 * 1024; }
+
+hipError_t launch_qgemm(const WView &w, const float *x, int64_t x_stride, int M, float *y,
+                        int64_t y_stride, uint8_t *xp, hipStream_t s)
+{
+    if (M <= 0 || w.cols % 32 != 0) return hipErrorInvalidValue;
+    if ((uint64_t)w.rows * (uint64_t)w.nb * (uint64_t)fmt_main_bytes(w.fmt) >= (1ull << 32))
+        return hipErrorInvalidValue;
+    const int K = (int)w.cols;
+    const int64_t threads = (int64_t)((M + 15) / 16 * 16) * (K / 32) * 4;
+    hipLaunchKernelGGL(k_qprep, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, x, x_stride, M, K, xp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    switch (w.fmt) {
+    case FMT_Q4_0: return launch_f<FMT_Q4_0>(w, xp, M, y, y_stride, s);
+    case FMT_Q8_0: return launch_f<FMT_Q8_0>(w, xp, M, y, y_stride, s);
+    case FMT_Q4_K: return launch_f<FMT_Q4_K>(w, xp, M, y, y_stride, s);
+    case FMT_Q5_K: return launch_f<FMT_Q5_K>(w, xp, M, y, y_stride, s);
+    case FMT_Q6_K: return launch_f<FMT_Q6_K>(w, xp, M, y, y_stride, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace smx

@@ -567,6 +567,10 @@ SMX_API int smx_weight_info(const smx_weight *w, int *type, int64_t *rows, int64
     return SMX_OK;
 }
 
+// Activation rows from which IWeightTensor.MatMul uses the matrix-core GEMM instead of one
+// GEMV pass per row.
+constexpr int kQgemmMinRows = 4;
+
 SMX_API int smx_weight_matmul(const smx_weight *w, const float *act_dev, float *out_dev, int m,
                               int k, int n, void *stream)
 {
@@ -575,6 +579,19 @@ SMX_API int smx_weight_matmul(const smx_weight *w, const float *act_dev, float *
         SMX_FAIL(SMX_EINVAL, "smx_weight_matmul: k=%d must equal cols=%lld and n=%d rows=%lld", k,
                  (long long)w->mat.cols, n, (long long)w->mat.rows);
     if (m <= 0 || m > 65535) SMX_FAIL(SMX_EINVAL, "smx_weight_matmul: m=%d out of range", m);
+    if (m >= kQgemmMinRows) {
+        // several activation rows: one pass over the weights on the matrix cores; the
+        // activation-part scratch is stream-ordered, so concurrent calls on other streams
+        // cannot share it
+        hipStream_t st = (hipStream_t)stream;
+        uint8_t *xp = nullptr;
+        SMX_HIP(hipMallocAsync((void **)&xp, qgemm_xp_bytes(m, k), st));
+        const hipError_t e = launch_qgemm(w->mat.view(), act_dev, k, m, out_dev, n, xp, st);
+        const hipError_t f = hipFreeAsync(xp, st);
+        SMX_HIP(e);
+        SMX_HIP(f);
+        return SMX_OK;
+    }
     GemvArgs a{};
     a.w = w->mat.view();
     a.x = act_dev;

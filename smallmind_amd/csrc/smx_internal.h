@@ -99,6 +99,12 @@ struct GemvArgs {
 
 hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s);
 
+// Quantized GEMM on the matrix cores for M activation rows (y[M][rows] = x[M][cols] W^T).
+// xp: scratch for the bf16 activation parts, qgemm_xp_bytes(M, cols) bytes.
+size_t qgemm_xp_bytes(int M, int K);
+hipError_t launch_qgemm(const WView &w, const float *x, int64_t x_stride, int M, float *y,
+                        int64_t y_stride, uint8_t *xp, hipStream_t s);
+
 // ---- persistent decode -------------------------------------------------------------------------
 struct LayerDesc {
     WView qkv, o, gu, down;

@@ -75,14 +75,48 @@ def test_q4_0_gemv_benchmark_shapes(gpu, N, K):
 
 @pytest.mark.parametrize("name", list(TYPES))
 def test_matmul_m_rows_equals_gemv_rows(gpu, name):
+    """Below the matrix-core threshold (m < 4) every activation row is one GEMV pass."""
     qt = TYPES[name]
-    N, K, m = 300, 512, 5
+    N, K, m = 300, 512, 3
     W = quantized(qt, (N, K), seed=5)
     X = np.random.default_rng(6).normal(0, 1, (m, K)).astype(np.float32)
     Y = _gemv(qt, W, N, K, X, m=m)
     for r in range(m):
         assert np.array_equal(Y[r], _gemv(qt, W, N, K, X[r])[0])
         assert rel_err(Y[r], O.gemv_f64(qt, W, N, K, X[r])) <= TIGHT
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("m,N,K", [(4, 272, 512), (16, 2560, 2048), (37, 300, 768),
+                                   (64, 1000, 2048), (100, 48, 5632)])
+def test_matmul_matrix_core_path_vs_oracle(gpu, name, m, N, K):
+    """m >= 4 rows: bf16 MFMA on exact integer codes and three-part activations; held to the
+    same bounds as the GEMV, row by row (ragged m and N exercise the tile padding)."""
+    qt = TYPES[name]
+    if K % O.BLOCK_ELEMS[qt]:
+        pytest.skip("row length not a multiple of the block")
+    W = quantized(qt, (N, K), seed=m * 31 + N + K)
+    X = np.random.default_rng(m + K).normal(0, 1, (m, K)).astype(np.float32)
+    X[m // 2] *= 1e-3        # rows of very different magnitude in one tile
+    Y = _gemv(qt, W, N, K, X, m=m)
+    for r in range(m):
+        err = rel_err(Y[r], O.gemv_f64(qt, W, N, K, X[r]))
+        assert err <= TOL and err <= TIGHT, (r, err)
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_matmul_matrix_core_random_bytes(gpu, name):
+    """Every code value and random (finite) scales through the matrix-core path."""
+    qt = TYPES[name]
+    N, K, m = 96, 2048, 20
+    W = random_blocks(qt, N * K // O.BLOCK_ELEMS[qt], 91)
+    X = np.random.default_rng(2).normal(0, 1, (m, K)).astype(np.float32)
+    Y = _gemv(qt, W, N, K, X, m=m)
+    Wf = O.dequant(qt, W, N * K).reshape(N, K).astype(np.float64)
+    for r in range(m):
+        ref = O.gemv_f64(qt, W, N, K, X[r])
+        scale = np.abs(Wf) @ np.abs(X[r].astype(np.float64))
+        assert np.all(np.abs(Y[r] - ref) <= TIGHT * scale + 1e-30), r
 
 
 def test_fused_equals_dequant_then_matmul(gpu):
