@@ -264,6 +264,90 @@ __global__ __launch_bounds__(kThreads) void k_embed(WView w, WView pw, int has_p
     }
 }
 
+// Embedding rows of a token batch: x[t] = emb[tok[t]] (+ pos_emb[pos[t]]), one workgroup per
+// token.
+__global__ __launch_bounds__(kThreads) void k_embed_tokens(WView w, WView pw, int has_pos,
+                                                           const int32_t *__restrict__ tok,
+                                                           const int32_t *__restrict__ pos,
+                                                           float *__restrict__ x, int64_t x_stride)
+{
+    const int t = blockIdx.x;
+    int64_t id = tok[t];
+    if (id < 0 || id >= w.rows) id = 0;   // the host validates tokens; never read out of bounds
+    const int p = pos[t];
+    float *xr = x + (int64_t)t * x_stride;
+    const WView *pp = has_pos ? &pw : nullptr;
+    switch (w.fmt) {
+    case FMT_Q4_0: embed_row<FMT_Q4_0>(w, id, xr, pp, p); break;
+    case FMT_Q8_0: embed_row<FMT_Q8_0>(w, id, xr, pp, p); break;
+    case FMT_Q4_K: embed_row<FMT_Q4_K>(w, id, xr, pp, p); break;
+    case FMT_Q5_K: embed_row<FMT_Q5_K>(w, id, xr, pp, p); break;
+    default: embed_row<FMT_Q6_K>(w, id, xr, pp, p); break;
+    }
+}
+
+// Decode attention for a token batch: token t (its own position and KV cache) x head h.
+template <int HD>
+__global__ __launch_bounds__(AttnCfg<HD>::NT) void k_attention_tokens(
+    const float *__restrict__ q, int64_t q_stride, float *const *__restrict__ kc_tok,
+    float *const *__restrict__ vc_tok, int64_t layer_off, float *__restrict__ out, int64_t out_stride,
+    int n_head, int n_kv_head, int ctx_stride, const int32_t *__restrict__ tok_pos)
+{
+    constexpr int NT = AttnCfg<HD>::NT;
+    extern __shared__ float4 smem4[];
+    __shared__ AttnSmem<HD, NT> sm;
+    const int b = blockIdx.x, t = blockIdx.y;
+    const int h = (n_head % 8 == 0) ? (b % 8) * (n_head / 8) + b / 8 : b;
+    const int kvh = h / (n_head / n_kv_head);
+    const int n_pos = tok_pos[t] + 1;
+    const int64_t off = layer_off + (int64_t)kvh * ctx_stride * HD;
+    attention_head<HD, NT, AttnCfg<HD>::U>(q + (int64_t)t * q_stride + (int64_t)h * HD, kc_tok[t] + off,
+                                           vc_tok[t] + off, out + (int64_t)t * out_stride + (int64_t)h * HD,
+                                           n_pos, ctx_stride, (float *)smem4, sm);
+}
+
+// Argmax of each row of logits [M][n] (lowest index on ties); with `tok_arr`, appends the
+// token to row t's session token array at tok_pos[t] + 1 and advances tok_pos[t]; tok_next
+// receives the token for the next step.
+__global__ __launch_bounds__(1024) void k_argmax_rows(const float *__restrict__ x, int n, int64_t stride,
+                                                      int32_t *__restrict__ tok_next,
+                                                      int32_t *__restrict__ tok_pos,
+                                                      int32_t *const *__restrict__ tok_arr)
+{
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    const float *xr = x + (int64_t)blockIdx.x * stride;
+    float best = -INFINITY;
+    int idx = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = xr[i];
+        if (v > best) { best = v; idx = i; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (ov > best || (ov == best && oi < idx)) { best = ov; idx = oi; }
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { bv[w] = best; bi[w] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        best = bv[0];
+        idx = bi[0];
+        for (int i = 1; i < (int)(blockDim.x >> 6); i++)
+            if (bv[i] > best || (bv[i] == best && bi[i] < idx)) { best = bv[i]; idx = bi[i]; }
+        if (idx == 0x7FFFFFFF) idx = 0;
+        const int t = blockIdx.x;
+        tok_next[t] = idx;
+        if (tok_arr) {
+            const int p = tok_pos[t];
+            tok_arr[t][p + 1] = idx;
+            tok_pos[t] = p + 1;
+        }
+    }
+}
+
 unsigned grid_for(int64_t n, int t = kThreads) { return (unsigned)((n + t - 1) / t); }
 
 }  // namespace
@@ -357,6 +441,51 @@ hipError_t launch_embed(const WView &tok, const WView *posw, const int32_t *toke
 {
     WView pw = posw ? *posw : tok;
     hipLaunchKernelGGL(k_embed, dim3(1), dim3(kThreads), 0, s, tok, pw, posw ? 1 : 0, tokens, pos, x);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_tokens(const WView &tok, const WView *posw, const int32_t *ids,
+                               const int32_t *pos, float *x, int64_t x_stride, int M, hipStream_t s)
+{
+    WView pw = posw ? *posw : tok;
+    hipLaunchKernelGGL(k_embed_tokens, dim3(M), dim3(kThreads), 0, s, tok, pw, posw ? 1 : 0, ids, pos, x, x_stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_tokens(const float *q, int64_t q_stride, float *const *kc_tok,
+                                   float *const *vc_tok, int64_t layer_off, float *out,
+                                   int64_t out_stride, int n_head, int n_kv_head, int hd,
+                                   int ctx_stride, const int32_t *tok_pos, int M, hipStream_t s)
+{
+    const size_t lds = (size_t)ctx_stride * 4;
+    const void *fn = nullptr;
+    switch (hd) {
+    case 16: fn = (const void *)k_attention_tokens<16>; break;
+    case 32: fn = (const void *)k_attention_tokens<32>; break;
+    case 64: fn = (const void *)k_attention_tokens<64>; break;
+    case 128: fn = (const void *)k_attention_tokens<128>; break;
+    default: return hipErrorInvalidValue;
+    }
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    const dim3 grid((unsigned)n_head, (unsigned)M);
+#define SMX_ATT_T(HD) hipLaunchKernelGGL(k_attention_tokens<HD>, grid, dim3(AttnCfg<HD>::NT), lds, s, q, q_stride, kc_tok, vc_tok, layer_off, out, out_stride, n_head, n_kv_head, ctx_stride, tok_pos)
+    switch (hd) {
+    case 16: SMX_ATT_T(16); break;
+    case 32: SMX_ATT_T(32); break;
+    case 64: SMX_ATT_T(64); break;
+    default: SMX_ATT_T(128); break;
+    }
+#undef SMX_ATT_T
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_rows(const float *x, int n, int64_t stride, int M, int32_t *tok_next,
+                              int32_t *tok_pos, int32_t *const *tok_arr, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_argmax_rows, dim3(M), dim3(1024), 0, s, x, n, stride, tok_next, tok_pos, tok_arr);
     return hipGetLastError();
 }
 

@@ -218,12 +218,62 @@ template <> struct QW<FMT_Q6_K> {
 constexpr uint4 kZero4 = {0u, 0u, 0u, 0u};
 constexpr uint32_t kOnes = 0x3F803F80u;   // bf16 1.0 pair
 
-template <int F, int RT, int TT>
-__global__ __launch_bounds__(256) void k_qgemm(WView w, const uint8_t *__restrict__ xp, int M,
-                                               float *__restrict__ y, int64_t y_stride)
+// Epilogue of one output value per (token, weight row); all lanes of the wave must call it
+// (adjacent weight rows are exchanged with DPP for the paired SwiGLU / RoPE epilogues).
+__device__ __forceinline__ void qgemm_epilogue(const QgemmArgs &a, float v, uint32_t row, int tok, bool live)
+{
+    const uint32_t N = (uint32_t)a.w.rows;
+    if (a.bias && row < N) v = v + a.bias[row];
+    // value of the neighbouring weight row (lane li ^ 1 holds row ^ 1)
+    const float nb = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    if (!live || row >= N || tok >= a.M) return;
+    float *yr = a.y + (int64_t)tok * a.y_stride;
+    switch (a.epi) {
+    case EPI_STORE: yr[row] = v; break;
+    case EPI_RESID: yr[row] = yr[row] + v; break;
+    case EPI_GELU: yr[row] = gelu_pade(v); break;
+    case EPI_SILU:
+        // rows interleave gate / up: out[i] = silu(gate_i) * up_i
+        if (!(row & 1)) yr[row >> 1] = silu_mul(v, nb);
+        break;
+    case EPI_QKV: {
+        if (row & 1) break;
+        const int d = a.d_model, kv = a.kv_dim, hd = a.head_dim, r = (int)row;
+        const int pos = a.tok_pos[tok];
+        float v0 = v, v1 = nb;
+        if (a.use_rope && r < d + kv) {
+            const int pair = ((r < d ? r : r - d) % hd) / 2, half = hd / 2;
+            const float c = a.rope_cos[(int64_t)pos * half + pair], sn = a.rope_sin[(int64_t)pos * half + pair];
+            const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;   // RotaryEmbedding.cs:115-116
+            v0 = t0 - t1;
+            v1 = t2 + t3;
+        }
+        if (r < d) {
+            yr[r] = v0;
+            yr[r + 1] = v1;
+        } else if (r < d + kv) {
+            float *dst = a.kc_tok[tok] + a.layer_off + (int64_t)(r - d) * a.ctx_stride + pos;
+            dst[0] = v0;
+            dst[a.ctx_stride] = v1;
+        } else {
+            const int vr = r - d - kv;
+            float *dst = a.vc_tok[tok] + a.layer_off + ((int64_t)(vr / hd) * a.ctx_stride + pos) * hd + (vr % hd);
+            dst[0] = v0;
+            dst[1] = v1;
+        }
+        break;
+    }
+    default: break;
+    }
+}
+
+template <int F, int RT, int TT, int NW, int SB>
+__global__ __launch_bounds__(64 * NW) void k_qgemm(QgemmArgs a)
 {
     using Q = QW<F>;
-    constexpr int NW = 4;
+    const WView &w = a.w;
+    const uint8_t *__restrict__ xp = a.xp;
+    const int M = a.M;
     __shared__ f32x4 s_part[NW - 1][RT * TT][64];
     const int wv = wave_id();
     const int lane = lane_id();
@@ -251,77 +301,73 @@ __global__ __launch_bounds__(256) void k_qgemm(WView w, const uint8_t *__restric
                                     : make_uint4(kOnes, kOnes, kOnes, kOnes);
     const uint4 ones_b = g >= 2 ? make_uint4(kOnes, kOnes, kOnes, kOnes) : kZero4;
 
-    // one sub-block ahead: raw weight words and activation parts of the next sub-block are in
-    // flight while the current one is multiplied
-    RawQ raw[RT];
-    uint4 xa[TT][3];
-    auto load = [&](int s, RawQ *rq, uint4 (*xq)[3]) {
+    // Wave wv takes sub-blocks wv, wv + NW, ...; SB of them at a time, all of whose loads (raw
+    // weight words and activation parts) are issued before any is consumed.
+    for (int s0 = wv; s0 < nsb; s0 += NW * SB) {
+        RawQ raw[SB][RT];
+        uint4 xa[SB][TT][3];
 #pragma unroll
-        for (int t = 0; t < TT; t++) {
-            const int tt = tt0 + t < ntt ? tt0 + t : ntt - 1;
+        for (int u = 0; u < SB; u++) {
+            const int s = s0 + u * NW < nsb ? s0 + u * NW : nsb - 1;
 #pragma unroll
-            for (int p = 0; p < 3; p++)
-                xq[t][p] = *(const uint4 *)(xp + (((size_t)tt * nsb + s) * 3 + p) * 1024 + lane * 16);
-        }
+            for (int t = 0; t < TT; t++) {
+                const int tt = tt0 + t < ntt ? tt0 + t : ntt - 1;
 #pragma unroll
-        for (int r = 0; r < RT; r++) rq[r] = Q::load(w, wrow[r], s, g);
-    };
-    if (wv < nsb) load(wv, raw, xa);
-    for (int s = wv; s < nsb; s += NW) {
-        RawQ rawn[RT];
-        uint4 xan[TT][3];
-        const bool more = s + NW < nsb;
-        if (more) load(s + NW, rawn, xan);
-        uint4 wc[RT];
-        Scl sc[RT];
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-            wc[r] = Q::codes(raw[r], g);
-            sc[r] = Q::scale(raw[r], s);
-        }
-        // sum(x) per token (and per half for Q6_K): the same for every weight row
-#pragma unroll
-        for (int t = 0; t < TT; t++) {
-            f32x4 sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int p = 0; p < 3; p++) {
-                sa = mfma(xa[t][p], ones_a, sa);
-                if constexpr (Q::kHalves) sb = mfma(xa[t][p], ones_b, sb);
+                for (int p = 0; p < 3; p++)
+                    xa[u][t][p] = *(const uint4 *)(xp + (((size_t)tt * nsb + s) * 3 + p) * 1024 + lane * 16);
             }
 #pragma unroll
+            for (int r = 0; r < RT; r++) raw[u][r] = Q::load(w, wrow[r], s, g);
+        }
+        // keep the whole batch of loads ahead of the first use
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            const int s = s0 + u * NW;
+            const float ok = s < nsb ? 1.0f : 0.0f;   // past the end: clamped duplicate, adds 0
+            uint4 wc[RT];
+            Scl sc[RT];
+#pragma unroll
             for (int r = 0; r < RT; r++) {
-                if constexpr (Q::kHalves) {
-                    const uint4 ca = g < 2 ? wc[r] : kZero4, cb = g >= 2 ? wc[r] : kZero4;
-                    f32x4 da = {0.0f, 0.0f, 0.0f, 0.0f}, db = {0.0f, 0.0f, 0.0f, 0.0f};
+                wc[r] = Q::codes(raw[u][r], g);
+                sc[r] = Q::scale(raw[u][r], s);
+            }
+            // sum(x) per token (and per half for Q6_K): the same for every weight row
 #pragma unroll
-                    for (int p = 0; p < 3; p++) {
-                        da = mfma(xa[t][p], ca, da);
-                        db = mfma(xa[t][p], cb, db);
+            for (int t = 0; t < TT; t++) {
+                f32x4 sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int p = 0; p < 3; p++) {
+                    sa = mfma(xa[u][t][p], ones_a, sa);
+                    if constexpr (Q::kHalves) sb = mfma(xa[u][t][p], ones_b, sb);
+                }
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    if constexpr (Q::kHalves) {
+                        const uint4 ca = g < 2 ? wc[r] : kZero4, cb = g >= 2 ? wc[r] : kZero4;
+                        f32x4 da = {0.0f, 0.0f, 0.0f, 0.0f}, db = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int p = 0; p < 3; p++) {
+                            da = mfma(xa[u][t][p], ca, da);
+                            db = mfma(xa[u][t][p], cb, db);
+                        }
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            acc[r][t][i] += ok * (sc[r].sc * (da[i] - Q::kOff * sa[i]) + sc[r].sc2 * (db[i] - Q::kOff * sb[i]));
+                    } else {
+                        f32x4 dc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int p = 0; p < 3; p++) dc = mfma(xa[u][t][p], wc[r], dc);
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            acc[r][t][i] += ok * (sc[r].sc * (dc[i] - Q::kOff * sa[i]) - sc[r].m * sa[i]);
                     }
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        acc[r][t][i] += sc[r].sc * (da[i] - Q::kOff * sa[i]) + sc[r].sc2 * (db[i] - Q::kOff * sb[i]);
-                } else {
-                    f32x4 dc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int p = 0; p < 3; p++) dc = mfma(xa[t][p], wc[r], dc);
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        acc[r][t][i] += sc[r].sc * (dc[i] - Q::kOff * sa[i]) - sc[r].m * sa[i];
                 }
             }
         }
-        if (more) {
-#pragma unroll
-            for (int r = 0; r < RT; r++) raw[r] = rawn[r];
-#pragma unroll
-            for (int t = 0; t < TT; t++)
-#pragma unroll
-                for (int p = 0; p < 3; p++) xa[t][p] = xan[t][p];
-        }
     }
 
-    // sum the four waves' partial tiles in a fixed order; wave 0 stores
+    // sum the NW waves' partial tiles in a fixed order; wave 0 stores
     if (wv > 0) {
 #pragma unroll
         for (int r = 0; r < RT; r++)
@@ -342,12 +388,8 @@ __global__ __launch_bounds__(256) void k_qgemm(WView w, const uint8_t *__restric
                 for (int i = 0; i < 4; i++) v[i] += o[i];
             }
             const uint32_t row = row_base + 16 * r + li;
-            if (row >= N) continue;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int tok = (tt0 + t) * 16 + 4 * g + i;
-                if (tok < M) y[(int64_t)tok * y_stride + row] = v[i];
-            }
+            for (int i = 0; i < 4; i++) qgemm_epilogue(a, v[i], row, (tt0 + t) * 16 + 4 * g + i, true);
         }
 }
 
@@ -360,92 +402,140 @@ __device__ __forceinline__ uint32_t bf16_rne(float f)
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-__global__ __launch_bounds__(256) void k_qprep(const float *__restrict__ x, int64_t x_stride, int M,
-                                               int K, uint8_t *__restrict__ xp)
+// One workgroup per token (rows M..Mp-1 of the last tile are zero): the norm statistic of the
+// row (RMSNorm: RMSNormOps.cs:114; LayerNorm: LayerNormOps.cs:92-119), the normalised value in
+// the reference's operation order (gamma * (x * invRms); fma(gamma, (x - mean) * invStd, beta)),
+// then its three bf16 parts at Xp[m/16][s][p][g][m%16][perm].
+__global__ __launch_bounds__(256) void k_qprep(const float *__restrict__ x, int64_t x_stride, int M, int K,
+                                               int pro, const float *__restrict__ gamma,
+                                               const float *__restrict__ beta, float eps,
+                                               uint8_t *__restrict__ xp)
 {
-    // one thread per (token, sub-block, group): 8 elements
-    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int nsb = K >> 5;
-    const int64_t Mp = ((int64_t)M + 15) & ~(int64_t)15;
-    if (id >= Mp * nsb * 4) return;
-    const int g = (int)(id & 3);
-    const int64_t r = id >> 2;
-    const int s = (int)(r % nsb);
-    const int m = (int)(r / nsb);
-    float v[8];
-    if (m < M) {
-        const float4 *src = (const float4 *)(x + (int64_t)m * x_stride + 32 * s + 8 * g);
-        const float4 a = src[0], b = src[1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
+    __shared__ float red[16];
+    const int m = blockIdx.x;
+    const int nsb = K >> 5, items = K >> 3;   // item = 8 elements (sub-block s, group g)
+    const float *xr = x + (int64_t)m * x_stride;
+    const bool live = m < M;
+    float sc = 1.0f, mean = 0.0f;
+    if (live && pro == PRO_RMS) {
+        float ss = 0.0f;
+        for (int i = threadIdx.x; i < items; i += 256) {
+            const float4 a = ((const float4 *)xr)[2 * i], b = ((const float4 *)xr)[2 * i + 1];
+            float q;
+            q = a.x * a.x; ss += q; q = a.y * a.y; ss += q; q = a.z * a.z; ss += q; q = a.w * a.w; ss += q;
+            q = b.x * b.x; ss += q; q = b.y * b.y; ss += q; q = b.z * b.z; ss += q; q = b.w * b.w; ss += q;
+        }
+        ss = block_sum<4>(ss, red);
+        sc = 1.0f / sqrtf(ss / (float)K + eps);
+    } else if (live && pro == PRO_LN) {
+        float t = 0.0f;
+        for (int i = threadIdx.x; i < items; i += 256) {
+            const float4 a = ((const float4 *)xr)[2 * i], b = ((const float4 *)xr)[2 * i + 1];
+            t += a.x; t += a.y; t += a.z; t += a.w; t += b.x; t += b.y; t += b.z; t += b.w;
+        }
+        mean = block_sum<4>(t, red) / (float)K;
+        float sq = 0.0f;
+        for (int i = threadIdx.x; i < items; i += 256) {
+            const float4 a = ((const float4 *)xr)[2 * i], b = ((const float4 *)xr)[2 * i + 1];
+            const float e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = 0.0f;
-    }
-    uint32_t part[3][8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float f = v[i];
-        const uint32_t h = bf16_rne(f);
-        const float r1 = f - __uint_as_float(h << 16);
-        const uint32_t mm = bf16_rne(r1);
-        const float r2 = r1 - __uint_as_float(mm << 16);
-        part[0][i] = h;
-        part[1][i] = mm;
-        part[2][i] = bf16_rne(r2);
+            for (int k = 0; k < 8; k++) { const float dd = e[k] - mean; const float q = dd * dd; sq += q; }
+        }
+        sq = block_sum<4>(sq, red);
+        sc = 1.0f / sqrtf(sq / (float)K + eps);
     }
     const int tt = m >> 4, t = m & 15;
+    for (int i = threadIdx.x; i < items; i += 256) {
+        const int s = i >> 2, g = i & 3;
+        float v[8];
+        if (live) {
+            const float4 a = ((const float4 *)xr)[2 * i], b = ((const float4 *)xr)[2 * i + 1];
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+            if (pro == PRO_RMS) {
+                const float4 ga = ((const float4 *)gamma)[2 * i], gb = ((const float4 *)gamma)[2 * i + 1];
+                const float gg[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
 #pragma unroll
-    for (int p = 0; p < 3; p++) {
-        // pair q = (element q, element q + 4)
-        uint4 o;
-        o.x = part[p][0] | (part[p][4] << 16);
-        o.y = part[p][1] | (part[p][5] << 16);
-        o.z = part[p][2] | (part[p][6] << 16);
-        o.w = part[p][3] | (part[p][7] << 16);
-        *(uint4 *)(xp + (((size_t)tt * nsb + s) * 3 + p) * 1024 + (g * 16 + t) * 16) = o;
+                for (int k = 0; k < 8; k++) v[k] = gg[k] * (v[k] * sc);
+            } else if (pro == PRO_LN) {
+                const float4 ga = ((const float4 *)gamma)[2 * i], gb = ((const float4 *)gamma)[2 * i + 1];
+                const float4 ba = ((const float4 *)beta)[2 * i], bb = ((const float4 *)beta)[2 * i + 1];
+                const float gg[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+                const float be[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+                for (int k = 0; k < 8; k++) v[k] = __builtin_fmaf(gg[k], (v[k] - mean) * sc, be[k]);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = 0.0f;
+        }
+        uint32_t part[3][8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float f = v[k];
+            const uint32_t h = bf16_rne(f);
+            const float r1 = f - __uint_as_float(h << 16);
+            const uint32_t mm = bf16_rne(r1);
+            const float r2 = r1 - __uint_as_float(mm << 16);
+            part[0][k] = h;
+            part[1][k] = mm;
+            part[2][k] = bf16_rne(r2);
+        }
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            // pair q = (element q, element q + 4)
+            uint4 o;
+            o.x = part[p][0] | (part[p][4] << 16);
+            o.y = part[p][1] | (part[p][5] << 16);
+            o.z = part[p][2] | (part[p][6] << 16);
+            o.w = part[p][3] | (part[p][7] << 16);
+            *(uint4 *)(xp + (((size_t)tt * nsb + s) * 3 + p) * 1024 + (g * 16 + t) * 16) = o;
+        }
     }
 }
 
-template <int F, int RT, int TT>
-hipError_t launch_frt(const WView &w, const uint8_t *xp, int M, float *y, int64_t ys, hipStream_t s)
+template <int F, int RT, int TT, int NW, int SB>
+hipError_t launch_frt(const QgemmArgs &a, hipStream_t s)
 {
-    const dim3 grid((unsigned)((w.rows + 16 * RT - 1) / (16 * RT)), (unsigned)(((M + 15) / 16 + TT - 1) / TT));
-    hipLaunchKernelGGL((k_qgemm<F, RT, TT>), grid, dim3(256), 0, s, w, xp, M, y, ys);
+    const dim3 grid((unsigned)((a.w.rows + 16 * RT - 1) / (16 * RT)), (unsigned)(((a.M + 15) / 16 + TT - 1) / TT));
+    hipLaunchKernelGGL((k_qgemm<F, RT, TT, NW, SB>), grid, dim3(64 * NW), 0, s, a);
     return hipGetLastError();
 }
 
 template <int F>
-hipError_t launch_f(const WView &w, const uint8_t *xp, int M, float *y, int64_t ys, hipStream_t s)
+hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
 {
-    // Token tiles per workgroup: 4 for prefill-sized M (weights reused across 64 tokens), else
-    // 1; row tiles: enough workgroups to fill the chip.
-    if (M > 32) return launch_frt<F, 1, 4>(w, xp, M, y, ys, s);
-    if (w.rows >= 16 * 4 * 256) return launch_frt<F, 4, 1>(w, xp, M, y, ys, s);
-    if (w.rows >= 16 * 2 * 256) return launch_frt<F, 2, 1>(w, xp, M, y, ys, s);
-    return launch_frt<F, 1, 1>(w, xp, M, y, ys, s);
+    // Up to 16 tokens: one token tile, 16 waves per workgroup splitting K, 4 sub-blocks per
+    // wave in flight.  More tokens: 4 token tiles per workgroup (the weight codes are reused
+    // across 64 tokens), 4 waves, 2 sub-blocks in flight.
+    if (a.M > 16) return launch_frt<F, 1, 4, 4, 2>(a, s);
+    if (a.w.rows >= 16 * 2 * 512) return launch_frt<F, 2, 1, 16, 4>(a, s);
+    return launch_frt<F, 1, 1, 16, 4>(a, s);
 }
 
 }  // namespace
 
 size_t qgemm_xp_bytes(int M, int K) { return (size_t)((M + 15) / 16) * (K / 32) * 3 * 1024; }
 
-hipError_t launch_qgemm(const WView &w, const float *x, int64_t x_stride, int M, float *y,
-                        int64_t y_stride, uint8_t *xp, hipStream_t s)
+hipError_t launch_qgemm(const QgemmArgs &a, const float *x, int64_t x_stride, int pro,
+                        const float *gamma, const float *beta, float eps, hipStream_t s)
 {
-    if (M <= 0 || w.cols % 32 != 0) return hipErrorInvalidValue;
-    if ((uint64_t)w.rows * (uint64_t)w.nb * (uint64_t)fmt_main_bytes(w.fmt) >= (1ull << 32))
+    if (a.M <= 0 || a.w.cols % 32 != 0 || (pro != PRO_NONE && !gamma) || (pro == PRO_LN && !beta))
         return hipErrorInvalidValue;
-    const int K = (int)w.cols;
-    const int64_t threads = (int64_t)((M + 15) / 16 * 16) * (K / 32) * 4;
-    hipLaunchKernelGGL(k_qprep, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, x, x_stride, M, K, xp);
+    if ((a.epi == EPI_SILU || a.epi == EPI_QKV) && (a.w.rows & 1)) return hipErrorInvalidValue;
+    if ((uint64_t)a.w.rows * (uint64_t)a.w.nb * (uint64_t)fmt_main_bytes(a.w.fmt) >= (1ull << 32))
+        return hipErrorInvalidValue;
+    const int K = (int)a.w.cols;
+    const unsigned mp = (unsigned)((a.M + 15) / 16 * 16);
+    hipLaunchKernelGGL(k_qprep, dim3(mp), dim3(256), 0, s, x, x_stride, a.M, K, pro, gamma, beta, eps,
+                       (uint8_t *)a.xp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    switch (w.fmt) {
-    case FMT_Q4_0: return launch_f<FMT_Q4_0>(w, xp, M, y, y_stride, s);
-    case FMT_Q8_0: return launch_f<FMT_Q8_0>(w, xp, M, y, y_stride, s);
-    case FMT_Q4_K: return launch_f<FMT_Q4_K>(w, xp, M, y, y_stride, s);
-    case FMT_Q5_K: return launch_f<FMT_Q5_K>(w, xp, M, y, y_stride, s);
-    case FMT_Q6_K: return launch_f<FMT_Q6_K>(w, xp, M, y, y_stride, s);
+    switch (a.w.fmt) {
+    case FMT_Q4_0: return launch_f<FMT_Q4_0>(a, s);
+    case FMT_Q8_0: return launch_f<FMT_Q8_0>(a, s);
+    case FMT_Q4_K: return launch_f<FMT_Q4_K>(a, s);
+    case FMT_Q5_K: return launch_f<FMT_Q5_K>(a, s);
+    case FMT_Q6_K: return launch_f<FMT_Q6_K>(a, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -179,6 +179,18 @@ struct smx_model {
     std::atomic<int> sessions{0};
 };
 
+// Device state for running a batch of tokens through the model at once: a prefill chunk of
+// one session, or one token of each of several sessions stepping in lockstep.  Token t has
+// its own id, position, KV cache (kc/vc: the session's layer-0 cache base) and token array.
+struct TokBatch {
+    int cap = 0, logits_rows = 0;
+    float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
+    uint8_t *xp = nullptr;
+    int32_t *ids = nullptr, *pos = nullptr;
+    float **kc = nullptr, **vc = nullptr;
+    int32_t **tok_arr = nullptr;
+};
+
 struct smx_session {
     smx_model *m = nullptr;
     int max_ctx = 0;
@@ -189,6 +201,7 @@ struct smx_session {
     float *head_val = nullptr;
     int32_t *head_idx = nullptr;
     hipGraphExec_t g_prefill = nullptr, g_decode = nullptr;
+    TokBatch pb;            // prefill chunks on the matrix cores (allocated on first use)
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     std::atomic<int> busy{0};
     // persistent decode (one cooperative launch per prefill / generation)
@@ -475,6 +488,162 @@ int check_abort(smx_session *S)
     return SMX_OK;
 }
 
+void batch_free(TokBatch &B)
+{
+    free_dev(B.x); free_dev(B.q); free_dev(B.att); free_dev(B.h); free_dev(B.logits);
+    free_dev(B.xp); free_dev(B.ids); free_dev(B.pos); free_dev(B.kc); free_dev(B.vc);
+    free_dev(B.tok_arr);
+    B = TokBatch{};
+}
+
+int batch_alloc(const smx_model *m, TokBatch &B, int cap, int logits_rows)
+{
+    const smx_model_config &c = m->cfg;
+    const int64_t maxk = m->hidden > c.d_model ? m->hidden : c.d_model;
+    hipError_t e = hipSuccess;
+    auto A = [&](void **p, size_t n) { if (e == hipSuccess) e = hipMalloc(p, n); };
+    A((void **)&B.x, (size_t)cap * c.d_model * 4);
+    A((void **)&B.q, (size_t)cap * m->nqkv * 4);
+    A((void **)&B.att, (size_t)cap * c.d_model * 4);
+    A((void **)&B.h, (size_t)cap * maxk * 4);
+    A((void **)&B.logits, (size_t)logits_rows * c.vocab * 4);
+    A((void **)&B.xp, qgemm_xp_bytes(cap, (int)maxk));
+    A((void **)&B.ids, (size_t)cap * 4);
+    A((void **)&B.pos, (size_t)cap * 4);
+    A((void **)&B.kc, (size_t)cap * sizeof(float *));
+    A((void **)&B.vc, (size_t)cap * sizeof(float *));
+    A((void **)&B.tok_arr, (size_t)cap * sizeof(int32_t *));
+    if (e != hipSuccess) {
+        batch_free(B);
+        SMX_HIP(e);
+    }
+    B.cap = cap;
+    B.logits_rows = logits_rows;
+    return SMX_OK;
+}
+
+// Runs tokens 0..M-1 of B (ids, pos, kc, vc filled on the device) through every layer on the
+// matrix-core GEMM path, writing K/V into each token's cache; the final norm + head run on rows
+// head_from..M-1 into B.logits.  Same graph as enqueue_step, per token.
+int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_from, hipStream_t s)
+{
+    const smx_model_config &c = m->cfg;
+    const int d = c.d_model, hd = m->hd, Hkv = c.n_kv_head;
+    const int pro = m->llama ? PRO_RMS : PRO_LN;
+    WView posw = m->pos.view();
+    SMX_HIP(launch_embed_tokens(m->tok.view(), m->llama ? nullptr : &posw, B.ids, B.pos, B.x, d, M, s));
+    for (int l = 0; l < c.n_layer; l++) {
+        const Layer &L = m->layers[l];
+        const int64_t layer_off = (int64_t)l * Hkv * ctx_stride * hd;
+        QgemmArgs a{};
+        a.w = L.qkv.view();
+        a.xp = B.xp;
+        a.M = M;
+        a.y = B.q;
+        a.y_stride = m->nqkv;
+        a.bias = L.d_bqkv;
+        a.epi = EPI_QKV;
+        a.d_model = d;
+        a.kv_dim = m->kvdim;
+        a.head_dim = hd;
+        a.use_rope = m->llama ? 1 : 0;
+        a.ctx_stride = ctx_stride;
+        a.layer_off = layer_off;
+        a.kc_tok = B.kc;
+        a.vc_tok = B.vc;
+        a.tok_pos = B.pos;
+        a.rope_cos = m->rope_cos;
+        a.rope_sin = m->rope_sin;
+        SMX_HIP(launch_qgemm(a, B.x, d, pro, L.d_attn_g, L.d_attn_b, c.norm_eps, s));
+        SMX_HIP(launch_attention_tokens(B.q, m->nqkv, B.kc, B.vc, layer_off, B.att, d, c.n_head, Hkv, hd,
+                                        ctx_stride, B.pos, M, s));
+        QgemmArgs o{};
+        o.w = L.o.view();
+        o.xp = B.xp;
+        o.M = M;
+        o.y = B.x;
+        o.y_stride = d;
+        o.bias = L.d_bo;
+        o.epi = EPI_RESID;
+        SMX_HIP(launch_qgemm(o, B.att, d, PRO_NONE, nullptr, nullptr, 0.0f, s));
+        QgemmArgs g{};
+        g.w = L.gu.view();
+        g.xp = B.xp;
+        g.M = M;
+        g.y = B.h;
+        g.y_stride = m->hidden;
+        g.bias = L.d_bgu;
+        g.epi = m->llama ? EPI_SILU : EPI_GELU;
+        SMX_HIP(launch_qgemm(g, B.x, d, pro, L.d_ffn_g, L.d_ffn_b, c.norm_eps, s));
+        QgemmArgs dn{};
+        dn.w = L.down.view();
+        dn.xp = B.xp;
+        dn.M = M;
+        dn.y = B.x;
+        dn.y_stride = d;
+        dn.bias = L.d_bdown;
+        dn.epi = EPI_RESID;
+        SMX_HIP(launch_qgemm(dn, B.h, m->hidden, PRO_NONE, nullptr, nullptr, 0.0f, s));
+    }
+    if (head_from < M) {
+        QgemmArgs hq{};
+        hq.w = m->head.view();
+        hq.xp = B.xp;
+        hq.M = M - head_from;
+        hq.y = B.logits;
+        hq.y_stride = c.vocab;
+        hq.epi = EPI_STORE;
+        SMX_HIP(launch_qgemm(hq, B.x + (int64_t)head_from * d, d, pro, m->d_out_g, m->d_out_b, c.norm_eps, s));
+    }
+    return SMX_OK;
+}
+
+// Tokens of one session per prefill chunk on the matrix-core path.
+constexpr int kPrefillChunk = 256;
+
+// Runs tokens[0..n) of session S at positions p0.. through the model in chunks (K/V written
+// to the session cache).  With want_head, the last token's logits land in S->logits and its
+// argmax is appended to the session token array at p0 + n with the device position advanced
+// to p0 + n, exactly as a decode step leaves them; without, the device position is untouched.
+// Prompts shorter than kPrefillMin tokens go through the per-token decode graph instead.
+constexpr int kPrefillMin = 8;
+int prefill_tokens(smx_session *S, const int32_t *tokens_host, int n, int p0, bool want_head, hipStream_t s)
+{
+    smx_model *m = S->m;
+    if (!S->pb.cap) {
+        int rc = batch_alloc(m, S->pb, kPrefillChunk, 1);
+        if (rc != SMX_OK) return rc;
+        std::vector<float *> kc((size_t)kPrefillChunk, S->kc), vc((size_t)kPrefillChunk, S->vc);
+        std::vector<int32_t *> ta((size_t)kPrefillChunk, S->tokens);
+        SMX_HIP(hipMemcpyAsync(S->pb.kc, kc.data(), kc.size() * sizeof(float *), hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(S->pb.vc, vc.data(), vc.size() * sizeof(float *), hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(S->pb.tok_arr, ta.data(), ta.size() * sizeof(int32_t *), hipMemcpyHostToDevice, s));
+        SMX_HIP(hipStreamSynchronize(s));
+    }
+    TokBatch &B = S->pb;
+    std::vector<int32_t> pos((size_t)kPrefillChunk);
+    for (int i0 = 0; i0 < n; i0 += kPrefillChunk) {
+        const int M = n - i0 < kPrefillChunk ? n - i0 : kPrefillChunk;
+        for (int i = 0; i < M; i++) pos[(size_t)i] = p0 + i0 + i;
+        SMX_HIP(hipMemcpyAsync(B.ids, tokens_host + i0, (size_t)M * 4, hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(B.pos, pos.data(), (size_t)M * 4, hipMemcpyHostToDevice, s));
+        const bool last = i0 + M == n;
+        int rc = run_tokens(m, B, M, S->max_ctx, (want_head && last) ? M - 1 : M, s);
+        if (rc != SMX_OK) return rc;
+        // the host arrays are reused by the next chunk: let this chunk's copies finish
+        SMX_HIP(hipStreamSynchronize(s));
+    }
+    if (want_head) {
+        // token array / position exactly as after a decode step at position p0 + n - 1
+        const int32_t plast = p0 + n - 1;
+        SMX_HIP(hipMemcpyAsync(S->pos, &plast, 4, hipMemcpyHostToDevice, s));
+        SMX_HIP(launch_argmax_rows(B.logits, m->cfg.vocab, m->cfg.vocab, 1, S->amax, S->pos, B.tok_arr, s));
+        SMX_HIP(hipMemcpyAsync(S->logits, B.logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToDevice, s));
+        SMX_HIP(hipStreamSynchronize(s));
+    }
+    return SMX_OK;
+}
+
 struct BusyGuard {
     std::atomic<int> &flag;
     bool ok;
@@ -586,7 +755,14 @@ SMX_API int smx_weight_matmul(const smx_weight *w, const float *act_dev, float *
         hipStream_t st = (hipStream_t)stream;
         uint8_t *xp = nullptr;
         SMX_HIP(hipMallocAsync((void **)&xp, qgemm_xp_bytes(m, k), st));
-        const hipError_t e = launch_qgemm(w->mat.view(), act_dev, k, m, out_dev, n, xp, st);
+        QgemmArgs q{};
+        q.w = w->mat.view();
+        q.xp = xp;
+        q.M = m;
+        q.y = out_dev;
+        q.y_stride = n;
+        q.epi = EPI_STORE;
+        const hipError_t e = launch_qgemm(q, act_dev, k, PRO_NONE, nullptr, nullptr, 0.0f, st);
         const hipError_t f = hipFreeAsync(xp, st);
         SMX_HIP(e);
         SMX_HIP(f);
@@ -1020,6 +1196,8 @@ SMX_API int smx_session_forward(smx_session *S, const int32_t *tokens, int n_tok
     if (S->persistent) {
         rc = run_persistent(S, pos_offset, n_tokens, n_tokens - 1, nullptr);
         if (rc != SMX_OK) return rc;
+    } else if (n_tokens >= kPrefillMin) {
+        if ((rc = prefill_tokens(S, tokens, n_tokens, pos_offset, true, s)) != SMX_OK) return rc;
     } else {
         for (int i = 0; i + 1 < n_tokens; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
         SMX_HIP(hipGraphLaunch(S->g_decode, s));
@@ -1057,6 +1235,10 @@ SMX_API int smx_session_generate(smx_session *S, const int32_t *prompt, int n_pr
     SMX_HIP(hipEventRecord(S->ev[0], s));
     if (S->persistent) {
         if (n_prompt > 1 && (rc = run_persistent(S, 0, n_prompt - 1, n_prompt - 1, nullptr)) != SMX_OK) return rc;
+    } else if (n_prompt - 1 >= kPrefillMin) {
+        if ((rc = prefill_tokens(S, prompt, n_prompt - 1, 0, false, s)) != SMX_OK) return rc;
+        const int32_t plast = n_prompt - 1;
+        SMX_HIP(hipMemcpyAsync(S->pos, &plast, 4, hipMemcpyHostToDevice, s));
     } else {
         for (int i = 0; i + 1 < n_prompt; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
     }
@@ -1111,6 +1293,7 @@ SMX_API int smx_session_destroy(smx_session *S)
     free_dev(S->kc); free_dev(S->vc); free_dev(S->x); free_dev(S->q); free_dev(S->att);
     free_dev(S->h); free_dev(S->logits); free_dev(S->tokens); free_dev(S->pos); free_dev(S->amax);
     free_dev(S->head_val); free_dev(S->head_idx);
+    batch_free(S->pb);
     free_dev(S->d_layers); free_dev(S->bar); free_dev(S->abort_flag); free_dev(S->wg_val);
     free_dev(S->wg_idx); free_dev(S->logits_all); free_dev(S->trace);
     S->m->sessions.fetch_sub(1);

@@ -99,11 +99,32 @@ struct GemvArgs {
 
 hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s);
 
-// Quantized GEMM on the matrix cores for M activation rows (y[M][rows] = x[M][cols] W^T).
-// xp: scratch for the bf16 activation parts, qgemm_xp_bytes(M, cols) bytes.
+// ---- quantized GEMM on the matrix cores for M activation rows (tokens) ------------------------
+// y[M][rows] = norm(x)[M][cols] W^T with the GEMV's prologues and epilogues applied per token.
+// For EPI_QKV every token carries its own position and KV cache (several sessions may share
+// one launch): K/V rows go to kc_tok[t] / vc_tok[t] + layer_off at position tok_pos[t].
+struct QgemmArgs {
+    WView w;
+    const uint8_t *xp;          // activation parts (k_qprep output)
+    int M;
+    float *y;                   // [M][y_stride]
+    int64_t y_stride;
+    const float *bias;          // [rows] or nullptr (interleaved like the rows for EPI_SILU)
+    int epi;                    // EPI_STORE / EPI_RESID / EPI_GELU / EPI_SILU / EPI_QKV
+    // EPI_QKV
+    int d_model, kv_dim, head_dim, use_rope, ctx_stride;
+    int64_t layer_off;
+    float *const *kc_tok;
+    float *const *vc_tok;
+    const int32_t *tok_pos;
+    const float *rope_cos, *rope_sin;
+};
+// Scratch bytes of the activation parts for M tokens of K elements.
 size_t qgemm_xp_bytes(int M, int K);
-hipError_t launch_qgemm(const WView &w, const float *x, int64_t x_stride, int M, float *y,
-                        int64_t y_stride, uint8_t *xp, hipStream_t s);
+// Prepares the parts of the (normalised, PRO_RMS / PRO_LN) activations into xp, then runs the
+// GEMM.  a.xp must point at qgemm_xp_bytes(a.M, cols) bytes of scratch.
+hipError_t launch_qgemm(const QgemmArgs &a, const float *x, int64_t x_stride, int pro,
+                        const float *gamma, const float *beta, float eps, hipStream_t s);
 
 // ---- persistent decode -------------------------------------------------------------------------
 struct LayerDesc {
@@ -169,6 +190,16 @@ hipError_t launch_argmax_pairs(const float *val, const int32_t *idx, int n, int3
 hipError_t launch_embed(const WView &tok, const WView *posw, const int32_t *tokens,
                         const int32_t *pos, float *x, hipStream_t s);
 hipError_t launch_advance(int32_t *pos, hipStream_t s);
+// Token batches (prefill chunks, several sessions in lockstep): embedding rows, decode
+// attention per (token, head) with per-token position and KV cache, argmax per logits row.
+hipError_t launch_embed_tokens(const WView &tok, const WView *posw, const int32_t *ids,
+                               const int32_t *pos, float *x, int64_t x_stride, int M, hipStream_t s);
+hipError_t launch_attention_tokens(const float *q, int64_t q_stride, float *const *kc_tok,
+                                   float *const *vc_tok, int64_t layer_off, float *out,
+                                   int64_t out_stride, int n_head, int n_kv_head, int hd,
+                                   int ctx_stride, const int32_t *tok_pos, int M, hipStream_t s);
+hipError_t launch_argmax_rows(const float *x, int n, int64_t stride, int M, int32_t *tok_next,
+                              int32_t *tok_pos, int32_t *const *tok_arr, hipStream_t s);
 
 // ---- errors --------------------------------------------------------------------------------
 void set_error(const std::string &msg);

@@ -96,12 +96,20 @@ def test_decode_is_deterministic_and_cache_equals_recompute(pairs):
     t1, _ = s.generate_greedy(prompt, 20)
     t2, _ = s.generate_greedy(prompt, 20)
     assert np.array_equal(t1, t2)
-    # KV-cached decode == full recompute of the whole sequence on the GPU
+    # KV-cached decode == full recompute of the whole sequence on the GPU.  The recompute runs
+    # as one prefill chunk on the matrix-core GEMM, the decode on the GEMV: the same fp32
+    # products summed in a different order (a wrong cache entry would differ at O(1)).
     seq = np.concatenate([prompt, t1[:-1]])
     last = s.forward(seq, 0)
     s2 = gm.create_session(64)
     _, _, lg = s2.generate_greedy(prompt, 20, return_logits=True)
-    assert rel_err(last, lg[-1]) < 1e-6
+    assert rel_err(last, lg[-1]) < 1e-4
+    # and the decode path against itself: a 6-token forward (below the prefill-chunk
+    # threshold) replays the decode graph, bit-identical to generate's first decode step
+    s3 = gm.create_session(64)
+    _, _, lg3 = s3.generate_greedy(prompt[:6], 2, return_logits=True)
+    assert np.array_equal(s.forward(prompt[:6], 0), lg3[0])
+    s3.close()
     s.close()
     s2.close()
 
@@ -119,6 +127,32 @@ def test_errors_out_of_range_and_bad_tokens(pairs):
     with pytest.raises(SmxError):
         s.generate_greedy(np.zeros(10, np.int32), 10)
     s.close()
+
+
+def test_prefill_across_chunks_matches_reference():
+    """A 300-token prompt is prefilled as two matrix-core chunks (256 + 44 tokens); the
+    logits of the following decode steps and the greedy tokens must match the reference."""
+    cfg = ModelConfig("llama", 500, 320, 256, 2, 4, 2, 512)
+    om, gm, _ = build_pair(cfg, O.Q4_K, O.Q6_K, O.Q6_K, seed=300)
+    prompt = np.random.default_rng(4).integers(0, cfg.vocab_size, 300).astype(np.int32)
+    s = gm.create_session(320)
+    toks, stats, logits = s.generate_greedy(prompt, 8, return_logits=True)
+    osess = om.session(320)
+    for p, t in enumerate(prompt[:-1]):
+        osess.step(int(t), p, want_logits=False)
+    tok = int(prompt[-1])
+    for i in range(8):
+        ref = osess.step(tok, len(prompt) - 1 + i)
+        assert rel_err(logits[i], ref) <= LOGIT_TOL, (i, rel_err(logits[i], ref))
+        assert int(toks[i]) == int(np.argmax(ref)), i
+        tok = int(toks[i])
+    # forward() over the whole sequence (two chunks + head) equals the no-cache reference
+    seq = np.concatenate([prompt, toks[:4]])
+    got = s.forward(seq, 0)
+    full = om.forward_nocache(seq, all_rows=False)
+    assert rel_err(got, full) <= LOGIT_TOL
+    s.close()
+    gm.close()
 
 
 def test_full_size_llama_q4k_short_prompt():
