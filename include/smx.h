@@ -183,6 +183,16 @@ SMX_API int smx_session_forward(smx_session *s, const int32_t *tokens, int n_tok
  * out_tokens (host, n_new).  logits_out (host, n_new*vocab) may be NULL. */
 SMX_API int smx_session_generate(smx_session *s, const int32_t *prompt, int n_prompt, int n_new,
                                  int32_t *out_tokens, float *logits_out, smx_gen_stats *stats);
+/* Greedy generation for n_sessions sessions of one model in lockstep: each session's prompt
+ * is prefilled, then every decode step advances all sessions by one token, reading each weight
+ * once per step for all of them (the reference serves sessions one at a time:
+ * BatchedInferenceEngine, InferenceSession.cs:478-546 per session).  prompts holds the prompts
+ * back to back, prompt_lens[i] tokens for session i; out_tokens is [n_sessions][n_new] (host).
+ * The sessions must be distinct, share one model and have the same max_ctx; each ends as
+ * smx_session_generate would leave it.  stats (may be NULL) sums the prefill steps. */
+SMX_API int smx_batch_generate(smx_session *const *sessions, int n_sessions, const int32_t *prompts,
+                               const int32_t *prompt_lens, int n_new, int32_t *out_tokens,
+                               smx_gen_stats *stats);
 /* ResetKVCache (TransformerModel.cs:476-506): next forward starts at position 0. */
 SMX_API int smx_session_reset(smx_session *s);
 SMX_API int smx_session_destroy(smx_session *s);

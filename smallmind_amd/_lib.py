@@ -27,7 +27,8 @@ EXPORTS = [
     "smx_scale_mask_softmax", "smx_attention_decode", "smx_silu_mul", "smx_gelu", "smx_argmax",
     "smx_context_create", "smx_context_destroy", "smx_model_create", "smx_model_upload_tensor",
     "smx_model_finalize", "smx_model_weight_bytes", "smx_model_destroy", "smx_session_create",
-    "smx_session_forward", "smx_session_generate", "smx_session_reset", "smx_session_destroy",
+    "smx_session_forward", "smx_session_generate", "smx_batch_generate", "smx_session_reset",
+    "smx_session_destroy",
 ]
 
 
@@ -106,6 +107,7 @@ def load() -> ctypes.CDLL:
         "smx_session_create": (i32, [vp, i32, pp]),
         "smx_session_forward": (i32, [vp, vp, i32, i32, vp]),
         "smx_session_generate": (i32, [vp, vp, i32, i32, vp, vp, ctypes.POINTER(GenStatsC)]),
+        "smx_batch_generate": (i32, [vp, i32, vp, vp, i32, vp, ctypes.POINTER(GenStatsC)]),
         "smx_session_reset": (i32, [vp]),
         "smx_session_destroy": (i32, [vp]),
     }

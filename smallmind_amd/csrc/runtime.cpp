@@ -15,6 +15,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -1268,6 +1269,131 @@ SMX_API int smx_session_generate(smx_session *S, const int32_t *prompt, int n_pr
         stats->n_prefill_steps = n_prompt - 1;
         stats->n_decode_steps = n_new;
     }
+    return SMX_OK;
+}
+
+// Upper bound on sessions per lockstep batch (one token tile of the GEMM per 16 sessions).
+constexpr int kMaxBatchSessions = 256;
+
+SMX_API int smx_batch_generate(smx_session *const *sessions, int n_sessions, const int32_t *prompts,
+                               const int32_t *prompt_lens, int n_new, int32_t *out_tokens,
+                               smx_gen_stats *stats)
+{
+    if (!sessions || !prompts || !prompt_lens || !out_tokens || n_sessions <= 0 || n_new <= 0)
+        SMX_FAIL(SMX_EINVAL, "smx_batch_generate: bad arguments");
+    if (n_sessions > kMaxBatchSessions)
+        SMX_FAIL(SMX_EINVAL, "smx_batch_generate: %d sessions exceed the limit %d", n_sessions, kMaxBatchSessions);
+    smx_model *m = sessions[0] ? sessions[0]->m : nullptr;
+    if (!m) SMX_FAIL(SMX_EINVAL, "smx_batch_generate: null session");
+    const int max_ctx = sessions[0]->max_ctx;
+    std::vector<int64_t> off((size_t)n_sessions + 1, 0);
+    for (int i = 0; i < n_sessions; i++) {
+        smx_session *S = sessions[i];
+        if (!S) SMX_FAIL(SMX_EINVAL, "smx_batch_generate: null session %d", i);
+        if (S->m != m) SMX_FAIL(SMX_EINVAL, "smx_batch_generate: session %d belongs to another model", i);
+        if (S->max_ctx != max_ctx) SMX_FAIL(SMX_EINVAL, "smx_batch_generate: sessions differ in max_ctx");
+        for (int j = 0; j < i; j++)
+            if (sessions[j] == S) SMX_FAIL(SMX_EINVAL, "smx_batch_generate: session %d listed twice", i);
+        const int n = prompt_lens[i];
+        if (n <= 0) SMX_FAIL(SMX_EINVAL, "smx_batch_generate: empty prompt for session %d", i);
+        if ((int64_t)n + n_new - 1 > max_ctx)
+            SMX_FAIL(SMX_ERANGE, "prompt %d + new tokens %d exceed the session context %d", n, n_new, max_ctx);
+        off[(size_t)i + 1] = off[(size_t)i] + n;
+    }
+    std::vector<std::unique_ptr<BusyGuard>> guards;
+    for (int i = 0; i < n_sessions; i++) {
+        guards.emplace_back(new BusyGuard(sessions[i]->busy));
+        if (!guards.back()->ok) SMX_FAIL(SMX_EBUSY, "smx_batch_generate: session %d in use on another thread", i);
+        int rc = check_tokens(sessions[i], prompts + off[(size_t)i], prompt_lens[i]);
+        if (rc != SMX_OK) return rc;
+    }
+    SMX_HIP(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    const int V = m->cfg.vocab, n = n_sessions;
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    TokBatch D;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int rc = SMX_OK;
+    auto cleanup = [&]() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        batch_free(D);
+        for (hipEvent_t e : ev) if (e) (void)hipEventDestroy(e);
+    };
+#define SMX_BHIP(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { cleanup(); SMX_HIP(e_); } } while (0)
+    for (auto &e : ev) SMX_BHIP(hipEventCreate(&e));
+    // prefill every session's prompt except its last token
+    SMX_BHIP(hipEventRecord(ev[0], s));
+    int64_t n_prefill = 0;
+    for (int i = 0; i < n; i++) {
+        smx_session *S = sessions[i];
+        const int len = prompt_lens[i];
+        SMX_BHIP(hipMemcpyAsync(S->tokens, prompts + off[(size_t)i], (size_t)len * 4, hipMemcpyHostToDevice, s));
+        if (len > 1 && (rc = prefill_tokens(S, prompts + off[(size_t)i], len - 1, 0, false, s)) != SMX_OK) {
+            cleanup();
+            return rc;
+        }
+        n_prefill += len - 1;
+    }
+    SMX_BHIP(hipEventRecord(ev[1], s));
+    // one token per session per step
+    if ((rc = batch_alloc(m, D, n, n)) != SMX_OK) {
+        cleanup();
+        return rc;
+    }
+    {
+        std::vector<int32_t> ids((size_t)n), pos((size_t)n);
+        std::vector<float *> kc((size_t)n), vc((size_t)n);
+        std::vector<int32_t *> ta((size_t)n);
+        for (int i = 0; i < n; i++) {
+            ids[(size_t)i] = prompts[off[(size_t)i] + prompt_lens[i] - 1];
+            pos[(size_t)i] = prompt_lens[i] - 1;
+            kc[(size_t)i] = sessions[i]->kc;
+            vc[(size_t)i] = sessions[i]->vc;
+            ta[(size_t)i] = sessions[i]->tokens;
+        }
+        SMX_BHIP(hipMemcpyAsync(D.ids, ids.data(), (size_t)n * 4, hipMemcpyHostToDevice, s));
+        SMX_BHIP(hipMemcpyAsync(D.pos, pos.data(), (size_t)n * 4, hipMemcpyHostToDevice, s));
+        SMX_BHIP(hipMemcpyAsync(D.kc, kc.data(), (size_t)n * sizeof(float *), hipMemcpyHostToDevice, s));
+        SMX_BHIP(hipMemcpyAsync(D.vc, vc.data(), (size_t)n * sizeof(float *), hipMemcpyHostToDevice, s));
+        SMX_BHIP(hipMemcpyAsync(D.tok_arr, ta.data(), (size_t)n * sizeof(int32_t *), hipMemcpyHostToDevice, s));
+        SMX_BHIP(hipStreamSynchronize(s));
+    }
+    // capture one lockstep step: all layers for the n tokens, head, argmax (appends each
+    // session's token at pos + 1 and advances pos on the device)
+    SMX_BHIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    rc = run_tokens(m, D, n, max_ctx, 0, s);
+    if (rc == SMX_OK) {
+        const hipError_t e = launch_argmax_rows(D.logits, V, V, n, D.ids, D.pos, D.tok_arr, s);
+        if (e != hipSuccess) { set_error(hipGetErrorString(e)); rc = SMX_EDEVICE; }
+    }
+    const hipError_t ce = hipStreamEndCapture(s, &graph);
+    if (rc != SMX_OK) {
+        cleanup();
+        return rc;
+    }
+    SMX_BHIP(ce);
+    SMX_BHIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+    for (int k = 0; k < n_new; k++) SMX_BHIP(hipGraphLaunch(exec, s));
+    SMX_BHIP(hipEventRecord(ev[2], s));
+    for (int i = 0; i < n; i++) {
+        SMX_BHIP(hipMemcpyAsync(out_tokens + (size_t)i * n_new, sessions[i]->tokens + prompt_lens[i],
+                                (size_t)n_new * 4, hipMemcpyDeviceToHost, s));
+        SMX_BHIP(hipMemcpyAsync(sessions[i]->pos, D.pos + i, 4, hipMemcpyDeviceToDevice, s));
+    }
+    SMX_BHIP(hipStreamSynchronize(s));
+    if (stats) {
+        float a = 0.0f, b = 0.0f;
+        SMX_BHIP(hipEventElapsedTime(&a, ev[0], ev[1]));
+        SMX_BHIP(hipEventElapsedTime(&b, ev[1], ev[2]));
+        stats->prefill_ms = a;
+        stats->decode_ms = b;
+        stats->n_prefill_steps = (int32_t)n_prefill;
+        stats->n_decode_steps = n_new;
+    }
+#undef SMX_BHIP
+    cleanup();
     return SMX_OK;
 }
 

@@ -162,6 +162,27 @@ class GpuInferenceSession:
     def reset_kv_cache(self):
         call("smx_session_reset", self._h)
 
+    @staticmethod
+    def generate_greedy_batch(sessions, prompts, max_new_tokens: int):
+        """Greedy generation for several sessions of one model in lockstep (smx_batch_generate):
+        every decode step advances all sessions by one token with one pass over the weights.
+        Returns (tokens [n_sessions][max_new_tokens], stats)."""
+        n = len(sessions)
+        ps = [np.ascontiguousarray(p, dtype=np.int32).reshape(-1) for p in prompts]
+        if len(ps) != n:
+            raise ValueError("one prompt per session")
+        flat = np.concatenate(ps).astype(np.int32)
+        lens = np.array([p.size for p in ps], np.int32)
+        handles = (ctypes.c_void_p * n)(*[s._h.value for s in sessions])
+        toks = np.empty((n, max_new_tokens), np.int32)
+        st = GenStatsC()
+        call("smx_batch_generate", ctypes.cast(handles, ctypes.c_void_p), n,
+             flat.ctypes.data_as(ctypes.c_void_p), lens.ctypes.data_as(ctypes.c_void_p),
+             max_new_tokens, toks.ctypes.data_as(ctypes.c_void_p), ctypes.byref(st))
+        stats = {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
+                 "prefill_steps": st.n_prefill_steps, "decode_steps": st.n_decode_steps}
+        return toks, stats
+
     def close(self):
         if getattr(self, "_h", None) and self._h.value:
             call("smx_session_destroy", self._h)

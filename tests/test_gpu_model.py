@@ -155,6 +155,58 @@ def test_prefill_across_chunks_matches_reference():
     gm.close()
 
 
+@pytest.mark.parametrize("key", ["smollm-q5k", "llama-q4k", "gpt2-q8_0"])
+def test_batch_generate_lockstep_matches_single_sessions_and_reference(pairs, key):
+    """several sessions stepping together (smx_batch_generate) produce, per
+    session, the greedy tokens of the reference run alone; prompts of different lengths, so
+    every step mixes positions."""
+    from smallmind_amd.model import GpuInferenceSession
+    om, gm = _pair(pairs, key)
+    cfg = SMALL[key][0]
+    rng = np.random.default_rng(9)
+    lens = [1, 5, 12, 20, 9, 30, 2, 17, 11, 40, 3, 25, 7, 15, 33, 19, 6]
+    prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.int32) for n in lens]
+    n_new = 24
+    sess = [gm.create_session(96) for _ in lens]
+    toks, stats = GpuInferenceSession.generate_greedy_batch(sess, prompts, n_new)
+    assert toks.shape == (len(lens), n_new) and stats["decode_steps"] == n_new
+    for i, p in enumerate(prompts):
+        osess = om.session(96)
+        for q, t in enumerate(p[:-1]):
+            osess.step(int(t), q, want_logits=False)
+        tok = int(p[-1])
+        for k in range(n_new):
+            ref = osess.step(tok, len(p) - 1 + k)
+            assert int(toks[i, k]) == int(np.argmax(ref)), (i, k)
+            tok = int(toks[i, k])
+    # each session continues where smx_session_generate would leave it: one more step via
+    # forward() at the next position equals the reference
+    s0, p0 = sess[3], prompts[3]
+    nxt = s0.forward(np.array([toks[3, -1]], np.int32), len(p0) + n_new - 1)
+    full = om.forward_nocache(np.concatenate([p0, toks[3]]), all_rows=False)
+    assert rel_err(nxt, full) <= LOGIT_TOL
+    for s in sess:
+        s.close()
+
+
+def test_batch_generate_errors(pairs):
+    from smallmind_amd.model import GpuInferenceSession
+    from smallmind_amd.quantization import SmxError
+    om, gm = _pair(pairs, "llama-q4k")
+    a, b = gm.create_session(32), gm.create_session(64)
+    with pytest.raises(SmxError) as e:          # different max_ctx
+        GpuInferenceSession.generate_greedy_batch([a, b], [np.arange(3), np.arange(3)], 4)
+    assert e.value.code == -1
+    with pytest.raises(SmxError) as e:          # the same session twice
+        GpuInferenceSession.generate_greedy_batch([a, a], [np.arange(3), np.arange(3)], 4)
+    assert e.value.code == -1
+    with pytest.raises(SmxError) as e:          # context overflow
+        GpuInferenceSession.generate_greedy_batch([a], [np.arange(30)], 4)
+    assert e.value.code == -7
+    a.close()
+    b.close()
+
+
 def test_full_size_llama_q4k_short_prompt():
     """configs[2] at full size (22 layers, d=2048, GQA 32/4, ff=5632, V=32000, Q4_K + Q6_K),
     weights drawn and encoded on the device, checked against the oracle on a short prompt."""
