@@ -88,6 +88,51 @@ def c2_gemv_lines():
     return out
 
 
+def other_configs():
+    """configs[0], [3] and [4] measured on the same build: GPT-2-small Q8_0 decode; LLaMA-1.1B
+    Q8_0 with a 4096-token prefill (matrix-core GEMM chunks) then decode at ~4.1K context; and
+    SmolLM-1.7B Q5_K with 16 sessions (256-token prompts, 128 tokens each) in lockstep."""
+    import torch
+
+    from smallmind_amd.model import GpuInferenceSession, GpuTransformerModel
+    from smallmind_amd.synthetic import WORKLOADS, load_synthetic_on_device, prompt_tokens
+    out = {}
+    for key in ("gpt2-small-q8_0", "llama-1.1b-q8_0-4k"):
+        wl = WORKLOADS[key]
+        log(f"other configs: {key}")
+        model = GpuTransformerModel(wl.config)
+        load_synthetic_on_device(model, wl, seed=42, keep_blocks=False)
+        sess = model.create_session(wl.prompt_len + wl.new_tokens)
+        prompt = prompt_tokens(7, wl.prompt_len, wl.config.vocab_size)
+        sess.generate_greedy(prompt, 8)                      # warmup
+        toks, st = sess.generate_greedy(prompt, wl.new_tokens)
+        out[key] = {"prompt_len": wl.prompt_len, "new_tokens": wl.new_tokens,
+                    "prefill_tok_s": round((wl.prompt_len - 1) / (st["prefill_ms"] * 1e-3), 1),
+                    "decode_tok_s": round(wl.new_tokens / (st["decode_ms"] * 1e-3), 1),
+                    "weight_bytes": int(model.weight_bytes())}
+        sess.close()
+        model.close()
+        torch.cuda.synchronize()
+    wl = WORKLOADS["smollm-1.7b-q5_k"]
+    log("other configs: smollm-1.7b-q5_k (16 sessions in lockstep)")
+    model = GpuTransformerModel(wl.config)
+    load_synthetic_on_device(model, wl, seed=42, keep_blocks=False)
+    sess = [model.create_session(wl.prompt_len + wl.new_tokens) for _ in range(wl.sessions)]
+    prompts = [prompt_tokens(100 + i, wl.prompt_len, wl.config.vocab_size) for i in range(wl.sessions)]
+    GpuInferenceSession.generate_greedy_batch(sess, prompts, 8)        # warmup
+    toks, st = GpuInferenceSession.generate_greedy_batch(sess, prompts, wl.new_tokens)
+    out["smollm-1.7b-q5_k"] = {
+        "sessions": wl.sessions, "prompt_len": wl.prompt_len, "new_tokens": wl.new_tokens,
+        "prefill_tok_s": round(st["prefill_steps"] / (st["prefill_ms"] * 1e-3), 1),
+        "decode_tok_s_aggregate": round(wl.sessions * wl.new_tokens / (st["decode_ms"] * 1e-3), 1),
+        "decode_ms_per_step": round(st["decode_ms"] / wl.new_tokens, 4),
+        "weight_bytes": int(model.weight_bytes())}
+    for x in sess:
+        x.close()
+    model.close()
+    return out
+
+
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemv_q4k_11264x2048_pmc.md")
 
 
@@ -150,6 +195,8 @@ def main():
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="time only the dominant GEMV kernel (for rocprofv3 --pmc passes)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the configs[0]/[3]/[4] measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -228,11 +275,13 @@ def main():
         log("timing the configs[1] Q4_0 GEMV shapes")
         out["c2_q4_0_gemv"] = c2_gemv_lines()
     sess.close()
+    model.close()
+    if not args.no_other_configs:
+        out["other_configs"] = other_configs()
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle, one thread)")
         out["cpu_baseline"] = cpu_baseline(kept, wl)
     del kept
-    model.close()
     print(json.dumps(out), flush=True)
 
 
