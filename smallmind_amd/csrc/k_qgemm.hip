@@ -393,6 +393,240 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm(QgemmArgs a)
         }
 }
 
+// ---- LDS-staged variant --------------------------------------------------------------------
+// The lane-per-(row, k-group) operand layout makes direct weight loads touch 16 rows (16 cache
+// lines) per instruction for 4 useful bytes each.  Here every wave copies its weight tile --
+// 16*RT rows x one 256-element super-block -- into its own LDS region with coalesced 16-byte
+// loads (the next super-block's copy in flight while the current one is multiplied), and reads
+// the operand dwords from LDS.  RT row tiles per wave share each activation-part load.
+// Waves of a workgroup take contiguous super-block ranges of K.
+template <int F> struct Stage;
+template <> struct Stage<FMT_Q4_0> { static constexpr int kBytes = 128, kD = 8; };
+template <> struct Stage<FMT_Q8_0> { static constexpr int kBytes = 256, kD = 8; };
+template <> struct Stage<FMT_Q4_K> { static constexpr int kBytes = 144, kD = 0; };
+template <> struct Stage<FMT_Q5_K> { static constexpr int kBytes = 176, kD = 0; };
+template <> struct Stage<FMT_Q6_K> { static constexpr int kBytes = 208, kD = 1; };
+
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const uint32_t *)p; }
+
+// Raw operand words of (tile row, sub-block j of the staged super-block, k-group g) from LDS:
+// `row` points at the row's staged main bytes, `dr` at its staged fp16 scales (packed in
+// dwords).  Staged data is written and read as 32-bit words only, so the compiler cannot
+// treat a narrower read as independent of the staging stores and move it above them.
+template <int F>
+__device__ __forceinline__ RawQ stage_raw(const uint8_t *row, const uint32_t *dr, int j, int g)
+{
+    RawQ r{};
+    if constexpr (F == FMT_Q4_0) {
+        r.v = lds_u32(row + 16 * j + 4 * g);
+        r.d = (dr[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+    } else if constexpr (F == FMT_Q8_0) {
+        r.v = lds_u32(row + 32 * j + 8 * g);
+        r.v2 = lds_u32(row + 32 * j + 8 * g + 4);
+        r.d = (dr[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+    } else if constexpr (F == FMT_Q4_K) {
+        r.h = make_uint4(lds_u32(row), lds_u32(row + 4), lds_u32(row + 8), lds_u32(row + 12));
+        r.v = lds_u32(row + 16 + 16 * j + 4 * g);
+    } else if constexpr (F == FMT_Q5_K) {
+        r.h = make_uint4(lds_u32(row), lds_u32(row + 4), lds_u32(row + 8), lds_u32(row + 12));
+        r.v = lds_u32(row + 48 + 16 * j + 4 * g);
+        r.H = lds_u32(row + 16 + 4 * j);
+    } else {
+        r.v = lds_u32(row + 16 * j + 4 * g);
+        r.H = lds_u32(row + 128 + 8 * j);
+        r.H2 = lds_u32(row + 128 + 8 * j + 4);
+        const uint32_t scw = (lds_u32(row + 192 + 4 * (j >> 1)) >> (16 * (j & 1))) & 0xFFFFu;
+        r.d = (dr[0] & 0xFFFFu) | (scw << 16);
+    }
+    return r;
+}
+
+template <int F, int RT, int TT, int NW>
+__global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
+{
+    using Q = QW<F>;
+    using G = Stage<F>;
+    constexpr int R16 = 16 * RT;
+    constexpr int RS = G::kBytes + 4;                       // row stride: dword pad, odd in dwords
+    constexpr int NPC = (R16 * G::kBytes / 16 + 63) / 64;   // 16-byte pieces per lane
+    // dword accesses below: the byte array must be dword (here 16-byte) aligned
+    __shared__ __align__(16) uint8_t s_w[NW][R16 * RS];
+    __shared__ __align__(16) uint32_t s_d[NW][R16][G::kD > 1 ? G::kD / 2 : 1];
+    __shared__ f32x4 s_part[NW - 1][RT * TT][64];
+    const WView &w = a.w;
+    const uint8_t *__restrict__ xp = a.xp;
+    const int M = a.M;
+    const int wv = wave_id();
+    const int lane = lane_id();
+    const int g = lane >> 4, li = lane & 15;
+    const uint32_t N = (uint32_t)w.rows;
+    const int nsb = (int)(w.cols >> 5), nsup = nsb >> 3;
+    const uint32_t row_base = blockIdx.x * R16;
+    const int tt0 = blockIdx.y * TT;
+    const int ntt = (M + 15) >> 4;
+    const uint32_t row_bytes = (uint32_t)nsup * G::kBytes;
+    // contiguous super-block range of this wave
+    const int per = (nsup + NW - 1) / NW;
+    const int sup0 = wv * per, sup1 = sup0 + per < nsup ? sup0 + per : nsup;
+
+    f32x4 acc[RT][TT];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int t = 0; t < TT; t++) acc[r][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint4 ones_a = Q::kHalves ? (g < 2 ? make_uint4(kOnes, kOnes, kOnes, kOnes) : kZero4)
+                                    : make_uint4(kOnes, kOnes, kOnes, kOnes);
+    const uint4 ones_b = g >= 2 ? make_uint4(kOnes, kOnes, kOnes, kOnes) : kZero4;
+
+    // staging loads of one super-block: piece p -> (row p / (kBytes/16), 16-byte column)
+    uint4 wp[NPC];
+    uint4 dp = kZero4;
+    auto issue = [&](int sup) {
+#pragma unroll
+        for (int k = 0; k < NPC; k++) {
+            const int p = lane + 64 * k;
+            const int row = p / (G::kBytes / 16), col = p % (G::kBytes / 16);
+            uint32_t gr = row_base + (uint32_t)row;
+            gr = gr < N ? gr : N - 1;
+            wp[k] = p < R16 * G::kBytes / 16
+                        ? *(const uint4 *)(w.q + gr * row_bytes + (uint32_t)sup * G::kBytes + 16u * col)
+                        : kZero4;
+        }
+        if constexpr (G::kD == 8) {
+            if (lane < R16) {
+                uint32_t gr = row_base + (uint32_t)lane;
+                gr = gr < N ? gr : N - 1;
+                dp = *(const uint4 *)(w.d + (gr * (uint32_t)nsb + (uint32_t)sup * 8));
+            }
+        } else if constexpr (G::kD == 1) {
+            if (lane < R16) {
+                uint32_t gr = row_base + (uint32_t)lane;
+                gr = gr < N ? gr : N - 1;
+                dp.x = w.d[gr * (uint32_t)nsup + (uint32_t)sup];
+            }
+        }
+    };
+    auto stage = [&]() {
+        // the previous super-block's reads of the tile stay above these stores
+        asm volatile("" ::: "memory");
+        uint8_t *dst = s_w[wv];
+#pragma unroll
+        for (int k = 0; k < NPC; k++) {
+            const int p = lane + 64 * k;
+            if (p < R16 * G::kBytes / 16) {
+                const int row = p / (G::kBytes / 16), col = p % (G::kBytes / 16);
+                uint32_t *o = (uint32_t *)(dst + row * RS + 16 * col);
+                o[0] = wp[k].x;
+                o[1] = wp[k].y;
+                o[2] = wp[k].z;
+                o[3] = wp[k].w;
+            }
+        }
+        if constexpr (G::kD == 8) {
+            if (lane < R16) {
+                uint32_t *o = s_d[wv][lane];
+                o[0] = dp.x; o[1] = dp.y; o[2] = dp.z; o[3] = dp.w;
+            }
+        } else if constexpr (G::kD == 1) {
+            if (lane < R16) s_d[wv][lane][0] = dp.x;
+        }
+        // keep every read of the staged tile below these stores
+        asm volatile("" ::: "memory");
+    };
+
+    if (sup0 < sup1) issue(sup0);
+    for (int sup = sup0; sup < sup1; sup++) {
+        stage();                               // this wave's LDS region only: in-order LDS ops
+        if (sup + 1 < sup1) issue(sup + 1);    // next super-block in flight
+        // XU sub-blocks of activation parts in flight at once (fewer with more token tiles)
+        constexpr int XU = TT == 1 ? 4 : 1;
+#pragma unroll
+        for (int h = 0; h < 8 / XU; h++) {
+            uint4 xa[XU][TT][3];
+#pragma unroll
+            for (int u = 0; u < XU; u++) {
+                const int s = sup * 8 + XU * h + u;
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    const int tt = tt0 + t < ntt ? tt0 + t : ntt - 1;
+#pragma unroll
+                    for (int p = 0; p < 3; p++)
+                        xa[u][t][p] = *(const uint4 *)(xp + (((size_t)tt * nsb + s) * 3 + p) * 1024 + lane * 16);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < XU; u++) {
+                const int j = XU * h + u;
+                uint4 wc[RT];
+                Scl sc[RT];
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    const int row = 16 * r + li;
+                    const RawQ raw = stage_raw<F>(s_w[wv] + row * RS, s_d[wv][row], j, g);
+                    wc[r] = Q::codes(raw, g);
+                    sc[r] = Q::scale(raw, j);
+                }
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    f32x4 sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int p = 0; p < 3; p++) {
+                        sa = mfma(xa[u][t][p], ones_a, sa);
+                        if constexpr (Q::kHalves) sb = mfma(xa[u][t][p], ones_b, sb);
+                    }
+#pragma unroll
+                    for (int r = 0; r < RT; r++) {
+                        if constexpr (Q::kHalves) {
+                            const uint4 ca = g < 2 ? wc[r] : kZero4, cb = g >= 2 ? wc[r] : kZero4;
+                            f32x4 da = {0.0f, 0.0f, 0.0f, 0.0f}, db = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                            for (int p = 0; p < 3; p++) {
+                                da = mfma(xa[u][t][p], ca, da);
+                                db = mfma(xa[u][t][p], cb, db);
+                            }
+#pragma unroll
+                            for (int i = 0; i < 4; i++)
+                                acc[r][t][i] += sc[r].sc * (da[i] - Q::kOff * sa[i]) + sc[r].sc2 * (db[i] - Q::kOff * sb[i]);
+                        } else {
+                            f32x4 dc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                            for (int p = 0; p < 3; p++) dc = mfma(xa[u][t][p], wc[r], dc);
+#pragma unroll
+                            for (int i = 0; i < 4; i++)
+                                acc[r][t][i] += sc[r].sc * (dc[i] - Q::kOff * sa[i]) - sc[r].m * sa[i];
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    // sum the NW waves' partial tiles in a fixed order; wave 0 applies the epilogue
+    if (wv > 0) {
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int t = 0; t < TT; t++) s_part[wv - 1][r * TT + t][lane] = acc[r][t];
+    }
+    __syncthreads();
+    if (wv != 0) return;
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            f32x4 v = acc[r][t];
+#pragma unroll
+            for (int k = 0; k < NW - 1; k++) {
+                const f32x4 o = s_part[k][r * TT + t][lane];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] += o[i];
+            }
+            const uint32_t row = row_base + 16 * r + li;
+#pragma unroll
+            for (int i = 0; i < 4; i++) qgemm_epilogue(a, v[i], row, (tt0 + t) * 16 + 4 * g + i, true);
+        }
+}
+
 // Activation parts: token m, sub-block s, part p -> Xp[m/16][s][p][g][m%16][perm] (bf16).
 // x = hi + mid + lo with hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid), each
 // rounded to nearest even; tokens beyond M (tile padding) are zero.
@@ -501,9 +735,24 @@ hipError_t launch_frt(const QgemmArgs &a, hipStream_t s)
     return hipGetLastError();
 }
 
+template <int F, int RT, int TT, int NW>
+hipError_t launch_st(const QgemmArgs &a, hipStream_t s)
+{
+    const dim3 grid((unsigned)((a.w.rows + 16 * RT - 1) / (16 * RT)), (unsigned)(((a.M + 15) / 16 + TT - 1) / TT));
+    hipLaunchKernelGGL((k_qgemm_st<F, RT, TT, NW>), grid, dim3(64 * NW), 0, s, a);
+    return hipGetLastError();
+}
+
 template <int F>
 hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
 {
+    // Rows of whole 256-element super-blocks: LDS-staged weight tiles (16 or 32 rows per wave;
+    // tall matrices 32).  Up to 16 tokens: one token tile; more: 4 token tiles per workgroup.
+    if (a.w.cols % 256 == 0) {
+        const bool tall = a.w.rows >= 8192;
+        if (a.M > 16) return tall ? launch_st<F, 2, 4, 4>(a, s) : launch_st<F, 1, 4, 8>(a, s);
+        return tall ? launch_st<F, 2, 1, 4>(a, s) : launch_st<F, 1, 1, 8>(a, s);
+    }
     // Up to 16 tokens: one token tile, 16 waves per workgroup splitting K, 4 sub-blocks per
     // wave in flight.  More tokens: 4 token tiles per workgroup (the weight codes are reused
     // across 64 tokens), 4 waves, 2 sub-blocks in flight.
