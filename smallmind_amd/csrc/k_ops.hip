@@ -121,6 +121,186 @@ __global__ __launch_bounds__(AttnCfg<HD>::NT) void k_attention_decode(
                                            n_pos, ctx_stride, (float *)smem4, sm);
 }
 
+// Decode attention split over the whole chip in two launches (the single-workgroup-per-head
+// kernel above streams a head's K and V through one CU).  The kernel boundary between them
+// supplies the exact maximum over all positions that the Pade FastExp needs before any
+// exponential (MathUtils.cs:20-32; MultiHeadAttention.cs:676-844).
+//
+// 1. k_attn_scores: workgroup = (KV head, block of 32 positions).  The block of K
+//    ([HD][32], dimension-major) is staged in LDS once and serves every query head of the
+//    group: thread (position tl, head slot hs) computes q_h . k_t for heads h = hs, hs+8, ...
+//    with the same FMA order as attention_head (dimension 0 first), then multiplies by
+//    1/sqrt(HD).  Scores go to sc_out[head][ctx_stride].
+// 2. k_attn_pv: workgroup = (query head, slice of 16 dimensions).  Each workgroup reads the
+//    head's scores, takes the exact max, FastExp(s - max), the sum (fixed reduction order,
+//    so every slice of a head obtains the same bits), scales by 1/sum, and accumulates
+//    P.V for its slice (V is position-major, so a position's slice is 64 contiguous bytes).
+constexpr int kScorePB = 32;    // positions per score workgroup
+constexpr int kPvSlice = 16;    // dimensions per P.V workgroup
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q, const float *__restrict__ kc,
+                                                     float *__restrict__ sc_out, int n_head, int n_kv_head,
+                                                     int ctx_stride, const int32_t *__restrict__ pos_dev,
+                                                     int n_pos_fixed, int nblk)
+{
+    __shared__ float ks[HD][kScorePB];
+    extern __shared__ float4 qs4[];   // [G][HD / 4]
+    const int G = n_head / n_kv_head, GQ4 = G * HD / 4;
+    const int g = blockIdx.x / nblk, blk = blockIdx.x % nblk;
+    const int t0 = blk * kScorePB;
+    const int tid = threadIdx.x, tl = tid & (kScorePB - 1), hs = tid >> 5;
+    const float *K = kc + (int64_t)g * HD * ctx_stride;
+    const int t = t0 + tl;
+    // The loads do not wait for the position: every column index is clamped into the cache
+    // row (valid memory), and columns at or past n_pos are never stored.
+    const int tc = min(t, ctx_stride - 1);
+    float kr[HD / 8];
+#pragma unroll
+    for (int i = 0; i < HD / 8; i++) kr[i] = K[(int64_t)(hs + 8 * i) * ctx_stride + tc];
+    const float4 *qg = (const float4 *)(q + (int64_t)g * G * HD);
+    float4 qr[2];   // the first 2048 floats of the group's queries
+#pragma unroll
+    for (int i = 0; i < 2; i++) qr[i] = qg[min(tid + 256 * i, GQ4 - 1)];
+    const int n_pos = pos_dev ? ld_uniform(pos_dev) + 1 : n_pos_fixed;
+#pragma unroll
+    for (int i = 0; i < HD / 8; i++) ks[hs + 8 * i][tl] = kr[i];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+        if (tid + 256 * i < GQ4) qs4[tid + 256 * i] = qr[i];
+    for (int i = tid + 512; i < GQ4; i += 256) qs4[i] = qg[i];   // groups beyond 2048 floats
+    if (t0 >= n_pos) return;   // uniform over the workgroup
+    __syncthreads();
+    const float *qs = (const float *)qs4;
+    const float scale = 1.0f / sqrtf((float)HD);   // MultiHeadAttention.cs:686
+    for (int hg = hs; hg < G; hg += 8) {
+        float s = 0.0f;
+#pragma unroll
+        for (int e = 0; e < HD; e++) s = __builtin_fmaf(qs[hg * HD + e], ks[e][tl], s);
+        if (t < n_pos) sc_out[(int64_t)(g * G + hg) * ctx_stride + t] = s * scale;
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ scores, const float *__restrict__ vc,
+                                                 float *__restrict__ out, int n_head, int n_kv_head,
+                                                 int ctx_stride, const int32_t *__restrict__ pos_dev,
+                                                 int n_pos_fixed)
+{
+    constexpr int NS = HD / kPvSlice;   // slices per head
+    constexpr int C4 = kPvSlice / 4;    // float4 columns per slice
+    constexpr int PL = 256 / C4;        // position lanes
+    constexpr int U = 16;               // positions per lane in the first batch
+    constexpr int NSC = 4;              // scores per thread in the first batch
+    extern __shared__ float p[];        // [n_pos]
+    __shared__ float red[4];
+    __shared__ float4 part[4][C4];
+    // Workgroups are dealt to the 8 XCDs round-robin; consecutive (head, slice) indices are
+    // grouped per XCD so that the query heads of one KV head share that XCD's L2.
+    const int T = n_head * NS, b = blockIdx.x;
+    const int L = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
+    const int h = L / NS, slice = L % NS;
+    const int kvh = h / (n_head / n_kv_head);
+    const int tid = threadIdx.x;
+    const int c4 = tid % C4, pl = tid / C4;
+    const float *srow = scores + (int64_t)h * ctx_stride;
+    const char *Vb = (const char *)(vc + (int64_t)kvh * ctx_stride * HD + slice * kPvSlice);
+    auto vload = [&](int j) {
+        return *(const float4 *)(Vb + 4u * ((uint32_t)j * HD + 4u * (uint32_t)c4));
+    };
+    // Every load of the first batch is issued up front, before the position is known, with
+    // its index clamped into the cache row (valid memory; entries at or past n_pos are masked
+    // by selection, never multiplied), so the scores arrive first and the first batch of V
+    // streams in while the softmax is computed.
+    float sv[NSC];
+#pragma unroll
+    for (int u = 0; u < NSC; u++) sv[u] = srow[min(tid + 256 * u, ctx_stride - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    float4 vv[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) vv[u] = vload(min(pl + PL * u, ctx_stride - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    const int n_pos = pos_dev ? ld_uniform(pos_dev) + 1 : n_pos_fixed;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NSC; u++) {
+        const int j = tid + 256 * u;
+        if (j < n_pos) {
+            p[j] = sv[u];
+            mx = fmaxf(mx, sv[u]);
+        }
+    }
+    for (int j = tid + 256 * NSC; j < n_pos; j += 256) {
+        const float v = srow[j];
+        p[j] = v;
+        mx = fmaxf(mx, v);
+    }
+    mx = block_max<4>(mx, red);
+    float sum = 0.0f;
+    for (int j = tid; j < n_pos; j += 256) {
+        const float e = fastexp(p[j] - mx);
+        p[j] = e;
+        sum += e;
+    }
+    sum = block_sum<4>(sum, red);
+    const float inv = 1.0f / sum;
+    for (int j = tid; j < n_pos; j += 256) p[j] = p[j] * inv;
+    __syncthreads();
+
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int j = pl + PL * u;
+        if (j < n_pos) {
+            const float pp = p[j];
+            acc.x = __builtin_fmaf(pp, vv[u].x, acc.x);
+            acc.y = __builtin_fmaf(pp, vv[u].y, acc.y);
+            acc.z = __builtin_fmaf(pp, vv[u].z, acc.z);
+            acc.w = __builtin_fmaf(pp, vv[u].w, acc.w);
+        }
+    }
+    // positions beyond the first batch (n_pos > PL * U)
+    constexpr int U2 = 8;
+    for (int j0 = pl + PL * U; j0 < n_pos; j0 += PL * U2) {
+        float4 v2[U2];
+        float p2[U2];
+#pragma unroll
+        for (int u = 0; u < U2; u++) {
+            const int j = j0 + u * PL;
+            const bool ok = j < n_pos;
+            v2[u] = ok ? vload(j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            p2[u] = ok ? p[j] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < U2; u++) {
+            acc.x = __builtin_fmaf(p2[u], v2[u].x, acc.x);
+            acc.y = __builtin_fmaf(p2[u], v2[u].y, acc.y);
+            acc.z = __builtin_fmaf(p2[u], v2[u].z, acc.z);
+            acc.w = __builtin_fmaf(p2[u], v2[u].w, acc.w);
+        }
+    }
+    // lanes with the same column: butterfly over lane bits C4, 2*C4, ..., 32; then the waves
+#pragma unroll
+    for (int m = C4; m < 64; m <<= 1) {
+        acc.x += __shfl_xor(acc.x, m);
+        acc.y += __shfl_xor(acc.y, m);
+        acc.z += __shfl_xor(acc.z, m);
+        acc.w += __shfl_xor(acc.w, m);
+    }
+    const int w = tid >> 6;
+    if ((tid & 63) < C4) part[w][c4] = acc;
+    __syncthreads();
+    if (tid < C4) {
+        float4 o = part[0][tid];
+#pragma unroll
+        for (int i = 1; i < 4; i++) {
+            const float4 v = part[i][tid];
+            o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+        }
+        ((float4 *)(out + (int64_t)h * HD + slice * kPvSlice))[tid] = o;
+    }
+}
+
 __global__ void k_silu_mul(const float *__restrict__ g, const float *__restrict__ u,
                            float *__restrict__ y, int64_t n)
 {
@@ -404,6 +584,51 @@ hipError_t launch_attention_decode(const float *q, const float *kc, const float 
     case 32: hipLaunchKernelGGL(k_attention_decode<32>, dim3(n_head), dim3(AttnCfg<32>::NT), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
     case 64: hipLaunchKernelGGL(k_attention_decode<64>, dim3(n_head), dim3(AttnCfg<64>::NT), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
     default: hipLaunchKernelGGL(k_attention_decode<128>, dim3(n_head), dim3(AttnCfg<128>::NT), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_split(const float *q, const float *kc, const float *vc, float *out,
+                                  float *scores, int n_head, int n_kv_head, int hd, int ctx_stride,
+                                  const int32_t *pos_dev, int n_pos_fixed, int max_pos, hipStream_t s)
+{
+    if (hd % kPvSlice || hd > 128 || n_head % n_kv_head || max_pos > ctx_stride)
+        return hipErrorInvalidValue;
+    const int G = n_head / n_kv_head;
+    const int nblk = (max_pos + kScorePB - 1) / kScorePB;
+    const size_t q_lds = (size_t)G * hd * 4, p_lds = (size_t)max_pos * 4;
+    if (q_lds > 64 * 1024 || p_lds > 160 * 1024) return hipErrorInvalidValue;
+    const dim3 g1((unsigned)(n_kv_head * nblk)), g2((unsigned)(n_head * (hd / kPvSlice)));
+    const void *fp = nullptr;
+    switch (hd) {
+    case 16: fp = (const void *)k_attn_pv<16>; break;
+    case 32: fp = (const void *)k_attn_pv<32>; break;
+    case 64: fp = (const void *)k_attn_pv<64>; break;
+    default: fp = (const void *)k_attn_pv<128>; break;
+    }
+    if (p_lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(fp, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p_lds);
+        if (e != hipSuccess) return e;
+    }
+    switch (hd) {
+    case 16:
+        hipLaunchKernelGGL(k_attn_scores<16>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, nblk);
+        hipLaunchKernelGGL(k_attn_pv<16>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed);
+        break;
+    case 32:
+        hipLaunchKernelGGL(k_attn_scores<32>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, nblk);
+        hipLaunchKernelGGL(k_attn_pv<32>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed);
+        break;
+    case 64:
+        hipLaunchKernelGGL(k_attn_scores<64>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, nblk);
+        hipLaunchKernelGGL(k_attn_pv<64>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed);
+        break;
+    case 128:
+        hipLaunchKernelGGL(k_attn_scores<128>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, nblk);
+        hipLaunchKernelGGL(k_attn_pv<128>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed);
+        break;
+    default:
+        return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }

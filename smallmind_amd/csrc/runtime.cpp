@@ -197,6 +197,7 @@ struct smx_session {
     int max_ctx = 0;
     float *kc = nullptr, *vc = nullptr;
     float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
+    float *scores = nullptr;   // decode attention scores [n_head][max_ctx]
     int32_t *tokens = nullptr, *pos = nullptr, *amax = nullptr;
     // argmax fused into the head GEMV: per-workgroup partials
     float *head_val = nullptr;
@@ -283,8 +284,8 @@ int enqueue_step(smx_session *S, bool with_head, hipStream_t s)
         a.pos = S->pos;
         SMX_HIP(launch_gemv(a, 1, s));
 
-        SMX_HIP(launch_attention_decode(S->q, a.k_cache, a.v_cache, S->att, c.n_head, Hkv, hd,
-                                        S->max_ctx, S->pos, 0, S->max_ctx, s));
+        SMX_HIP(launch_attention_split(S->q, a.k_cache, a.v_cache, S->att, S->scores, c.n_head, Hkv, hd,
+                                       S->max_ctx, S->pos, 0, S->max_ctx, s));
 
         GemvArgs o{};
         o.w = L.o.view();
@@ -857,8 +858,15 @@ SMX_API int smx_attention_decode(const float *q, const float *kc, const float *v
         SMX_FAIL(SMX_EUNSUPPORTED, "smx_attention_decode: head_dim must be 16, 32, 64 or 128");
     if (n_pos <= 0 || n_pos > ctx_stride || ctx_stride > 40000)
         SMX_FAIL(SMX_EINVAL, "smx_attention_decode: need 1 <= n_pos <= ctx_stride <= 40000");
-    SMX_HIP(launch_attention_decode(q, kc, vc, out, n_head, n_kv_head, head_dim, ctx_stride, nullptr,
-                                    n_pos, n_pos, (hipStream_t)stream));
+    // scores scratch [n_head][ctx_stride], stream-ordered like the caller's work
+    hipStream_t st = (hipStream_t)stream;
+    float *scores = nullptr;
+    SMX_HIP(hipMallocAsync((void **)&scores, (size_t)n_head * ctx_stride * 4, st));
+    const hipError_t e = launch_attention_split(q, kc, vc, out, scores, n_head, n_kv_head, head_dim,
+                                                ctx_stride, nullptr, n_pos, n_pos, st);
+    const hipError_t f = hipFreeAsync(scores, st);
+    SMX_HIP(e);
+    SMX_HIP(f);
     return SMX_OK;
 }
 
@@ -1141,6 +1149,7 @@ SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out)
     A((void **)&S->x, (size_t)c.d_model * 4);
     A((void **)&S->q, (size_t)m->nqkv * 4);
     A((void **)&S->att, (size_t)c.d_model * 4);
+    A((void **)&S->scores, (size_t)c.n_head * max_ctx * 4);
     A((void **)&S->h, maxv * 4);
     A((void **)&S->logits, (size_t)c.vocab * 4);
     A((void **)&S->tokens, (size_t)(max_ctx + 1) * 4);
@@ -1416,7 +1425,7 @@ SMX_API int smx_session_destroy(smx_session *S)
     if (S->g_prefill) (void)hipGraphExecDestroy(S->g_prefill);
     if (S->g_decode) (void)hipGraphExecDestroy(S->g_decode);
     for (hipEvent_t e : S->ev) if (e) (void)hipEventDestroy(e);
-    free_dev(S->kc); free_dev(S->vc); free_dev(S->x); free_dev(S->q); free_dev(S->att);
+    free_dev(S->kc); free_dev(S->vc); free_dev(S->x); free_dev(S->q); free_dev(S->att); free_dev(S->scores);
     free_dev(S->h); free_dev(S->logits); free_dev(S->tokens); free_dev(S->pos); free_dev(S->amax);
     free_dev(S->head_val); free_dev(S->head_idx);
     batch_free(S->pb);

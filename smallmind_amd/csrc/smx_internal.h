@@ -180,6 +180,12 @@ hipError_t launch_attention_decode(const float *q, const float *kc, const float 
                                    int n_head, int n_kv_head, int hd, int ctx_stride,
                                    const int32_t *pos_dev, int n_pos_fixed, int max_pos,
                                    hipStream_t s);
+// Decode attention as two launches spread over the chip: scores per (KV head, position block)
+// into `scores` [n_head][ctx_stride], then softmax + P.V per (head, 16-dimension slice).
+// Positions up to max_pos (<= ctx_stride) are covered; pos_dev (if set) gives n_pos - 1.
+hipError_t launch_attention_split(const float *q, const float *kc, const float *vc, float *out,
+                                  float *scores, int n_head, int n_kv_head, int hd, int ctx_stride,
+                                  const int32_t *pos_dev, int n_pos_fixed, int max_pos, hipStream_t s);
 hipError_t launch_silu_mul(const float *g, const float *u, float *y, int64_t n, hipStream_t s);
 hipError_t launch_gelu(const float *x, float *y, int64_t n, hipStream_t s);
 hipError_t launch_argmax(const float *x, int n, int32_t *out, int32_t *tokens, int32_t *pos,
