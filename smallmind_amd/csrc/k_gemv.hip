@@ -79,14 +79,37 @@ __device__ __forceinline__ void epi_load(const GemvArgs &a, uint32_t row0, uint3
     }
 }
 
+// Lane-indexed pick of one of P wave-uniform values (lanes >= P get the last one).
+template <int P>
+__device__ __forceinline__ float pick(const float *v, int lane)
+{
+    float o = v[P - 1];
+#pragma unroll
+    for (int r = P - 2; r >= 0; r--) o = lane == r ? v[r] : o;
+    return o;
+}
+
+// Epilogue of one row group.  Called by the whole wave: SwiGLU computes its R/2 outputs on
+// lanes 0 .. R/2-1 in parallel (two long-latency exp/divide chains would otherwise run back
+// to back on one lane) and stores them with one instruction; the other epilogues run on lane 0.
 template <int R, int EC>
 __device__ __forceinline__ void epi_store(const GemvArgs &a, const float *t, const EpiIn<R, EC> &e,
-                                          uint32_t row0, uint32_t N, int my)
+                                          uint32_t row0, uint32_t N, int my, int lane)
 {
     float *out = a.out + (int64_t)my * a.out_stride;
     float v[R];
 #pragma unroll
     for (int r = 0; r < R; r++) v[r] = a.bias ? t[r] + e.bias[r] : t[r];
+    if constexpr (EC == EC_SILU) {
+        // rows interleave gate / up: out[i] = silu(gate_i) * up_i
+        float g[R / 2], u[R / 2];
+#pragma unroll
+        for (int p = 0; p < R / 2; p++) { g[p] = v[2 * p]; u[p] = v[2 * p + 1]; }
+        const float y = silu_mul(pick<R / 2>(g, lane), pick<R / 2>(u, lane));
+        if (lane < R / 2 && row0 + 2u * (uint32_t)lane + 1u < N) out[row0 / 2 + (uint32_t)lane] = y;
+        return;
+    }
+    if (lane != 0) return;
     if constexpr (EC == EC_ARGMAX) {
 #pragma unroll
         for (int r = 0; r < R; r++)
@@ -101,11 +124,6 @@ __device__ __forceinline__ void epi_store(const GemvArgs &a, const float *t, con
             else if (epi == EPI_GELU) y = gelu_pade(v[r]);
             out[row0 + r] = y;
         }
-    } else if constexpr (EC == EC_SILU) {
-        // rows interleave gate / up: out[i] = silu(gate_i) * up_i
-#pragma unroll
-        for (int r = 0; r < R; r += 2)
-            if (row0 + r + 1 < N) out[(row0 + r) / 2] = silu_mul(v[r], v[r + 1]);
     } else {
         // rows [Q | K | V]: RoPE on Q and K pairs (RotaryEmbedding.cs:115-116); Q -> out,
         // K -> k_cache [kv_head][head_dim][ctx_stride] (dimension-major), V -> v_cache
@@ -345,7 +363,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
             t[r] = v;
         }
     }
-    if (ws == 0 && lane == 0 && row0 < N) epi_store<R, EC>(a, t, e, row0, N, my);
+    if (ws == 0 && row0 < N) epi_store<R, EC>(a, t, e, row0, N, my, lane);
     if constexpr (EC == EC_ARGMAX) {
         __shared__ float s_bv[4];
         __shared__ int s_bi[4];
