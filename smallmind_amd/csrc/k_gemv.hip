@@ -64,18 +64,27 @@ __device__ __forceinline__ void epi_load(const GemvArgs &a, uint32_t row0, uint3
             if (a.epi == EPI_RESID) e.res[r] = ld_uniform(a.resid + (int64_t)my * a.out_stride + row);
     }
     e.pos = 0;
-    if constexpr (EC == EC_QKV) {
-        e.pos = a.pos ? ld_uniform(a.pos) : a.pos_val;
-        const int half = a.head_dim / 2, d = a.d_model, kv = a.kv_dim;
+    if constexpr (EC == EC_QKV) e.pos = a.pos ? ld_uniform(a.pos) : a.pos_val;
+}
+
+// RoPE table entries of the group's row pairs, loaded once the activation vector is staged.
+// They depend on the position, a scalar load, and go through the vector path on purpose:
+// scalar loads share a counter with LDS operations and return out of order, so one still
+// outstanding would hold up every later LDS wait of the dot products.  Issued after the
+// weights, they are not waited for until the epilogue.
+template <int R, int EC>
+__device__ __forceinline__ void epi_load_rope(const GemvArgs &a, uint32_t row0, EpiIn<R, EC> &e)
+{
+    const int half = a.head_dim / 2, d = a.d_model, kv = a.kv_dim;
+    const int z = opaque_tid() >> 30;   // 0, but lane-varying to the compiler: vector loads
 #pragma unroll
-        for (int p = 0; p < R / 2; p++) {
-            const int row = (int)row0 + 2 * p;
-            int pair = -1;
-            if (a.use_rope && row < d) pair = (row % a.head_dim) / 2;
-            else if (a.use_rope && row < d + kv) pair = ((row - d) % a.head_dim) / 2;
-            e.cs[p] = pair >= 0 ? ld_uniform(a.rope_cos + (int64_t)e.pos * half + pair) : 1.0f;
-            e.sn[p] = pair >= 0 ? ld_uniform(a.rope_sin + (int64_t)e.pos * half + pair) : 0.0f;
-        }
+    for (int p = 0; p < R / 2; p++) {
+        const int row = (int)row0 + 2 * p;
+        int pair = -1;
+        if (a.use_rope && row < d) pair = (row % a.head_dim) / 2;
+        else if (a.use_rope && row < d + kv) pair = ((row - d) % a.head_dim) / 2;
+        e.cs[p] = pair >= 0 ? a.rope_cos[(int64_t)e.pos * half + pair + z] : 1.0f;
+        e.sn[p] = pair >= 0 ? a.rope_sin[(int64_t)e.pos * half + pair + z] : 0.0f;
     }
 }
 
@@ -299,6 +308,8 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
         }
         __syncthreads();
     }
+
+    if constexpr (EC == EC_QKV) epi_load_rope<R, EC>(a, row0, e);
 
     float acc[R];
 #pragma unroll
