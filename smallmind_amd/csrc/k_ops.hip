@@ -141,7 +141,7 @@ constexpr int kPvSlice = 16;    // dimensions per P.V workgroup
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q, const float *__restrict__ kc,
                                                      float *__restrict__ sc_out, int n_head, int n_kv_head,
-                                                     int ctx_stride, const int32_t *__restrict__ pos_dev,
+                                                     int ctx_stride, int sc_stride, const int32_t *__restrict__ pos_dev,
                                                      int n_pos_fixed, int nblk)
 {
     __shared__ float ks[HD][kScorePB];
@@ -177,22 +177,22 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
         float s = 0.0f;
 #pragma unroll
         for (int e = 0; e < HD; e++) s = __builtin_fmaf(qs[hg * HD + e], ks[e][tl], s);
-        if (t < n_pos) sc_out[(int64_t)(g * G + hg) * ctx_stride + t] = s * scale;
+        if (t < n_pos) sc_out[(int64_t)(g * G + hg) * sc_stride + t] = s * scale;
     }
 }
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ scores, const float *__restrict__ vc,
                                                  float *__restrict__ out, int n_head, int n_kv_head,
-                                                 int ctx_stride, const int32_t *__restrict__ pos_dev,
+                                                 int ctx_stride, int sc_stride, const int32_t *__restrict__ pos_dev,
                                                  int n_pos_fixed)
 {
     constexpr int NS = HD / kPvSlice;   // slices per head
     constexpr int C4 = kPvSlice / 4;    // float4 columns per slice
     constexpr int PL = 256 / C4;        // position lanes
-    constexpr int U = 16;               // positions per lane in the first batch
-    constexpr int NSC = 4;              // scores per thread in the first batch
-    extern __shared__ float p[];        // [n_pos]
+    constexpr int U = 16;               // consecutive positions per lane in the first batch
+    constexpr int NB = PL * U;          // positions of the first batch
+    extern __shared__ float p[];        // [n_pos], only for n_pos > NB
     __shared__ float red[4];
     __shared__ float4 part[4][C4];
     // Workgroups are dealt to the 8 XCDs round-robin; consecutive (head, slice) indices are
@@ -203,70 +203,103 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ score
     const int kvh = h / (n_head / n_kv_head);
     const int tid = threadIdx.x;
     const int c4 = tid % C4, pl = tid / C4;
-    const float *srow = scores + (int64_t)h * ctx_stride;
+    const float *srow = scores + (int64_t)h * sc_stride;
     const char *Vb = (const char *)(vc + (int64_t)kvh * ctx_stride * HD + slice * kPvSlice);
     auto vload = [&](int j) {
         return *(const float4 *)(Vb + 4u * ((uint32_t)j * HD + 4u * (uint32_t)c4));
     };
-    // Every load of the first batch is issued up front, before the position is known, with
-    // its index clamped into the cache row (valid memory; entries at or past n_pos are masked
-    // by selection, never multiplied), so the scores arrive first and the first batch of V
-    // streams in while the softmax is computed.
-    float sv[NSC];
+    // Lane pl owns positions j0 .. j0 + U - 1 of the first batch.  Its scores and V rows are
+    // all loaded up front, before the position is known, with indices clamped into the cache
+    // row (valid memory; entries at or past n_pos are dropped by selection, never multiplied),
+    // so the scores arrive first and V streams in while the softmax is computed.
+    const int j0 = pl * U;
+    float sv[U];
 #pragma unroll
-    for (int u = 0; u < NSC; u++) sv[u] = srow[min(tid + 256 * u, ctx_stride - 1)];
+    for (int u = 0; u < U; u += 4) {
+        const int j = min(j0 + u, sc_stride - 4);   // sc_stride is a multiple of 4
+        const float4 t = *(const float4 *)(srow + j);
+        sv[u] = t.x; sv[u + 1] = t.y; sv[u + 2] = t.z; sv[u + 3] = t.w;
+    }
     __builtin_amdgcn_sched_barrier(0);
     float4 vv[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) vv[u] = vload(min(pl + PL * u, ctx_stride - 1));
+    for (int u = 0; u < U; u++) vv[u] = vload(min(j0 + u, ctx_stride - 1));
     __builtin_amdgcn_sched_barrier(0);
     const int n_pos = pos_dev ? ld_uniform(pos_dev) + 1 : n_pos_fixed;
-    float mx = -INFINITY;
+    float pu[U];
+    if (n_pos <= NB) {
+        // Whole softmax in registers.  The C4 = 4 lanes of a position lane form a DPP quad
+        // holding the same positions: lane c4 takes the exact max over its quarter, computes
+        // FastExp for positions j0 + 4*c4 .. +3 and the quad shares the results; the sum runs
+        // over every lane once per position, in the same order in every workgroup of the head.
+        static_assert(C4 == 4 && U == 16, "one quarter of the positions per lane of a quad");
+        float mx = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < NSC; u++) {
-        const int j = tid + 256 * u;
-        if (j < n_pos) {
-            p[j] = sv[u];
-            mx = fmaxf(mx, sv[u]);
+        for (int u = 0; u < U; u++)
+            if (j0 + u < n_pos) mx = fmaxf(mx, sv[u]);
+        mx = block_max<4>(mx, red);
+        float e[4], sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int u = 4 * c4 + k;
+            float sk = sv[0];
+#pragma unroll
+            for (int i = 1; i < U; i++) sk = u == i ? sv[i] : sk;
+            e[k] = j0 + u < n_pos ? fastexp(sk - mx) : 0.0f;
+            sum += e[k];
         }
+        sum = block_sum<4>(sum, red);
+        const float inv = 1.0f / sum;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            e[k] = e[k] * inv;
+            pu[k] = dpp_mov<0x00>(e[k]);        // quad_perm [0,0,0,0]
+            pu[4 + k] = dpp_mov<0x55>(e[k]);    // quad_perm [1,1,1,1]
+            pu[8 + k] = dpp_mov<0xAA>(e[k]);    // quad_perm [2,2,2,2]
+            pu[12 + k] = dpp_mov<0xFF>(e[k]);   // quad_perm [3,3,3,3]
+        }
+    } else {
+        // long contexts: the scores of all positions pass through LDS
+        float mx = -INFINITY;
+        for (int j = tid; j < n_pos; j += 256) {
+            const float v = srow[j];
+            p[j] = v;
+            mx = fmaxf(mx, v);
+        }
+        mx = block_max<4>(mx, red);
+        float sum = 0.0f;
+        for (int j = tid; j < n_pos; j += 256) {
+            const float e = fastexp(p[j] - mx);
+            p[j] = e;
+            sum += e;
+        }
+        sum = block_sum<4>(sum, red);
+        const float inv = 1.0f / sum;
+        for (int j = tid; j < n_pos; j += 256) p[j] = p[j] * inv;
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < U; u++) pu[u] = p[j0 + u];   // j0 + u < NB < n_pos
     }
-    for (int j = tid + 256 * NSC; j < n_pos; j += 256) {
-        const float v = srow[j];
-        p[j] = v;
-        mx = fmaxf(mx, v);
-    }
-    mx = block_max<4>(mx, red);
-    float sum = 0.0f;
-    for (int j = tid; j < n_pos; j += 256) {
-        const float e = fastexp(p[j] - mx);
-        p[j] = e;
-        sum += e;
-    }
-    sum = block_sum<4>(sum, red);
-    const float inv = 1.0f / sum;
-    for (int j = tid; j < n_pos; j += 256) p[j] = p[j] * inv;
-    __syncthreads();
 
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int u = 0; u < U; u++) {
-        const int j = pl + PL * u;
-        if (j < n_pos) {
-            const float pp = p[j];
+        if (j0 + u < n_pos) {
+            const float pp = pu[u];
             acc.x = __builtin_fmaf(pp, vv[u].x, acc.x);
             acc.y = __builtin_fmaf(pp, vv[u].y, acc.y);
             acc.z = __builtin_fmaf(pp, vv[u].z, acc.z);
             acc.w = __builtin_fmaf(pp, vv[u].w, acc.w);
         }
     }
-    // positions beyond the first batch (n_pos > PL * U)
+    // positions beyond the first batch (n_pos > NB)
     constexpr int U2 = 8;
-    for (int j0 = pl + PL * U; j0 < n_pos; j0 += PL * U2) {
+    for (int jb = NB + pl; jb < n_pos; jb += PL * U2) {
         float4 v2[U2];
         float p2[U2];
 #pragma unroll
         for (int u = 0; u < U2; u++) {
-            const int j = j0 + u * PL;
+            const int j = jb + u * PL;
             const bool ok = j < n_pos;
             v2[u] = ok ? vload(j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             p2[u] = ok ? p[j] : 0.0f;
@@ -588,12 +621,15 @@ hipError_t launch_attention_decode(const float *q, const float *kc, const float 
     return hipGetLastError();
 }
 
+size_t attention_scores_floats(int n_head, int max_pos) { return (size_t)n_head * ((max_pos + 3) & ~3); }
+
 hipError_t launch_attention_split(const float *q, const float *kc, const float *vc, float *out,
                                   float *scores, int n_head, int n_kv_head, int hd, int ctx_stride,
                                   const int32_t *pos_dev, int n_pos_fixed, int max_pos, hipStream_t s)
 {
-    if (hd % kPvSlice || hd > 128 || n_head % n_kv_head || max_pos > ctx_stride)
+    if (hd % kPvSlice || hd > 128 || n_head % n_kv_head || max_pos > ctx_stride || max_pos < 1)
         return hipErrorInvalidValue;
+    const int sc_stride = (max_pos + 3) & ~3;
     const int G = n_head / n_kv_head;
     const int nblk = (max_pos + kScorePB - 1) / kScorePB;
     const size_t q_lds = (size_t)G * hd * 4, p_lds = (size_t)max_pos * 4;
@@ -612,20 +648,20 @@ hipError_t launch_attention_split(const float *q, const float *kc, const float *
     }
     switch (hd) {
     case 16:
-        hipLaunchKernelGGL(k_attn_scores<16>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, nblk);
-        hipLaunchKernelGGL(k_attn_pv<16>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed);
+        hipLaunchKernelGGL(k_attn_scores<16>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk);
+        hipLaunchKernelGGL(k_attn_pv<16>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed);
         break;
     case 32:
-        hipLaunchKernelGGL(k_attn_scores<32>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, nblk);
-        hipLaunchKernelGGL(k_attn_pv<32>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed);
+        hipLaunchKernelGGL(k_attn_scores<32>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk);
+        hipLaunchKernelGGL(k_attn_pv<32>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed);
         break;
     case 64:
-        hipLaunchKernelGGL(k_attn_scores<64>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, nblk);
-        hipLaunchKernelGGL(k_attn_pv<64>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed);
+        hipLaunchKernelGGL(k_attn_scores<64>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk);
+        hipLaunchKernelGGL(k_attn_pv<64>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed);
         break;
     case 128:
-        hipLaunchKernelGGL(k_attn_scores<128>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, nblk);
-        hipLaunchKernelGGL(k_attn_pv<128>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed);
+        hipLaunchKernelGGL(k_attn_scores<128>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk);
+        hipLaunchKernelGGL(k_attn_pv<128>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed);
         break;
     default:
         return hipErrorInvalidValue;

@@ -858,10 +858,10 @@ SMX_API int smx_attention_decode(const float *q, const float *kc, const float *v
         SMX_FAIL(SMX_EUNSUPPORTED, "smx_attention_decode: head_dim must be 16, 32, 64 or 128");
     if (n_pos <= 0 || n_pos > ctx_stride || ctx_stride > 40000)
         SMX_FAIL(SMX_EINVAL, "smx_attention_decode: need 1 <= n_pos <= ctx_stride <= 40000");
-    // scores scratch [n_head][ctx_stride], stream-ordered like the caller's work
+    // scores scratch, stream-ordered like the caller's work
     hipStream_t st = (hipStream_t)stream;
     float *scores = nullptr;
-    SMX_HIP(hipMallocAsync((void **)&scores, (size_t)n_head * ctx_stride * 4, st));
+    SMX_HIP(hipMallocAsync((void **)&scores, attention_scores_floats(n_head, n_pos) * 4, st));
     const hipError_t e = launch_attention_split(q, kc, vc, out, scores, n_head, n_kv_head, head_dim,
                                                 ctx_stride, nullptr, n_pos, n_pos, st);
     const hipError_t f = hipFreeAsync(scores, st);
@@ -1149,7 +1149,7 @@ SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out)
     A((void **)&S->x, (size_t)c.d_model * 4);
     A((void **)&S->q, (size_t)m->nqkv * 4);
     A((void **)&S->att, (size_t)c.d_model * 4);
-    A((void **)&S->scores, (size_t)c.n_head * max_ctx * 4);
+    A((void **)&S->scores, attention_scores_floats(c.n_head, max_ctx) * 4);
     A((void **)&S->h, maxv * 4);
     A((void **)&S->logits, (size_t)c.vocab * 4);
     A((void **)&S->tokens, (size_t)(max_ctx + 1) * 4);

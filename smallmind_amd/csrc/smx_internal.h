@@ -181,8 +181,10 @@ hipError_t launch_attention_decode(const float *q, const float *kc, const float 
                                    const int32_t *pos_dev, int n_pos_fixed, int max_pos,
                                    hipStream_t s);
 // Decode attention as two launches spread over the chip: scores per (KV head, position block)
-// into `scores` [n_head][ctx_stride], then softmax + P.V per (head, 16-dimension slice).
-// Positions up to max_pos (<= ctx_stride) are covered; pos_dev (if set) gives n_pos - 1.
+// into `scores` (attention_scores_floats(n_head, max_pos) floats: rows of max_pos rounded up
+// to a multiple of 4), then softmax + P.V per (head, 16-dimension slice).  Positions up to
+// max_pos (<= ctx_stride) are covered; pos_dev (if set) gives n_pos - 1.
+size_t attention_scores_floats(int n_head, int max_pos);
 hipError_t launch_attention_split(const float *q, const float *kc, const float *vc, float *out,
                                   float *scores, int n_head, int n_kv_head, int hd, int ctx_stride,
                                   const int32_t *pos_dev, int n_pos_fixed, int max_pos, hipStream_t s);
