@@ -181,7 +181,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     }
 }
 
-template <int HD>
+template <int HD, int U>
 __global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ scores, const float *__restrict__ vc,
                                                  float *__restrict__ out, int n_head, int n_kv_head,
                                                  int ctx_stride, int sc_stride, const int32_t *__restrict__ pos_dev,
@@ -190,7 +190,8 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ score
     constexpr int NS = HD / kPvSlice;   // slices per head
     constexpr int C4 = kPvSlice / 4;    // float4 columns per slice
     constexpr int PL = 256 / C4;        // position lanes
-    constexpr int U = 16;               // consecutive positions per lane in the first batch
+    // U: consecutive positions per lane in the first batch (sized by the launcher to the
+    // session's context, so the first batch loads no rows past it)
     constexpr int NB = PL * U;          // positions of the first batch
     extern __shared__ float p[];        // [n_pos], only for n_pos > NB
     __shared__ float red[4];
@@ -232,31 +233,32 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ score
         // holding the same positions: lane c4 takes the exact max over its quarter, computes
         // FastExp for positions j0 + 4*c4 .. +3 and the quad shares the results; the sum runs
         // over every lane once per position, in the same order in every workgroup of the head.
-        static_assert(C4 == 4 && U == 16, "one quarter of the positions per lane of a quad");
+        static_assert(C4 == 4 && U % 4 == 0, "one quarter of the positions per lane of a quad");
+        constexpr int UQ = U / 4;
         float mx = -INFINITY;
 #pragma unroll
         for (int u = 0; u < U; u++)
             if (j0 + u < n_pos) mx = fmaxf(mx, sv[u]);
         mx = block_max<4>(mx, red);
-        float e[4], sum = 0.0f;
+        float e[UQ], sum = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int u = 4 * c4 + k;
-            float sk = sv[0];
+        for (int k = 0; k < UQ; k++) {
+            const int u = UQ * c4 + k;
+            float sk = sv[k];
 #pragma unroll
-            for (int i = 1; i < U; i++) sk = u == i ? sv[i] : sk;
+            for (int i = 1; i < 4; i++) sk = c4 == i ? sv[UQ * i + k] : sk;
             e[k] = j0 + u < n_pos ? fastexp(sk - mx) : 0.0f;
             sum += e[k];
         }
         sum = block_sum<4>(sum, red);
         const float inv = 1.0f / sum;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < UQ; k++) {
             e[k] = e[k] * inv;
-            pu[k] = dpp_mov<0x00>(e[k]);        // quad_perm [0,0,0,0]
-            pu[4 + k] = dpp_mov<0x55>(e[k]);    // quad_perm [1,1,1,1]
-            pu[8 + k] = dpp_mov<0xAA>(e[k]);    // quad_perm [2,2,2,2]
-            pu[12 + k] = dpp_mov<0xFF>(e[k]);   // quad_perm [3,3,3,3]
+            pu[k] = dpp_mov<0x00>(e[k]);             // quad_perm [0,0,0,0]
+            pu[UQ + k] = dpp_mov<0x55>(e[k]);        // quad_perm [1,1,1,1]
+            pu[2 * UQ + k] = dpp_mov<0xAA>(e[k]);    // quad_perm [2,2,2,2]
+            pu[3 * UQ + k] = dpp_mov<0xFF>(e[k]);    // quad_perm [3,3,3,3]
         }
     } else {
         // long contexts: the scores of all positions pass through LDS
@@ -621,6 +623,38 @@ hipError_t launch_attention_decode(const float *q, const float *kc, const float 
     return hipGetLastError();
 }
 
+template <int HD, int U>
+hipError_t launch_pv(dim3 g2, size_t p_lds, const float *scores, const float *vc, float *out, int n_head,
+                     int n_kv_head, int ctx_stride, int sc_stride, const int32_t *pos_dev, int n_pos_fixed,
+                     hipStream_t s)
+{
+    const void *fp = (const void *)k_attn_pv<HD, U>;
+    if (p_lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(fp, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p_lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((k_attn_pv<HD, U>), g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride,
+                       sc_stride, pos_dev, n_pos_fixed);
+    return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch_attn_hd(dim3 g1, dim3 g2, size_t q_lds, size_t p_lds, int U, const float *q, const float *kc,
+                          const float *vc, float *out, float *scores, int n_head, int n_kv_head, int ctx_stride,
+                          int sc_stride, const int32_t *pos_dev, int n_pos_fixed, int nblk, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_attn_scores<HD>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride,
+                       sc_stride, pos_dev, n_pos_fixed, nblk);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    switch (U) {
+    case 4: return launch_pv<HD, 4>(g2, p_lds, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, s);
+    case 8: return launch_pv<HD, 8>(g2, p_lds, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, s);
+    case 12: return launch_pv<HD, 12>(g2, p_lds, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, s);
+    default: return launch_pv<HD, 16>(g2, p_lds, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, s);
+    }
+}
+
 size_t attention_scores_floats(int n_head, int max_pos) { return (size_t)n_head * ((max_pos + 3) & ~3); }
 
 hipError_t launch_attention_split(const float *q, const float *kc, const float *vc, float *out,
@@ -635,38 +669,14 @@ hipError_t launch_attention_split(const float *q, const float *kc, const float *
     const size_t q_lds = (size_t)G * hd * 4, p_lds = (size_t)max_pos * 4;
     if (q_lds > 64 * 1024 || p_lds > 160 * 1024) return hipErrorInvalidValue;
     const dim3 g1((unsigned)(n_kv_head * nblk)), g2((unsigned)(n_head * (hd / kPvSlice)));
-    const void *fp = nullptr;
+    const int U = max_pos <= 256 ? 4 : max_pos <= 512 ? 8 : max_pos <= 768 ? 12 : 16;
     switch (hd) {
-    case 16: fp = (const void *)k_attn_pv<16>; break;
-    case 32: fp = (const void *)k_attn_pv<32>; break;
-    case 64: fp = (const void *)k_attn_pv<64>; break;
-    default: fp = (const void *)k_attn_pv<128>; break;
+    case 16: return launch_attn_hd<16>(g1, g2, q_lds, p_lds, U, q, kc, vc, out, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk, s);
+    case 32: return launch_attn_hd<32>(g1, g2, q_lds, p_lds, U, q, kc, vc, out, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk, s);
+    case 64: return launch_attn_hd<64>(g1, g2, q_lds, p_lds, U, q, kc, vc, out, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk, s);
+    case 128: return launch_attn_hd<128>(g1, g2, q_lds, p_lds, U, q, kc, vc, out, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk, s);
+    default: return hipErrorInvalidValue;
     }
-    if (p_lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute(fp, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p_lds);
-        if (e != hipSuccess) return e;
-    }
-    switch (hd) {
-    case 16:
-        hipLaunchKernelGGL(k_attn_scores<16>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk);
-        hipLaunchKernelGGL(k_attn_pv<16>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed);
-        break;
-    case 32:
-        hipLaunchKernelGGL(k_attn_scores<32>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk);
-        hipLaunchKernelGGL(k_attn_pv<32>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed);
-        break;
-    case 64:
-        hipLaunchKernelGGL(k_attn_scores<64>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk);
-        hipLaunchKernelGGL(k_attn_pv<64>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed);
-        break;
-    case 128:
-        hipLaunchKernelGGL(k_attn_scores<128>, g1, dim3(256), q_lds, s, q, kc, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk);
-        hipLaunchKernelGGL(k_attn_pv<128>, g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed);
-        break;
-    default:
-        return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
 }
 
 hipError_t launch_silu_mul(const float *g, const float *u, float *y, int64_t n, hipStream_t s)
