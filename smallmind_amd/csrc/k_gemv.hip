@@ -415,6 +415,9 @@ hipError_t launch_v(const GemvArgs &a, int m, hipStream_t s)
         // makes them visible without a device-scope fence in each of the many workgroups
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
+        if (a.x_next)
+            return launch_argmax_embed(a.wg_val, a.wg_idx, (int)grid.x, a.amax_out, a.tokens, a.tok_pos,
+                                       a.next_emb, a.next_embp.q ? &a.next_embp : nullptr, a.x_next, s);
         return launch_argmax_pairs(a.wg_val, a.wg_idx, (int)grid.x, a.amax_out, a.tokens, a.tok_pos, s);
     }
     return hipGetLastError();

@@ -479,6 +479,68 @@ __global__ __launch_bounds__(kThreads) void k_embed(WView w, WView pw, int has_p
     }
 }
 
+// End of a decode step with the next step's embedding folded in: argmax over the head's
+// per-workgroup (value, index) pairs (lowest index on ties), token appended at tokens[pos + 1],
+// position advanced, and x_next = emb[token] (+ pos_emb[pos + 1]).  The position is read up
+// front, before the reduction, so it costs no round trip of its own.
+__global__ __launch_bounds__(kThreads) void k_argmax_embed(const float *__restrict__ val,
+                                                           const int32_t *__restrict__ idx, int n,
+                                                           int32_t *__restrict__ out,
+                                                           int32_t *__restrict__ tokens,
+                                                           int32_t *__restrict__ pos, WView w, WView pw,
+                                                           int has_pos, float *__restrict__ x_next)
+{
+    __shared__ float bv[kWaves];
+    __shared__ int bi[kWaves];
+    __shared__ int s_p;
+    // only thread 0 touches the position in memory (read here, advanced at the end); the
+    // other threads take it from LDS after the barrier
+    int p = 0;
+    if (threadIdx.x == 0) p = *pos;
+    float best = -INFINITY;
+    int bidx = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const float v = val[i];
+        const int ix = idx[i];
+        if (v > best || (v == best && ix < bidx)) { best = v; bidx = ix; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bidx, o, 64);
+        if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
+    }
+    const int wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { bv[wv] = best; bi[wv] = bidx; }
+    if (threadIdx.x == 0) s_p = p;
+    __syncthreads();
+    p = s_p;
+    best = bv[0];
+    bidx = bi[0];
+#pragma unroll
+    for (int k = 1; k < kWaves; k++)
+        if (bv[k] > best || (bv[k] == best && bi[k] < bidx)) { best = bv[k]; bidx = bi[k]; }
+    if (bidx == 0x7FFFFFFF) bidx = 0;
+    if (threadIdx.x == 0) {
+        if (out) *out = bidx;
+        tokens[p + 1] = bidx;
+        *pos = p + 1;
+    }
+    int64_t tok = bidx;
+    if (tok < 0 || tok >= w.rows) tok = 0;
+    // the learned position row of the next position (clamped: after the last step of a full
+    // context it is never used)
+    const int64_t prow = has_pos ? (p + 1 < pw.rows ? p + 1 : pw.rows - 1) : 0;
+    const WView *pp = has_pos ? &pw : nullptr;
+    switch (w.fmt) {
+    case FMT_Q4_0: embed_row<FMT_Q4_0>(w, tok, x_next, pp, prow); break;
+    case FMT_Q8_0: embed_row<FMT_Q8_0>(w, tok, x_next, pp, prow); break;
+    case FMT_Q4_K: embed_row<FMT_Q4_K>(w, tok, x_next, pp, prow); break;
+    case FMT_Q5_K: embed_row<FMT_Q5_K>(w, tok, x_next, pp, prow); break;
+    default: embed_row<FMT_Q6_K>(w, tok, x_next, pp, prow); break;
+    }
+}
+
 // Embedding rows of a token batch: x[t] = emb[tok[t]] (+ pos_emb[pos[t]]), one workgroup per
 // token.
 __global__ __launch_bounds__(kThreads) void k_embed_tokens(WView w, WView pw, int has_pos,
@@ -704,6 +766,16 @@ hipError_t launch_argmax_pairs(const float *val, const int32_t *idx, int n, int3
                                int32_t *tokens, int32_t *pos, hipStream_t s)
 {
     hipLaunchKernelGGL(k_argmax_pairs, dim3(1), dim3(256), 0, s, val, idx, n, out, tokens, pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_embed(const float *val, const int32_t *idx, int n, int32_t *out,
+                               int32_t *tokens, int32_t *pos, const WView &tok, const WView *posw,
+                               float *x_next, hipStream_t s)
+{
+    WView pw = posw ? *posw : tok;
+    hipLaunchKernelGGL(k_argmax_embed, dim3(1), dim3(kThreads), 0, s, val, idx, n, out, tokens, pos, tok, pw,
+                       posw ? 1 : 0, x_next);
     return hipGetLastError();
 }
 

@@ -202,7 +202,9 @@ struct smx_session {
     // argmax fused into the head GEMV: per-workgroup partials
     float *head_val = nullptr;
     int32_t *head_idx = nullptr;
-    hipGraphExec_t g_prefill = nullptr, g_decode = nullptr;
+    // g_decode looks up the embedding of tokens[pos]; g_decode_next follows a decode step, whose
+    // argmax already wrote the embedding row of the token it appended
+    hipGraphExec_t g_prefill = nullptr, g_decode = nullptr, g_decode_next = nullptr;
     TokBatch pb;            // prefill chunks on the matrix cores (allocated on first use)
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     std::atomic<int> busy{0};
@@ -252,14 +254,17 @@ int parse_layer(const char *name, std::string &rest)
 }
 
 // Builds the step's kernel sequence on stream s (captured into a graph by the caller).
-int enqueue_step(smx_session *S, bool with_head, hipStream_t s)
+// with_embed = false: x already holds the step's embedding row, written by the previous decode
+// step's argmax (a step with a head folds the next step's embedding lookup into its argmax).
+int enqueue_step(smx_session *S, bool with_head, bool with_embed, hipStream_t s)
 {
     smx_model *m = S->m;
     const smx_model_config &c = m->cfg;
     const int Hkv = c.n_kv_head, hd = m->hd;
     const size_t layer_cache = (size_t)Hkv * S->max_ctx * hd;
     WView posw = m->pos.view();
-    SMX_HIP(launch_embed(m->tok.view(), m->llama ? nullptr : &posw, S->tokens, S->pos, S->x, s));
+    if (with_embed)
+        SMX_HIP(launch_embed(m->tok.view(), m->llama ? nullptr : &posw, S->tokens, S->pos, S->x, s));
     for (int l = 0; l < c.n_layer; l++) {
         Layer &L = m->layers[l];
         GemvArgs a{};
@@ -334,6 +339,9 @@ int enqueue_step(smx_session *S, bool with_head, hipStream_t s)
         hgt.amax_out = S->amax;
         hgt.tokens = S->tokens;
         hgt.tok_pos = S->pos;
+        hgt.x_next = S->x;   // x is dead once the head has read it
+        hgt.next_emb = m->tok.view();
+        if (!m->llama) hgt.next_embp = posw;
         SMX_HIP(launch_gemv(hgt, 1, s));
     } else {
         SMX_HIP(launch_advance(S->pos, s));
@@ -341,12 +349,12 @@ int enqueue_step(smx_session *S, bool with_head, hipStream_t s)
     return SMX_OK;
 }
 
-int capture_step(smx_session *S, bool with_head, hipGraphExec_t *out)
+int capture_step(smx_session *S, bool with_head, bool with_embed, hipGraphExec_t *out)
 {
     hipStream_t s = S->m->ctx->stream;
     hipGraph_t graph = nullptr;
     SMX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_step(S, with_head, s);
+    int rc = enqueue_step(S, with_head, with_embed, s);
     hipError_t e = hipStreamEndCapture(s, &graph);
     if (rc != SMX_OK) {
         if (graph) (void)hipGraphDestroy(graph);
@@ -1168,8 +1176,9 @@ SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out)
     }
     int rc = setup_persistent(S);
     if (rc == SMX_OK && !S->persistent) {
-        rc = capture_step(S, false, &S->g_prefill);
-        if (rc == SMX_OK) rc = capture_step(S, true, &S->g_decode);
+        rc = capture_step(S, false, true, &S->g_prefill);
+        if (rc == SMX_OK) rc = capture_step(S, true, true, &S->g_decode);
+        if (rc == SMX_OK) rc = capture_step(S, true, false, &S->g_decode_next);
     }
     if (rc != SMX_OK) {
         std::string msg = smx::last_error();
@@ -1260,7 +1269,7 @@ SMX_API int smx_session_generate(smx_session *S, const int32_t *prompt, int n_pr
             SMX_HIP(hipMemcpyAsync(logits_out, S->logits_all, (size_t)n_new * V * 4, hipMemcpyDeviceToHost, s));
     } else {
         for (int i = 0; i < n_new; i++) {
-            SMX_HIP(hipGraphLaunch(S->g_decode, s));
+            SMX_HIP(hipGraphLaunch(i == 0 ? S->g_decode : S->g_decode_next, s));
             if (logits_out)
                 SMX_HIP(hipMemcpyAsync(logits_out + (size_t)i * V, S->logits, (size_t)V * 4, hipMemcpyDeviceToHost, s));
         }
@@ -1424,6 +1433,7 @@ SMX_API int smx_session_destroy(smx_session *S)
     (void)hipSetDevice(S->m->ctx->device);
     if (S->g_prefill) (void)hipGraphExecDestroy(S->g_prefill);
     if (S->g_decode) (void)hipGraphExecDestroy(S->g_decode);
+    if (S->g_decode_next) (void)hipGraphExecDestroy(S->g_decode_next);
     for (hipEvent_t e : S->ev) if (e) (void)hipEventDestroy(e);
     free_dev(S->kc); free_dev(S->vc); free_dev(S->x); free_dev(S->q); free_dev(S->att); free_dev(S->scores);
     free_dev(S->h); free_dev(S->logits); free_dev(S->tokens); free_dev(S->pos); free_dev(S->amax);

@@ -95,6 +95,11 @@ struct GemvArgs {
     float *wg_val;
     int32_t *wg_idx;
     int32_t *amax_out, *tokens, *tok_pos;
+    // EPI_ARGMAX with x_next set: the selected token's embedding row (+ the learned position
+    // row of the next position when next_embp.q is set) is written to x_next, ready for the
+    // next decode step
+    float *x_next;
+    WView next_emb, next_embp;
 };
 
 hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s);
@@ -195,6 +200,11 @@ hipError_t launch_argmax(const float *x, int n, int32_t *out, int32_t *tokens, i
 // Argmax over n (value, index) pairs, lowest index on ties; same outputs as launch_argmax.
 hipError_t launch_argmax_pairs(const float *val, const int32_t *idx, int n, int32_t *out,
                                int32_t *tokens, int32_t *pos, hipStream_t s);
+// The same, then the selected token's embedding row (+ learned position row pos + 1 when posw
+// is set) written to x_next: the embedding lookup of the next decode step.
+hipError_t launch_argmax_embed(const float *val, const int32_t *idx, int n, int32_t *out,
+                               int32_t *tokens, int32_t *pos, const WView &tok, const WView *posw,
+                               float *x_next, hipStream_t s);
 hipError_t launch_embed(const WView &tok, const WView *posw, const int32_t *tokens,
                         const int32_t *pos, float *x, hipStream_t s);
 hipError_t launch_advance(int32_t *pos, hipStream_t s);
