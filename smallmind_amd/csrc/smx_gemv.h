@@ -52,6 +52,28 @@ __device__ __forceinline__ float dot8(uint32_t lo, uint32_t hi, const float4 *xv
     return acc;
 }
 
+// dot8 for 4-bit codes (every byte of lo / hi below 16), scaled by 2^-9: a byte 0000qqqq read
+// as an OCP E4M3 value is exactly q * 2^-9 (subnormal for q < 8, exponent 1 above), so one
+// v_cvt_pk_f32_fp8 turns two codes into floats.  The products and partial sums are the
+// dot8 ones times 2^-9 exactly (a power-of-two scaling commutes with fp32 rounding away from
+// the subnormal range), in the same order; callers fold 512 into the block scale.
+__device__ __forceinline__ float dot8_nib(uint32_t lo, uint32_t hi, const float4 *xv, int g, float acc)
+{
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const int e = 8 * g;
+    const f2 l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false), l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+    const f2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false), h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+    acc = __builtin_fmaf(l01.x, xget(xv, e + 0), acc);
+    acc = __builtin_fmaf(h01.x, xget(xv, e + 1), acc);
+    acc = __builtin_fmaf(l01.y, xget(xv, e + 2), acc);
+    acc = __builtin_fmaf(h01.y, xget(xv, e + 3), acc);
+    acc = __builtin_fmaf(l23.x, xget(xv, e + 4), acc);
+    acc = __builtin_fmaf(h23.x, xget(xv, e + 5), acc);
+    acc = __builtin_fmaf(l23.y, xget(xv, e + 6), acc);
+    acc = __builtin_fmaf(h23.y, xget(xv, e + 7), acc);
+    return acc;
+}
+
 template <int S>
 __device__ __forceinline__ uint32_t shl(uint32_t v)
 {
@@ -81,12 +103,13 @@ template <> struct Raw<FMT_Q4_0> {
     {
         const uint32_t v[4] = {q.x ^ 0x88888888u, q.y ^ 0x88888888u, q.z ^ 0x88888888u, q.w ^ 0x88888888u};
         float s0 = 0.0f, s1 = 0.0f;
-        s0 = dot8(v[0] & 0x0F0F0F0Fu, (v[0] >> 4) & 0x0F0F0F0Fu, xv, 0, s0);
-        s1 = dot8(v[1] & 0x0F0F0F0Fu, (v[1] >> 4) & 0x0F0F0F0Fu, xv, 1, s1);
-        s0 = dot8(v[2] & 0x0F0F0F0Fu, (v[2] >> 4) & 0x0F0F0F0Fu, xv, 2, s0);
-        s1 = dot8(v[3] & 0x0F0F0F0Fu, (v[3] >> 4) & 0x0F0F0F0Fu, xv, 3, s1);
-        // codes are (n ^ 8) = value + 8 (Q4Tensor.DecodeNibble two's complement)
-        return h2f(d) * ((s0 + s1) - 8.0f * (xa + xb));
+        s0 = dot8_nib(v[0] & 0x0F0F0F0Fu, (v[0] >> 4) & 0x0F0F0F0Fu, xv, 0, s0);
+        s1 = dot8_nib(v[1] & 0x0F0F0F0Fu, (v[1] >> 4) & 0x0F0F0F0Fu, xv, 1, s1);
+        s0 = dot8_nib(v[2] & 0x0F0F0F0Fu, (v[2] >> 4) & 0x0F0F0F0Fu, xv, 2, s0);
+        s1 = dot8_nib(v[3] & 0x0F0F0F0Fu, (v[3] >> 4) & 0x0F0F0F0Fu, xv, 3, s1);
+        // codes are (n ^ 8) = value + 8 (Q4Tensor.DecodeNibble two's complement); sums are
+        // scaled by 2^-9 (dot8_nib), the scale by 512
+        return (h2f(d) * 512.0f) * ((s0 + s1) - 0.015625f * (xa + xb));
     }
 };
 
@@ -141,11 +164,11 @@ template <> struct Raw<FMT_Q4_K> {
         const float m = h2f(h.x >> 16) * (float)kq_scale6(h.y, h.z, h.w, j, 1);
         const uint32_t v[4] = {q.x, q.y, q.z, q.w};
         float s0 = 0.0f, s1 = 0.0f;
-        s0 = dot8(v[0] & 0x0F0F0F0Fu, (v[0] >> 4) & 0x0F0F0F0Fu, xv, 0, s0);
-        s1 = dot8(v[1] & 0x0F0F0F0Fu, (v[1] >> 4) & 0x0F0F0F0Fu, xv, 1, s1);
-        s0 = dot8(v[2] & 0x0F0F0F0Fu, (v[2] >> 4) & 0x0F0F0F0Fu, xv, 2, s0);
-        s1 = dot8(v[3] & 0x0F0F0F0Fu, (v[3] >> 4) & 0x0F0F0F0Fu, xv, 3, s1);
-        return __builtin_fmaf(sc, s0 + s1, -(m * (xa + xb)));
+        s0 = dot8_nib(v[0] & 0x0F0F0F0Fu, (v[0] >> 4) & 0x0F0F0F0Fu, xv, 0, s0);
+        s1 = dot8_nib(v[1] & 0x0F0F0F0Fu, (v[1] >> 4) & 0x0F0F0F0Fu, xv, 1, s1);
+        s0 = dot8_nib(v[2] & 0x0F0F0F0Fu, (v[2] >> 4) & 0x0F0F0F0Fu, xv, 2, s0);
+        s1 = dot8_nib(v[3] & 0x0F0F0F0Fu, (v[3] >> 4) & 0x0F0F0F0Fu, xv, 3, s1);
+        return __builtin_fmaf(sc * 512.0f, s0 + s1, -(m * (xa + xb)));   // sums scaled by 2^-9
     }
 };
 
