@@ -429,20 +429,19 @@ hipError_t launch_v(const GemvArgs &a, int m, hipStream_t s)
 template <int PRO, int EC>
 hipError_t launch_pe(const GemvArgs &a, int m, hipStream_t s)
 {
-    const int64_t K = a.w.cols, nch = K / 32;
-    if (K > 8192) {
+    const int64_t K = a.w.cols;
+    switch (gemv_shape(a.w.rows, K)) {
+    case GS_WIDE:
         if constexpr (PRO == PRO_NONE && EC == EC_SIMPLE) {
             if (K <= 16384) return launch_v<2, 4, 2, PRO, EC, 2>(a, m, s);
             return launch_v<2, 4, 2, PRO, EC, 0>(a, m, s);
         }
         return hipErrorInvalidValue;
+    case GS_R4S1: return launch_v<4, 1, 1, PRO, EC, 1>(a, m, s);
+    case GS_R2S1: return launch_v<2, 1, 1, PRO, EC, 1>(a, m, s);
+    case GS_R2S2: return launch_v<2, 2, 1, PRO, EC, 1>(a, m, s);
+    default: return launch_v<2, 4, 1, PRO, EC, 1>(a, m, s);   // nch <= 256
     }
-    if (nch <= 64) {
-        if (a.w.rows >= 8192) return launch_v<4, 1, 1, PRO, EC, 1>(a, m, s);
-        return launch_v<2, 1, 1, PRO, EC, 1>(a, m, s);
-    }
-    if (nch <= 128) return launch_v<2, 2, 1, PRO, EC, 1>(a, m, s);
-    return launch_v<2, 4, 1, PRO, EC, 1>(a, m, s);   // nch <= 256
 }
 
 }  // namespace

@@ -104,6 +104,19 @@ struct GemvArgs {
 
 hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s);
 
+// Launch shape of the fused GEMV for a [rows][cols] matrix: R rows per wave, S waves per row
+// group, 4/S row groups per 4-wave workgroup (workgroup b owns rows [b*n, (b+1)*n), n = R*4/S).
+enum GemvShape { GS_R4S1, GS_R2S1, GS_R2S2, GS_R2S4, GS_WIDE };
+inline GemvShape gemv_shape(int64_t rows, int64_t cols)
+{
+    const int64_t nch = cols / 32;
+    if (cols > 8192) return GS_WIDE;                     // R=2, S=4 (plain GEMVs only)
+    if (nch <= 64) return rows >= 8192 ? GS_R4S1 : GS_R2S1;
+    if (nch <= 128) return GS_R2S2;
+    return GS_R2S4;                                      // nch <= 256
+}
+
+
 // ---- quantized GEMM on the matrix cores for M activation rows (tokens) ------------------------
 // y[M][rows] = norm(x)[M][cols] W^T with the GEMV's prologues and epilogues applied per token.
 // For EPI_QKV every token carries its own position and KV cache (several sessions may share
