@@ -205,6 +205,9 @@ struct smx_session {
     // g_decode looks up the embedding of tokens[pos]; g_decode_next follows a decode step, whose
     // argmax already wrote the embedding row of the token it appended
     hipGraphExec_t g_prefill = nullptr, g_decode = nullptr, g_decode_next = nullptr;
+    // kDecodeBlock chained decode steps in one graph: one launch per block of tokens when no
+    // per-step logits are copied out
+    hipGraphExec_t g_decode_block = nullptr;
     TokBatch pb;            // prefill chunks on the matrix cores (allocated on first use)
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     std::atomic<int> busy{0};
@@ -349,12 +352,16 @@ int enqueue_step(smx_session *S, bool with_head, bool with_embed, hipStream_t s)
     return SMX_OK;
 }
 
-int capture_step(smx_session *S, bool with_head, bool with_embed, hipGraphExec_t *out)
+constexpr int kDecodeBlock = 8;
+
+// Captures `steps` consecutive steps (steps > 1: chained decode steps) into one graph.
+int capture_step(smx_session *S, bool with_head, bool with_embed, hipGraphExec_t *out, int steps = 1)
 {
     hipStream_t s = S->m->ctx->stream;
     hipGraph_t graph = nullptr;
     SMX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_step(S, with_head, with_embed, s);
+    int rc = SMX_OK;
+    for (int i = 0; i < steps && rc == SMX_OK; i++) rc = enqueue_step(S, with_head, with_embed, s);
     hipError_t e = hipStreamEndCapture(s, &graph);
     if (rc != SMX_OK) {
         if (graph) (void)hipGraphDestroy(graph);
@@ -1179,6 +1186,7 @@ SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out)
         rc = capture_step(S, false, true, &S->g_prefill);
         if (rc == SMX_OK) rc = capture_step(S, true, true, &S->g_decode);
         if (rc == SMX_OK) rc = capture_step(S, true, false, &S->g_decode_next);
+        if (rc == SMX_OK) rc = capture_step(S, true, false, &S->g_decode_block, kDecodeBlock);
     }
     if (rc != SMX_OK) {
         std::string msg = smx::last_error();
@@ -1268,10 +1276,16 @@ SMX_API int smx_session_generate(smx_session *S, const int32_t *prompt, int n_pr
         if (logits_out)
             SMX_HIP(hipMemcpyAsync(logits_out, S->logits_all, (size_t)n_new * V * 4, hipMemcpyDeviceToHost, s));
     } else {
-        for (int i = 0; i < n_new; i++) {
+        for (int i = 0; i < n_new;) {
+            if (i > 0 && !logits_out && n_new - i >= kDecodeBlock) {
+                SMX_HIP(hipGraphLaunch(S->g_decode_block, s));
+                i += kDecodeBlock;
+                continue;
+            }
             SMX_HIP(hipGraphLaunch(i == 0 ? S->g_decode : S->g_decode_next, s));
             if (logits_out)
                 SMX_HIP(hipMemcpyAsync(logits_out + (size_t)i * V, S->logits, (size_t)V * 4, hipMemcpyDeviceToHost, s));
+            i++;
         }
     }
     SMX_HIP(hipEventRecord(S->ev[2], s));
@@ -1434,6 +1448,7 @@ SMX_API int smx_session_destroy(smx_session *S)
     if (S->g_prefill) (void)hipGraphExecDestroy(S->g_prefill);
     if (S->g_decode) (void)hipGraphExecDestroy(S->g_decode);
     if (S->g_decode_next) (void)hipGraphExecDestroy(S->g_decode_next);
+    if (S->g_decode_block) (void)hipGraphExecDestroy(S->g_decode_block);
     for (hipEvent_t e : S->ev) if (e) (void)hipEventDestroy(e);
     free_dev(S->kc); free_dev(S->vc); free_dev(S->x); free_dev(S->q); free_dev(S->att); free_dev(S->scores);
     free_dev(S->h); free_dev(S->logits); free_dev(S->tokens); free_dev(S->pos); free_dev(S->amax);

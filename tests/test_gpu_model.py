@@ -114,6 +114,22 @@ def test_decode_is_deterministic_and_cache_equals_recompute(pairs):
     s2.close()
 
 
+def test_decode_blocks_match_single_steps(pairs):
+    """Without per-step logits, generate replays blocks of chained decode steps in one graph;
+    the tokens equal those of the one-step-per-launch path (taken when logits are copied out),
+    including a tail shorter than a block."""
+    om, gm = _pair(pairs, "llama-q4k")
+    prompt = np.arange(9, dtype=np.int32) * 11
+    for n_new in (1, 8, 9, 19):
+        s1 = gm.create_session(64)
+        t_block, _ = s1.generate_greedy(prompt, n_new)
+        s2 = gm.create_session(64)
+        t_step, _, _ = s2.generate_greedy(prompt, n_new, return_logits=True)
+        assert np.array_equal(t_block, t_step), n_new
+        s1.close()
+        s2.close()
+
+
 def test_errors_out_of_range_and_bad_tokens(pairs):
     from smallmind_amd.quantization import SmxError
     om, gm = _pair(pairs, "llama-q4k")
