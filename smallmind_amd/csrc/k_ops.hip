@@ -261,12 +261,21 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ score
             pu[3 * UQ + k] = dpp_mov<0xFF>(e[k]);    // quad_perm [3,3,3,3]
         }
     } else {
-        // long contexts: the scores of all positions pass through LDS
+        // long contexts: the scores of all positions pass through LDS, loaded in batches of
+        // eight per thread (all loads of a batch in flight before any is used)
         float mx = -INFINITY;
-        for (int j = tid; j < n_pos; j += 256) {
-            const float v = srow[j];
-            p[j] = v;
-            mx = fmaxf(mx, v);
+        for (int jb = tid; jb < n_pos; jb += 256 * 8) {
+            float sb[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) sb[u] = srow[min(jb + 256 * u, sc_stride - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int j = jb + 256 * u;
+                if (j < n_pos) {
+                    p[j] = sb[u];
+                    mx = fmaxf(mx, sb[u]);
+                }
+            }
         }
         mx = block_max<4>(mx, red);
         float sum = 0.0f;
@@ -294,24 +303,34 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ score
             acc.w = __builtin_fmaf(pp, vv[u].w, acc.w);
         }
     }
-    // positions beyond the first batch (n_pos > NB)
-    constexpr int U2 = 8;
-    for (int jb = NB + pl; jb < n_pos; jb += PL * U2) {
+    // positions beyond the first batch (n_pos > NB): batches of U2 rows per lane, each batch's
+    // loads (clamped into the row, dropped by selection) issued before the previous batch's
+    // multiply-adds
+    constexpr int U2 = 16;
+    if (n_pos > NB) {
         float4 v2[U2];
-        float p2[U2];
+        auto load2 = [&](int jb) {
 #pragma unroll
-        for (int u = 0; u < U2; u++) {
-            const int j = jb + u * PL;
-            const bool ok = j < n_pos;
-            v2[u] = ok ? vload(j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            p2[u] = ok ? p[j] : 0.0f;
-        }
+            for (int u = 0; u < U2; u++) v2[u] = vload(min(jb + u * PL, ctx_stride - 1));
+        };
+        int jb = NB + pl;
+        load2(jb);
+        for (; jb < n_pos; jb += PL * U2) {
+            float4 cur[U2];
 #pragma unroll
-        for (int u = 0; u < U2; u++) {
-            acc.x = __builtin_fmaf(p2[u], v2[u].x, acc.x);
-            acc.y = __builtin_fmaf(p2[u], v2[u].y, acc.y);
-            acc.z = __builtin_fmaf(p2[u], v2[u].z, acc.z);
-            acc.w = __builtin_fmaf(p2[u], v2[u].w, acc.w);
+            for (int u = 0; u < U2; u++) cur[u] = v2[u];
+            if (jb + PL * U2 < n_pos) load2(jb + PL * U2);
+#pragma unroll
+            for (int u = 0; u < U2; u++) {
+                const int j = jb + u * PL;
+                if (j < n_pos) {
+                    const float pp = p[j];
+                    acc.x = __builtin_fmaf(pp, cur[u].x, acc.x);
+                    acc.y = __builtin_fmaf(pp, cur[u].y, acc.y);
+                    acc.z = __builtin_fmaf(pp, cur[u].z, acc.z);
+                    acc.w = __builtin_fmaf(pp, cur[u].w, acc.w);
+                }
+            }
         }
     }
     // lanes with the same column: butterfly over lane bits C4, 2*C4, ..., 32; then the waves
