@@ -89,40 +89,16 @@ __global__ __launch_bounds__(kThreads) void k_softmax(float *__restrict__ scores
     for (int j = threadIdx.x; j < k_seq; j += kThreads) row[j] = j < valid ? row[j] * inv : 0.0f;
 }
 
-// One decode position of MultiHeadAttention for every query head (one workgroup per head).
-// The softmax needs the exact maximum over all positions before any exponential (the Pade
-// FastExp is not multiplicative), so a head is not split across workgroups; instead the
-// workgroup is wide (512 threads) and, for head_dim 64, the score pass (one position per
-// thread) and the P.V pass (16 positions per thread) each cover 512 positions per round of
-// loads.
+// Attention of one (token, head) by a whole workgroup (attention_head), as used by the token
+// batches below: 512 threads; for head_dim 64 the score pass (one position per thread) and the
+// P.V pass (16 positions per thread) each cover 512 positions per round of loads.
 template <int HD> struct AttnCfg {
     static constexpr int NT = 512;
     static constexpr int U = HD <= 64 ? 16 : 8;
 };
 
-template <int HD>
-__global__ __launch_bounds__(AttnCfg<HD>::NT) void k_attention_decode(
-    const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
-    float *__restrict__ out, int n_head, int n_kv_head, int ctx_stride,
-    const int32_t *__restrict__ pos_dev, int n_pos_fixed)
-{
-    constexpr int NT = AttnCfg<HD>::NT;
-    extern __shared__ float4 smem4[];
-    __shared__ AttnSmem<HD, NT> sm;
-    // Workgroups are dealt to the 8 XCDs round-robin (workgroup b -> XCD b % 8); ordering the
-    // heads so that XCD x gets heads x*H/8 .. x*H/8 + H/8 - 1 keeps the query heads of one KV
-    // head on one XCD, whose L2 then serves their shared K/V rows.
-    const int b = blockIdx.x;
-    const int h = (n_head % 8 == 0) ? (b % 8) * (n_head / 8) + b / 8 : b;
-    const int kvh = h / (n_head / n_kv_head);
-    const int n_pos = pos_dev ? ld_uniform(pos_dev) + 1 : n_pos_fixed;
-    const int64_t off = (int64_t)kvh * ctx_stride * HD;
-    attention_head<HD, NT, AttnCfg<HD>::U>(q + (int64_t)h * HD, kc + off, vc + off, out + (int64_t)h * HD,
-                                           n_pos, ctx_stride, (float *)smem4, sm);
-}
-
-// Decode attention split over the whole chip in two launches (the single-workgroup-per-head
-// kernel above streams a head's K and V through one CU).  The kernel boundary between them
+// Decode attention split over the whole chip in two launches (one workgroup per head would
+// stream the head's K and V through one CU).  The kernel boundary between them
 // supplies the exact maximum over all positions that the Pade FastExp needs before any
 // exponential (MathUtils.cs:20-32; MultiHeadAttention.cs:676-844).
 //
@@ -674,33 +650,6 @@ hipError_t launch_rope(float *data, int n_heads, int seq, int hd, int pos0, cons
 hipError_t launch_softmax(float *scores, float scale, int seq, int k_seq, int cache_off, hipStream_t s)
 {
     hipLaunchKernelGGL(k_softmax, dim3(seq), dim3(kThreads), 0, s, scores, scale, k_seq, cache_off);
-    return hipGetLastError();
-}
-
-hipError_t launch_attention_decode(const float *q, const float *kc, const float *vc, float *out,
-                                   int n_head, int n_kv_head, int hd, int ctx_stride,
-                                   const int32_t *pos_dev, int n_pos_fixed, int max_pos,
-                                   hipStream_t s)
-{
-    const size_t lds = (size_t)max_pos * 4;
-    const void *fn = nullptr;
-    switch (hd) {
-    case 16: fn = (const void *)k_attention_decode<16>; break;
-    case 32: fn = (const void *)k_attention_decode<32>; break;
-    case 64: fn = (const void *)k_attention_decode<64>; break;
-    case 128: fn = (const void *)k_attention_decode<128>; break;
-    default: return hipErrorInvalidValue;
-    }
-    if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-    }
-    switch (hd) {
-    case 16: hipLaunchKernelGGL(k_attention_decode<16>, dim3(n_head), dim3(AttnCfg<16>::NT), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
-    case 32: hipLaunchKernelGGL(k_attention_decode<32>, dim3(n_head), dim3(AttnCfg<32>::NT), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
-    case 64: hipLaunchKernelGGL(k_attention_decode<64>, dim3(n_head), dim3(AttnCfg<64>::NT), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
-    default: hipLaunchKernelGGL(k_attention_decode<128>, dim3(n_head), dim3(AttnCfg<128>::NT), lds, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed); break;
-    }
     return hipGetLastError();
 }
 

@@ -194,10 +194,6 @@ hipError_t launch_layernorm(const float *x, const float *g, const float *b, floa
 hipError_t launch_rope(float *data, int n_heads, int seq, int hd, int pos0, const float *c,
                        const float *sn, hipStream_t s);
 hipError_t launch_softmax(float *scores, float scale, int seq, int k_seq, int cache_off, hipStream_t s);
-hipError_t launch_attention_decode(const float *q, const float *kc, const float *vc, float *out,
-                                   int n_head, int n_kv_head, int hd, int ctx_stride,
-                                   const int32_t *pos_dev, int n_pos_fixed, int max_pos,
-                                   hipStream_t s);
 // Decode attention as two launches spread over the chip: scores per (KV head, position block)
 // into `scores` (attention_scores_floats(n_head, max_pos) floats: rows of max_pos rounded up
 // to a multiple of 4), then softmax + P.V per (head, 16-dimension slice).  Positions up to
