@@ -23,8 +23,9 @@
 // one strided copy per wave.
 // Codes are unpacked with and/shift into bytes and converted with v_cvt_f32_ubyte*; block
 // scales are factored out of each 32-term sum (sum (sc*q - m) x = sc * sum q x - m * sum x).
-// The R per-lane partials are summed across the wave with DPP, combined across the S waves in
-// LDS in a fixed order, and one lane applies the epilogue.
+// The R per-lane partials are summed across the wave transposed (lane swaps fold two rows per
+// add, then DPP within 16-lane rows), combined across the S waves in LDS in a fixed order, and
+// the R rows' epilogues run on R lanes at once.
 //
 // Compiled once per block format (SMX_GEMV_FMT) so the instantiations build in parallel.
 #include "smx_device.h"
@@ -67,6 +68,19 @@ __device__ __forceinline__ void epi_load(const GemvArgs &a, uint32_t row0, uint3
     if constexpr (EC == EC_QKV) e.pos = a.pos ? ld_uniform(a.pos) : a.pos_val;
 }
 
+// R wave-uniform values moved to the first lane of each lane block: lane r*64/R receives v[r],
+// the other lanes 0.  v_writelane moves a scalar into one lane with no compares or selects
+// (a lane-indexed select chain over v can be folded into an indexed access, which puts the
+// array in scratch memory).
+template <int R>
+__device__ __forceinline__ float spread(const float *v)
+{
+    float o = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; r++) asm("v_writelane_b32 %0, %1, %2" : "+v"(o) : "s"(v[r]), "i"(r * (64 / R)));
+    return o;
+}
+
 // RoPE table entries of the group's row pairs, loaded once the activation vector is staged.
 // They depend on the position, a scalar load, and go through the vector path on purpose:
 // scalar loads share a counter with LDS operations and return out of order, so one still
@@ -88,90 +102,73 @@ __device__ __forceinline__ void epi_load_rope(const GemvArgs &a, uint32_t row0, 
     }
 }
 
-// Lane-indexed pick of one of P wave-uniform values (lanes >= P get the last one).
+// Lane-indexed pick of one of P values that are the same in every lane (i >= P gives the last).
 template <int P>
-__device__ __forceinline__ float pick(const float *v, int lane)
+__device__ __forceinline__ float pick(const float *v, int i)
 {
     float o = v[P - 1];
 #pragma unroll
-    for (int r = P - 2; r >= 0; r--) o = lane == r ? v[r] : o;
+    for (int r = P - 2; r >= 0; r--) o = i == r ? v[r] : o;
     return o;
 }
 
-// Epilogue of one row group.  Called by the whole wave: SwiGLU computes its R/2 outputs on
-// lanes 0 .. R/2-1 in parallel (two long-latency exp/divide chains would otherwise run back
-// to back on one lane) and stores them with one instruction; the other epilogues run on lane 0.
+// Epilogue of one row group.  Called by the whole wave with c = the transposed row totals
+// (wave_totals_t: row r in lane block r of 64/R lanes), so the R rows leave from R lanes in
+// one store instruction.  SwiGLU and QKV work on row pairs: a lane swap brings rows 2p and
+// 2p+1 together in lane 32p, and the pairs are computed in parallel (each SwiGLU output is a
+// long exp/divide chain).
 template <int R, int EC>
-__device__ __forceinline__ void epi_store(const GemvArgs &a, const float *t, const EpiIn<R, EC> &e,
+__device__ __forceinline__ void epi_store(const GemvArgs &a, float c, const EpiIn<R, EC> &e,
                                           uint32_t row0, uint32_t N, int my, int lane)
 {
+    constexpr int LB = 64 / R;
+    const int rl = lane / LB;   // row of this lane's block
     float *out = a.out + (int64_t)my * a.out_stride;
-    float v[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) v[r] = a.bias ? t[r] + e.bias[r] : t[r];
-    if constexpr (EC == EC_SILU) {
-        // rows interleave gate / up: out[i] = silu(gate_i) * up_i
-        float g[R / 2], u[R / 2];
-#pragma unroll
-        for (int p = 0; p < R / 2; p++) { g[p] = v[2 * p]; u[p] = v[2 * p + 1]; }
-        const float y = silu_mul(pick<R / 2>(g, lane), pick<R / 2>(u, lane));
-        if (lane < R / 2 && row0 + 2u * (uint32_t)lane + 1u < N) out[row0 / 2 + (uint32_t)lane] = y;
+    if constexpr (EC == EC_SIMPLE || EC == EC_ARGMAX) {
+        if (lane % LB != 0 || row0 + (uint32_t)rl >= N) return;
+        float y = c;
+        if constexpr (EC == EC_SIMPLE) {
+            if (a.epi == EPI_RESID) y = spread<R>(e.res) + c;
+            else if (a.epi == EPI_GELU) y = gelu_pade(c);
+        }
+        out[row0 + rl] = y;
         return;
     }
-    if (lane != 0) return;
-    if constexpr (EC == EC_ARGMAX) {
-#pragma unroll
-        for (int r = 0; r < R; r++)
-            if (row0 + r < N) out[row0 + r] = v[r];
-    } else if constexpr (EC == EC_SIMPLE) {
-        const int epi = a.epi;
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            if (row0 + r >= N) break;
-            float y = v[r];
-            if (epi == EPI_RESID) y = e.res[r] + v[r];
-            else if (epi == EPI_GELU) y = gelu_pade(v[r]);
-            out[row0 + r] = y;
-        }
+    const float2 pr = R == 4 ? swap16(c, c) : swap32(c, c);   // lane 32p: rows 2p, 2p+1
+    const int p = lane >> 5;
+    if ((lane & 31) != 0 || p >= R / 2) return;
+    const uint32_t row = row0 + 2u * (uint32_t)p;
+    if (row + 1u >= N) return;
+    if constexpr (EC == EC_SILU) {
+        // rows interleave gate / up: out[i] = silu(gate_i) * up_i
+        out[row / 2] = silu_mul(pr.x, pr.y);
     } else {
         // rows [Q | K | V]: RoPE on Q and K pairs (RotaryEmbedding.cs:115-116); Q -> out,
         // K -> k_cache [kv_head][head_dim][ctx_stride] (dimension-major), V -> v_cache
         // [kv_head][ctx_stride][head_dim].
         const int d = a.d_model, kv = a.kv_dim, hd = a.head_dim, pos = e.pos;
-#pragma unroll
-        for (int p = 0; p < R / 2; p++) {
-            const int row = (int)row0 + 2 * p;
-            if (row + 1 >= (int)N) break;
-            float v0 = v[2 * p], v1 = v[2 * p + 1];
-            if (a.use_rope && row < d + kv) {
-                const float c = e.cs[p], s = e.sn[p];
-                const float t0 = v0 * c, t1 = v1 * s, t2 = v0 * s, t3 = v1 * c;
-                v0 = t0 - t1;
-                v1 = t2 + t3;
-            }
-            if (row < d) {
-                out[row] = v0;
-                out[row + 1] = v1;
-            } else if (row < d + kv) {
-                float *dst = a.k_cache + (int64_t)(row - d) * a.ctx_stride + pos;
-                dst[0] = v0;
-                dst[a.ctx_stride] = v1;
-            } else {
-                const int vr = row - d - kv;
-                float *dst = a.v_cache + ((int64_t)(vr / hd) * a.ctx_stride + pos) * hd + (vr % hd);
-                dst[0] = v0;
-                dst[1] = v1;
-            }
+        const int r = (int)row;
+        float v0 = pr.x, v1 = pr.y;
+        if (a.use_rope && r < d + kv) {
+            const float cs = pick<R / 2>(e.cs, p), sn = pick<R / 2>(e.sn, p);
+            const float t0 = v0 * cs, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * cs;
+            v0 = t0 - t1;
+            v1 = t2 + t3;
+        }
+        if (r < d) {
+            out[r] = v0;
+            out[r + 1] = v1;
+        } else if (r < d + kv) {
+            float *dst = a.k_cache + (int64_t)(r - d) * a.ctx_stride + pos;
+            dst[0] = v0;
+            dst[a.ctx_stride] = v1;
+        } else {
+            const int vr = r - d - kv;
+            float *dst = a.v_cache + ((int64_t)(vr / hd) * a.ctx_stride + pos) * hd + (vr % hd);
+            dst[0] = v0;
+            dst[1] = v1;
         }
     }
-}
-
-// Wave-uniform totals of R per-lane partials (DPP row sums + lane reads, no LDS).
-template <int R>
-__device__ __forceinline__ void wave_totals(const float *acc, float *t)
-{
-#pragma unroll
-    for (int r = 0; r < R; r++) t[r] = wave_sum_uniform(acc[r]);
 }
 
 // (v, i) beats (bv, bi): larger value, or equal value and lower index (NaN never wins).
@@ -357,34 +354,32 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
         }
     }
 
-    // 6. reduction across the wave, then across the S waves of the row group
-    float t[R];
-    wave_totals<R>(acc, t);
+    // 6. reduction across the wave (row r's total in lane block r), then across the S waves
+    // of the row group in a fixed order
+    constexpr int LB = 64 / R;
+    float c = wave_totals_t<R>(acc);
     if constexpr (S > 1) {
-        if (lane == 0) {
-#pragma unroll
-            for (int r = 0; r < R; r++) s_red[w][r] = t[r];
-        }
+        if (lane % LB == 0) s_red[w][lane / LB] = c;
         __syncthreads();
+        float v = s_red[grp * S][lane / LB];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            float v = s_red[grp * S][r];
-#pragma unroll
-            for (int s = 1; s < S; s++) v += s_red[grp * S + s][r];
-            t[r] = v;
-        }
+        for (int s = 1; s < S; s++) v += s_red[grp * S + s][lane / LB];
+        c = v;
     }
-    if (ws == 0 && row0 < N) epi_store<R, EC>(a, t, e, row0, N, my, lane);
+    if (a.bias) c += spread<R>(e.bias);   // in the first lane of each block
+    if (ws == 0 && row0 < N) epi_store<R, EC>(a, c, e, row0, N, my, lane);
     if constexpr (EC == EC_ARGMAX) {
         __shared__ float s_bv[4];
         __shared__ int s_bi[4];
+        float t[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) t[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), r * LB));
         if (ws == 0 && lane == 0) {
             float bv = -INFINITY;
             int bi = 0x7FFFFFFF;
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                const float v = a.bias ? t[r] + e.bias[r] : t[r];
-                if (row0 + r < N && am_better(v, (int)(row0 + r), bv, bi)) { bv = v; bi = (int)(row0 + r); }
+                if (row0 + r < N && am_better(t[r], (int)(row0 + r), bv, bi)) { bv = t[r]; bi = (int)(row0 + r); }
             }
             s_bv[grp] = bv;
             s_bi[grp] = bi;

@@ -154,6 +154,45 @@ __device__ __forceinline__ float wave_sum_uniform(float v)
     return (r0 + r1) + (r2 + r3);
 }
 
+// v_permlane32_swap_b32 (gfx950): lanes 32..63 of `a` trade places with lanes 0..31 of `b`;
+// .x is the new `a`, .y the new `b`.
+__device__ __forceinline__ float2 swap32(float a, float b)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// v_permlane16_swap_b32 (gfx950): the odd 16-lane rows of `a` trade places with the even rows
+// of `b`; .x is the new `a`, .y the new `b`.
+__device__ __forceinline__ float2 swap16(float a, float b)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Totals of R per-lane partials (R = 2 or 4) over the wave, transposed: row r's total ends up
+// in every lane of block r (lanes [r*64/R, (r+1)*64/R)).  The lane swaps fold the halves so
+// that each add combines two rows' partials at once, then each 16-lane row is summed with
+// DPP: 2 + R/2 swaps and adds plus 4 DPP adds, against 11 instructions per row for separate
+// wave sums.  All lanes must be active.
+template <int R>
+__device__ __forceinline__ float wave_totals_t(const float *acc)
+{
+    static_assert(R == 2 || R == 4, "two or four rows per wave");
+    float c;
+    if constexpr (R == 4) {
+        const float2 p0 = swap32(acc[0], acc[2]);   // lanes 0..31: row 0, 32..63: row 2
+        const float2 p1 = swap32(acc[1], acc[3]);   // lanes 0..31: row 1, 32..63: row 3
+        const float2 q = swap16(p0.x + p0.y, p1.x + p1.y);
+        c = q.x + q.y;                              // 16-lane rows: rows 0, 1, 2, 3
+    } else {
+        const float2 p = swap32(acc[0], acc[1]);    // lanes 0..31: row 0, 32..63: row 1
+        const float b = p.x + p.y;
+        const float2 q = swap16(b, b);
+        c = q.x + q.y;
+    }
+    return row16_sum(c);
+}
+
 __device__ __forceinline__ float wave_max(float v)
 {
 #pragma unroll
