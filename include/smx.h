@@ -117,6 +117,16 @@ SMX_API int smx_attention_decode(const float *q_dev, const float *k_cache_dev,
                                  const float *v_cache_dev, float *out_dev, int n_head,
                                  int n_kv_head, int head_dim, int ctx_stride, int n_pos,
                                  void *stream);
+/* Causal attention of n_tok consecutive query tokens at positions p_first .. p_first+n_tok-1
+ * over the KV cache: MultiHeadAttention.Forward with T > 1 (MultiHeadAttention.cs:206-297;
+ * scores :676-745, OptimizedOps.FusedScaleMaskSoftmax OptimizedOps.cs:39-93, W.V :810-845).
+ * q [n_tok][n_head][hd], k_cache [n_kv_head][hd][ctx_stride], v_cache
+ * [n_kv_head][ctx_stride][hd] holding positions 0 .. p_first+n_tok-1, out [n_tok][n_head][hd].
+ * head_dim 64; n_head / n_kv_head must divide 32. */
+SMX_API int smx_attention_prefill(const float *q_dev, const float *k_cache_dev,
+                                  const float *v_cache_dev, float *out_dev, int n_head,
+                                  int n_kv_head, int head_dim, int ctx_stride, int p_first,
+                                  int n_tok, void *stream);
 /* ActivationOps.FusedSiLUMul (src/SmallMind.Core/Simd/ActivationOps.cs:565-580). */
 SMX_API int smx_silu_mul(const float *gate_dev, const float *up_dev, float *y_dev, int64_t n,
                          void *stream);

@@ -24,7 +24,7 @@ EXPORTS = [
     "smx_type_row_bytes", "smx_dequant", "smx_quantize", "smx_fill_normal",
     "smx_weight_create", "smx_weight_info", "smx_weight_matmul", "smx_weight_to_float32",
     "smx_weight_destroy", "smx_rmsnorm", "smx_layernorm", "smx_rope_tables", "smx_rope",
-    "smx_scale_mask_softmax", "smx_attention_decode", "smx_silu_mul", "smx_gelu", "smx_argmax",
+    "smx_scale_mask_softmax", "smx_attention_decode", "smx_attention_prefill", "smx_silu_mul", "smx_gelu", "smx_argmax",
     "smx_context_create", "smx_context_destroy", "smx_model_create", "smx_model_upload_tensor",
     "smx_model_finalize", "smx_model_weight_bytes", "smx_model_destroy", "smx_session_create",
     "smx_session_forward", "smx_session_generate", "smx_batch_generate", "smx_session_reset",
@@ -93,6 +93,7 @@ def load() -> ctypes.CDLL:
         "smx_rope": (i32, [vp, i32, i32, i32, i32, vp, vp, vp]),
         "smx_scale_mask_softmax": (i32, [vp, f32, i32, i32, i32, vp]),
         "smx_attention_decode": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
+        "smx_attention_prefill": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
         "smx_silu_mul": (i32, [vp, vp, vp, i64, vp]),
         "smx_gelu": (i32, [vp, vp, i64, vp]),
         "smx_argmax": (i32, [vp, i32, vp, vp]),

@@ -539,10 +539,18 @@ int batch_alloc(const smx_model *m, TokBatch &B, int cap, int logits_rows)
     return SMX_OK;
 }
 
+// Tokens p_first .. p_first+M-1 of one session (a prefill chunk): attention runs as one causal
+// block over the session cache instead of per (token, head).
+struct PrefillRun {
+    const float *kc, *vc;
+    int p_first;
+};
+
 // Runs tokens 0..M-1 of B (ids, pos, kc, vc filled on the device) through every layer on the
 // matrix-core GEMM path, writing K/V into each token's cache; the final norm + head run on rows
 // head_from..M-1 into B.logits.  Same graph as enqueue_step, per token.
-int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_from, hipStream_t s)
+int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_from, hipStream_t s,
+               const PrefillRun *run)
 {
     const smx_model_config &c = m->cfg;
     const int d = c.d_model, hd = m->hd, Hkv = c.n_kv_head;
@@ -572,8 +580,12 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
         a.rope_cos = m->rope_cos;
         a.rope_sin = m->rope_sin;
         SMX_HIP(launch_qgemm(a, B.x, d, pro, L.d_attn_g, L.d_attn_b, c.norm_eps, s));
-        SMX_HIP(launch_attention_tokens(B.q, m->nqkv, B.kc, B.vc, layer_off, B.att, d, c.n_head, Hkv, hd,
-                                        ctx_stride, B.pos, M, s));
+        if (run && attention_prefill_supported(c.n_head, Hkv, hd))
+            SMX_HIP(launch_attention_prefill(B.q, m->nqkv, run->kc + layer_off, run->vc + layer_off, B.att, d,
+                                             c.n_head, Hkv, hd, ctx_stride, run->p_first, M, s));
+        else
+            SMX_HIP(launch_attention_tokens(B.q, m->nqkv, B.kc, B.vc, layer_off, B.att, d, c.n_head, Hkv, hd,
+                                            ctx_stride, B.pos, M, s));
         QgemmArgs o{};
         o.w = L.o.view();
         o.xp = B.xp;
@@ -645,7 +657,8 @@ int prefill_tokens(smx_session *S, const int32_t *tokens_host, int n, int p0, bo
         SMX_HIP(hipMemcpyAsync(B.ids, tokens_host + i0, (size_t)M * 4, hipMemcpyHostToDevice, s));
         SMX_HIP(hipMemcpyAsync(B.pos, pos.data(), (size_t)M * 4, hipMemcpyHostToDevice, s));
         const bool last = i0 + M == n;
-        int rc = run_tokens(m, B, M, S->max_ctx, (want_head && last) ? M - 1 : M, s);
+        const PrefillRun run{S->kc, S->vc, p0 + i0};
+        int rc = run_tokens(m, B, M, S->max_ctx, (want_head && last) ? M - 1 : M, s, &run);
         if (rc != SMX_OK) return rc;
         // the host arrays are reused by the next chunk: let this chunk's copies finish
         SMX_HIP(hipStreamSynchronize(s));
@@ -882,6 +895,23 @@ SMX_API int smx_attention_decode(const float *q, const float *kc, const float *v
     const hipError_t f = hipFreeAsync(scores, st);
     SMX_HIP(e);
     SMX_HIP(f);
+    return SMX_OK;
+}
+
+SMX_API int smx_attention_prefill(const float *q, const float *kc, const float *vc, float *out,
+                                  int n_head, int n_kv_head, int head_dim, int ctx_stride, int p_first,
+                                  int n_tok, void *stream)
+{
+    if (!q || !kc || !vc || !out) SMX_FAIL(SMX_EINVAL, "smx_attention_prefill: null pointer");
+    if (n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head)
+        SMX_FAIL(SMX_EINVAL, "smx_attention_prefill: n_head must be a multiple of n_kv_head");
+    if (!attention_prefill_supported(n_head, n_kv_head, head_dim))
+        SMX_FAIL(SMX_EUNSUPPORTED, "smx_attention_prefill: needs head_dim 64 and n_head / n_kv_head dividing 32");
+    if (n_tok <= 0 || p_first < 0 || (int64_t)p_first + n_tok > ctx_stride || ctx_stride > 1000000)
+        SMX_FAIL(SMX_EINVAL, "smx_attention_prefill: need 0 <= p_first, p_first + n_tok <= ctx_stride <= 1000000");
+    const int row = n_head * head_dim;
+    SMX_HIP(launch_attention_prefill(q, row, kc, vc, out, row, n_head, n_kv_head, head_dim, ctx_stride, p_first,
+                                     n_tok, (hipStream_t)stream));
     return SMX_OK;
 }
 
@@ -1395,7 +1425,7 @@ SMX_API int smx_batch_generate(smx_session *const *sessions, int n_sessions, con
     // capture one lockstep step: all layers for the n tokens, head, argmax (appends each
     // session's token at pos + 1 and advances pos on the device)
     SMX_BHIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    rc = run_tokens(m, D, n, max_ctx, 0, s);
+    rc = run_tokens(m, D, n, max_ctx, 0, s, nullptr);
     if (rc == SMX_OK) {
         const hipError_t e = launch_argmax_rows(D.logits, V, V, n, D.ids, D.pos, D.tok_arr, s);
         if (e != hipSuccess) { set_error(hipGetErrorString(e)); rc = SMX_EDEVICE; }

@@ -221,6 +221,13 @@ hipError_t launch_advance(int32_t *pos, hipStream_t s);
 // attention per (token, head) with per-token position and KV cache, argmax per logits row.
 hipError_t launch_embed_tokens(const WView &tok, const WView *posw, const int32_t *ids,
                                const int32_t *pos, float *x, int64_t x_stride, int M, hipStream_t s);
+// Causal attention of M consecutive tokens of one session at positions p_first .. (prefill
+// chunks) on the matrix cores: q [M][q_stride] (head h at h*hd), kc / vc the layer's cache
+// ([n_kv_head][hd][ctx_stride] / [n_kv_head][ctx_stride][hd]), out [M][out_stride].
+bool attention_prefill_supported(int n_head, int n_kv_head, int hd);
+hipError_t launch_attention_prefill(const float *q, int q_stride, const float *kc, const float *vc, float *out,
+                                    int out_stride, int n_head, int n_kv_head, int hd, int ctx_stride,
+                                    int p_first, int M, hipStream_t s);
 hipError_t launch_attention_tokens(const float *q, int64_t q_stride, float *const *kc_tok,
                                    float *const *vc_tok, int64_t layer_off, float *out,
                                    int64_t out_stride, int n_head, int n_kv_head, int hd,

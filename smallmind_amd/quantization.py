@@ -199,6 +199,16 @@ def attention_decode(q, k_cache, v_cache, n_head: int, n_kv_head: int, head_dim:
     return out
 
 
+def attention_prefill(q, k_cache, v_cache, n_head: int, n_kv_head: int, head_dim: int,
+                      ctx_stride: int, p_first: int, n_tok: int):
+    torch = _torch()
+    _require_cuda(q, k_cache, v_cache)
+    out = torch.empty(n_tok * n_head * head_dim, dtype=torch.float32, device=q.device)
+    call("smx_attention_prefill", _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), n_head,
+         n_kv_head, head_dim, ctx_stride, p_first, n_tok, _stream())
+    return out
+
+
 def silu_mul(gate, up):
     torch = _torch()
     _require_cuda(gate, up)

@@ -79,6 +79,36 @@ def test_attention_decode_vs_oracle(gpu, H, Hkv, hd, npos):
     assert rel_err(got.reshape(H, hd), ref) < 1e-5
 
 
+@pytest.mark.parametrize("H,Hkv,p0,n", [(32, 4, 0, 37), (32, 4, 300, 64), (12, 12, 5, 33),
+                                        (16, 1, 0, 20), (8, 8, 1000, 17), (4, 2, 0, 1),
+                                        (32, 32, 255, 256), (32, 4, 3840, 256), (2, 2, 16, 48)])
+def test_attention_prefill_vs_oracle(gpu, H, Hkv, p0, n):
+    """Causal attention of n tokens at positions p0.. over the cache (MultiHeadAttention T > 1).
+    Cache entries past the last token hold NaN: they must never reach the output."""
+    from smallmind_amd.quantization import attention_prefill
+    hd = 64
+    rng = np.random.default_rng(p0 * 7 + n)
+    ctx = p0 + n + 9
+    q = rng.normal(0, 1, (n, H, hd)).astype(np.float32)
+    kc = rng.normal(0, 1, (Hkv, ctx, hd)).astype(np.float32)
+    vc = rng.normal(0, 1, (Hkv, ctx, hd)).astype(np.float32)
+    kc[:, p0 + n:] = np.nan
+    vc[:, p0 + n:] = np.nan
+    kt = np.ascontiguousarray(kc.transpose(0, 2, 1))   # the backend keeps K dimension-major
+    got = attention_prefill(_dev(q), _dev(kt), _dev(vc), H, Hkv, hd, ctx, p0, n).cpu().numpy()
+    got = got.reshape(n, H, hd)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    ref = np.empty((n, H, hd), np.float32)
+    kl = p0 + n
+    for h in range(H):
+        kv = h // (H // Hkv)
+        sc = (q[:, h].astype(np.float64) @ kc[kv, :kl].astype(np.float64).T).astype(np.float32)
+        p = O.scale_mask_softmax(sc, float(scale), cache_off=p0)
+        ref[:, h] = p.astype(np.float64) @ vc[kv, :kl].astype(np.float64)
+    assert np.isfinite(got).all()
+    assert rel_err(got, ref) < 2e-5
+
+
 def test_silu_mul_gelu(gpu):
     from smallmind_amd.quantization import gelu, silu_mul
     rng = np.random.default_rng(1)
