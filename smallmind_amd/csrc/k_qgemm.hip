@@ -746,11 +746,20 @@ hipError_t launch_st(const QgemmArgs &a, hipStream_t s)
 template <int F>
 hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
 {
-    // Rows of whole 256-element super-blocks: LDS-staged weight tiles (16 or 32 rows per wave;
-    // tall matrices 32).  Up to 16 tokens: one token tile; more: 4 token tiles per workgroup.
+    // Rows of whole 256-element super-blocks: LDS-staged weight tiles.  Up to 16 tokens: one
+    // token tile per workgroup; more: tiles of 64 tokens x 32 rows per wave, 8 waves splitting
+    // long K (or short K over few rows), else 4 waves (K-quants: 64 rows x 32 tokens on tall
+    // matrices; Q6_K 16 rows).  Chosen by measurement over the prefill shapes of the five
+    // formats at 256 tokens.
     if (a.w.cols % 256 == 0) {
         const bool tall = a.w.rows >= 8192;
-        if (a.M > 16) return tall ? launch_st<F, 2, 4, 4>(a, s) : launch_st<F, 1, 4, 8>(a, s);
+        if (a.M > 16) {
+            if (a.w.cols > 4096 || a.w.rows <= 2048) return launch_st<F, 2, 4, 8>(a, s);
+            if constexpr (F == FMT_Q4_K || F == FMT_Q5_K)
+                if (tall) return launch_st<F, 4, 2, 4>(a, s);
+            if constexpr (F == FMT_Q6_K) return launch_st<F, 1, 4, 8>(a, s);
+            return launch_st<F, 2, 4, 4>(a, s);
+        }
         return tall ? launch_st<F, 2, 1, 4>(a, s) : launch_st<F, 1, 1, 8>(a, s);
     }
     // Up to 16 tokens: one token tile, 16 waves per workgroup splitting K, 4 sub-blocks per
