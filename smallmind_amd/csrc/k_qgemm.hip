@@ -636,10 +636,46 @@ __device__ __forceinline__ uint32_t bf16_rne(float f)
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+// Parts and stores of one item (8 elements of sub-block s, group g) of token row t of tile tt.
+__device__ __forceinline__ void qprep_store(const float *v, uint8_t *__restrict__ xp, int nsb, int tt, int t, int i)
+{
+    const int s = i >> 2, g = i & 3;
+    uint32_t part[3][8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float f = v[k];
+        const uint32_t h = bf16_rne(f);
+        const float r1 = f - __uint_as_float(h << 16);
+        const uint32_t mm = bf16_rne(r1);
+        const float r2 = r1 - __uint_as_float(mm << 16);
+        part[0][k] = h;
+        part[1][k] = mm;
+        part[2][k] = bf16_rne(r2);
+    }
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+        // pair q = (element q, element q + 4)
+        uint4 o;
+        o.x = part[p][0] | (part[p][4] << 16);
+        o.y = part[p][1] | (part[p][5] << 16);
+        o.z = part[p][2] | (part[p][6] << 16);
+        o.w = part[p][3] | (part[p][7] << 16);
+        *(uint4 *)(xp + (((size_t)tt * nsb + s) * 3 + p) * 1024 + (g * 16 + t) * 16) = o;
+    }
+}
+
+__device__ __forceinline__ void unpack8(const float4 &a, const float4 &b, float *v)
+{
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
 // One workgroup per token (rows M..Mp-1 of the last tile are zero): the norm statistic of the
 // row (RMSNorm: RMSNormOps.cs:114; LayerNorm: LayerNormOps.cs:92-119), the normalised value in
 // the reference's operation order (gamma * (x * invRms); fma(gamma, (x - mean) * invStd, beta)),
-// then its three bf16 parts at Xp[m/16][s][p][g][m%16][perm].
+// then its three bf16 parts at Xp[m/16][s][p][g][m%16][perm].  Thread j holds items j + 256 u
+// (u < IPT, K <= 2048 * IPT): the row, gamma and beta are loaded in one batch before the
+// statistic, so the kernel makes one round trip to memory.
+template <int IPT>
 __global__ __launch_bounds__(256) void k_qprep(const float *__restrict__ x, int64_t x_stride, int M, int K,
                                                int pro, const float *__restrict__ gamma,
                                                const float *__restrict__ beta, float eps,
@@ -648,53 +684,144 @@ __global__ __launch_bounds__(256) void k_qprep(const float *__restrict__ x, int6
     __shared__ float red[16];
     const int m = blockIdx.x;
     const int nsb = K >> 5, items = K >> 3;   // item = 8 elements (sub-block s, group g)
+    const int tt = m >> 4, t = m & 15;
+    const float *xr = x + (int64_t)m * x_stride;
+    const int tid = threadIdx.x;
+    if (m >= M) {   // padding row of the last tile
+        float z[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = tid; i < items; i += 256) qprep_store(z, xp, nsb, tt, t, i);
+        return;
+    }
+    float4 xa[IPT][2], ga[IPT][2], ba[IPT][2];
+#pragma unroll
+    for (int u = 0; u < IPT; u++) {
+        const int i = tid + 256 * u;
+        if (i < items) {
+            xa[u][0] = ((const float4 *)xr)[2 * i];
+            xa[u][1] = ((const float4 *)xr)[2 * i + 1];
+            if (pro != PRO_NONE) {
+                ga[u][0] = ((const float4 *)gamma)[2 * i];
+                ga[u][1] = ((const float4 *)gamma)[2 * i + 1];
+            }
+            if (pro == PRO_LN) {
+                ba[u][0] = ((const float4 *)beta)[2 * i];
+                ba[u][1] = ((const float4 *)beta)[2 * i + 1];
+            }
+        }
+    }
+    float sc = 1.0f, mean = 0.0f;
+    if (pro == PRO_RMS) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < IPT; u++)
+            if (tid + 256 * u < items) {
+                float v[8];
+                unpack8(xa[u][0], xa[u][1], v);
+#pragma unroll
+                for (int k = 0; k < 8; k++) { const float q = v[k] * v[k]; ss += q; }
+            }
+        ss = block_sum<4>(ss, red);
+        sc = 1.0f / sqrtf(ss / (float)K + eps);
+    } else if (pro == PRO_LN) {
+        float tsum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < IPT; u++)
+            if (tid + 256 * u < items) {
+                float v[8];
+                unpack8(xa[u][0], xa[u][1], v);
+#pragma unroll
+                for (int k = 0; k < 8; k++) tsum += v[k];
+            }
+        mean = block_sum<4>(tsum, red) / (float)K;
+        float sq = 0.0f;
+#pragma unroll
+        for (int u = 0; u < IPT; u++)
+            if (tid + 256 * u < items) {
+                float v[8];
+                unpack8(xa[u][0], xa[u][1], v);
+#pragma unroll
+                for (int k = 0; k < 8; k++) { const float dd = v[k] - mean; const float q = dd * dd; sq += q; }
+            }
+        sq = block_sum<4>(sq, red);
+        sc = 1.0f / sqrtf(sq / (float)K + eps);
+    }
+#pragma unroll
+    for (int u = 0; u < IPT; u++) {
+        const int i = tid + 256 * u;
+        if (i >= items) continue;
+        float v[8];
+        unpack8(xa[u][0], xa[u][1], v);
+        if (pro == PRO_RMS) {
+            float gg[8];
+            unpack8(ga[u][0], ga[u][1], gg);
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = gg[k] * (v[k] * sc);
+        } else if (pro == PRO_LN) {
+            float gg[8], be[8];
+            unpack8(ga[u][0], ga[u][1], gg);
+            unpack8(ba[u][0], ba[u][1], be);
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = __builtin_fmaf(gg[k], (v[k] - mean) * sc, be[k]);
+        }
+        qprep_store(v, xp, nsb, tt, t, i);
+    }
+}
+
+// Rows longer than 2048 * 4: the same with the row read twice in loops.
+__global__ __launch_bounds__(256) void k_qprep_long(const float *__restrict__ x, int64_t x_stride, int M, int K,
+                                                    int pro, const float *__restrict__ gamma,
+                                                    const float *__restrict__ beta, float eps,
+                                                    uint8_t *__restrict__ xp)
+{
+    __shared__ float red[16];
+    const int m = blockIdx.x;
+    const int nsb = K >> 5, items = K >> 3;
     const float *xr = x + (int64_t)m * x_stride;
     const bool live = m < M;
     float sc = 1.0f, mean = 0.0f;
     if (live && pro == PRO_RMS) {
         float ss = 0.0f;
         for (int i = threadIdx.x; i < items; i += 256) {
-            const float4 a = ((const float4 *)xr)[2 * i], b = ((const float4 *)xr)[2 * i + 1];
-            float q;
-            q = a.x * a.x; ss += q; q = a.y * a.y; ss += q; q = a.z * a.z; ss += q; q = a.w * a.w; ss += q;
-            q = b.x * b.x; ss += q; q = b.y * b.y; ss += q; q = b.z * b.z; ss += q; q = b.w * b.w; ss += q;
+            float v[8];
+            unpack8(((const float4 *)xr)[2 * i], ((const float4 *)xr)[2 * i + 1], v);
+#pragma unroll
+            for (int k = 0; k < 8; k++) { const float q = v[k] * v[k]; ss += q; }
         }
         ss = block_sum<4>(ss, red);
         sc = 1.0f / sqrtf(ss / (float)K + eps);
     } else if (live && pro == PRO_LN) {
-        float t = 0.0f;
+        float tsum = 0.0f;
         for (int i = threadIdx.x; i < items; i += 256) {
-            const float4 a = ((const float4 *)xr)[2 * i], b = ((const float4 *)xr)[2 * i + 1];
-            t += a.x; t += a.y; t += a.z; t += a.w; t += b.x; t += b.y; t += b.z; t += b.w;
+            float v[8];
+            unpack8(((const float4 *)xr)[2 * i], ((const float4 *)xr)[2 * i + 1], v);
+#pragma unroll
+            for (int k = 0; k < 8; k++) tsum += v[k];
         }
-        mean = block_sum<4>(t, red) / (float)K;
+        mean = block_sum<4>(tsum, red) / (float)K;
         float sq = 0.0f;
         for (int i = threadIdx.x; i < items; i += 256) {
-            const float4 a = ((const float4 *)xr)[2 * i], b = ((const float4 *)xr)[2 * i + 1];
-            const float e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            float v[8];
+            unpack8(((const float4 *)xr)[2 * i], ((const float4 *)xr)[2 * i + 1], v);
 #pragma unroll
-            for (int k = 0; k < 8; k++) { const float dd = e[k] - mean; const float q = dd * dd; sq += q; }
+            for (int k = 0; k < 8; k++) { const float dd = v[k] - mean; const float q = dd * dd; sq += q; }
         }
         sq = block_sum<4>(sq, red);
         sc = 1.0f / sqrtf(sq / (float)K + eps);
     }
     const int tt = m >> 4, t = m & 15;
     for (int i = threadIdx.x; i < items; i += 256) {
-        const int s = i >> 2, g = i & 3;
         float v[8];
         if (live) {
-            const float4 a = ((const float4 *)xr)[2 * i], b = ((const float4 *)xr)[2 * i + 1];
-            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+            unpack8(((const float4 *)xr)[2 * i], ((const float4 *)xr)[2 * i + 1], v);
             if (pro == PRO_RMS) {
-                const float4 ga = ((const float4 *)gamma)[2 * i], gb = ((const float4 *)gamma)[2 * i + 1];
-                const float gg[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+                float gg[8];
+                unpack8(((const float4 *)gamma)[2 * i], ((const float4 *)gamma)[2 * i + 1], gg);
 #pragma unroll
                 for (int k = 0; k < 8; k++) v[k] = gg[k] * (v[k] * sc);
             } else if (pro == PRO_LN) {
-                const float4 ga = ((const float4 *)gamma)[2 * i], gb = ((const float4 *)gamma)[2 * i + 1];
-                const float4 ba = ((const float4 *)beta)[2 * i], bb = ((const float4 *)beta)[2 * i + 1];
-                const float gg[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
-                const float be[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
+                float gg[8], be[8];
+                unpack8(((const float4 *)gamma)[2 * i], ((const float4 *)gamma)[2 * i + 1], gg);
+                unpack8(((const float4 *)beta)[2 * i], ((const float4 *)beta)[2 * i + 1], be);
 #pragma unroll
                 for (int k = 0; k < 8; k++) v[k] = __builtin_fmaf(gg[k], (v[k] - mean) * sc, be[k]);
             }
@@ -702,28 +829,7 @@ __global__ __launch_bounds__(256) void k_qprep(const float *__restrict__ x, int6
 #pragma unroll
             for (int k = 0; k < 8; k++) v[k] = 0.0f;
         }
-        uint32_t part[3][8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const float f = v[k];
-            const uint32_t h = bf16_rne(f);
-            const float r1 = f - __uint_as_float(h << 16);
-            const uint32_t mm = bf16_rne(r1);
-            const float r2 = r1 - __uint_as_float(mm << 16);
-            part[0][k] = h;
-            part[1][k] = mm;
-            part[2][k] = bf16_rne(r2);
-        }
-#pragma unroll
-        for (int p = 0; p < 3; p++) {
-            // pair q = (element q, element q + 4)
-            uint4 o;
-            o.x = part[p][0] | (part[p][4] << 16);
-            o.y = part[p][1] | (part[p][5] << 16);
-            o.z = part[p][2] | (part[p][6] << 16);
-            o.w = part[p][3] | (part[p][7] << 16);
-            *(uint4 *)(xp + (((size_t)tt * nsb + s) * 3 + p) * 1024 + (g * 16 + t) * 16) = o;
-        }
+        qprep_store(v, xp, nsb, tt, t, i);
     }
 }
 
@@ -784,8 +890,16 @@ hipError_t launch_qgemm(const QgemmArgs &a, const float *x, int64_t x_stride, in
         return hipErrorInvalidValue;
     const int K = (int)a.w.cols;
     const unsigned mp = (unsigned)((a.M + 15) / 16 * 16);
-    hipLaunchKernelGGL(k_qprep, dim3(mp), dim3(256), 0, s, x, x_stride, a.M, K, pro, gamma, beta, eps,
-                       (uint8_t *)a.xp);
+    const int ipt = (K / 8 + 255) / 256;
+#define SMX_QPREP(KN) hipLaunchKernelGGL(KN, dim3(mp), dim3(256), 0, s, x, x_stride, a.M, K, pro, gamma, beta, eps, (uint8_t *)a.xp)
+    switch (ipt) {
+    case 1: SMX_QPREP(k_qprep<1>); break;
+    case 2: SMX_QPREP(k_qprep<2>); break;
+    case 3: SMX_QPREP(k_qprep<3>); break;
+    case 4: SMX_QPREP(k_qprep<4>); break;
+    default: SMX_QPREP(k_qprep_long); break;
+    }
+#undef SMX_QPREP
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     switch (a.w.fmt) {
