@@ -157,21 +157,22 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     }
 }
 
-template <int HD, int U>
-__global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ scores, const float *__restrict__ vc,
-                                                 float *__restrict__ out, int n_head, int n_kv_head,
-                                                 int ctx_stride, int sc_stride, const int32_t *__restrict__ pos_dev,
-                                                 int n_pos_fixed)
+template <int HD, int U, int NT>
+__global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores, const float *__restrict__ vc,
+                                                float *__restrict__ out, int n_head, int n_kv_head,
+                                                int ctx_stride, int sc_stride, const int32_t *__restrict__ pos_dev,
+                                                int n_pos_fixed)
 {
+    constexpr int NW = NT / 64;         // waves
     constexpr int NS = HD / kPvSlice;   // slices per head
     constexpr int C4 = kPvSlice / 4;    // float4 columns per slice
-    constexpr int PL = 256 / C4;        // position lanes
+    constexpr int PL = NT / C4;         // position lanes
     // U: consecutive positions per lane in the first batch (sized by the launcher to the
     // session's context, so the first batch loads no rows past it)
     constexpr int NB = PL * U;          // positions of the first batch
     extern __shared__ float p[];        // [n_pos], only for n_pos > NB
-    __shared__ float red[4];
-    __shared__ float4 part[4][C4];
+    __shared__ float red[16];
+    __shared__ float4 part[NW][C4];
     // Workgroups are dealt to the 8 XCDs round-robin; consecutive (head, slice) indices are
     // grouped per XCD so that the query heads of one KV head share that XCD's L2.
     const int T = n_head * NS, b = blockIdx.x;
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ score
 #pragma unroll
         for (int u = 0; u < U; u++)
             if (j0 + u < n_pos) mx = fmaxf(mx, sv[u]);
-        mx = block_max<4>(mx, red);
+        mx = block_max<NW>(mx, red);
         float e[UQ], sum = 0.0f;
 #pragma unroll
         for (int k = 0; k < UQ; k++) {
@@ -226,7 +227,7 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ score
             e[k] = j0 + u < n_pos ? fastexp(sk - mx) : 0.0f;
             sum += e[k];
         }
-        sum = block_sum<4>(sum, red);
+        sum = block_sum<NW>(sum, red);
         const float inv = 1.0f / sum;
 #pragma unroll
         for (int k = 0; k < UQ; k++) {
@@ -240,29 +241,29 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ score
         // long contexts: the scores of all positions pass through LDS, loaded in batches of
         // eight per thread (all loads of a batch in flight before any is used)
         float mx = -INFINITY;
-        for (int jb = tid; jb < n_pos; jb += 256 * 8) {
+        for (int jb = tid; jb < n_pos; jb += NT * 8) {
             float sb[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) sb[u] = srow[min(jb + 256 * u, sc_stride - 1)];
+            for (int u = 0; u < 8; u++) sb[u] = srow[min(jb + NT * u, sc_stride - 1)];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                const int j = jb + 256 * u;
+                const int j = jb + NT * u;
                 if (j < n_pos) {
                     p[j] = sb[u];
                     mx = fmaxf(mx, sb[u]);
                 }
             }
         }
-        mx = block_max<4>(mx, red);
+        mx = block_max<NW>(mx, red);
         float sum = 0.0f;
-        for (int j = tid; j < n_pos; j += 256) {
+        for (int j = tid; j < n_pos; j += NT) {
             const float e = fastexp(p[j] - mx);
             p[j] = e;
             sum += e;
         }
-        sum = block_sum<4>(sum, red);
+        sum = block_sum<NW>(sum, red);
         const float inv = 1.0f / sum;
-        for (int j = tid; j < n_pos; j += 256) p[j] = p[j] * inv;
+        for (int j = tid; j < n_pos; j += NT) p[j] = p[j] * inv;
         __syncthreads();
 #pragma unroll
         for (int u = 0; u < U; u++) pu[u] = p[j0 + u];   // j0 + u < NB < n_pos
@@ -323,7 +324,7 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float *__restrict__ score
     if (tid < C4) {
         float4 o = part[0][tid];
 #pragma unroll
-        for (int i = 1; i < 4; i++) {
+        for (int i = 1; i < NW; i++) {
             const float4 v = part[i][tid];
             o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
         }
@@ -653,23 +654,23 @@ hipError_t launch_softmax(float *scores, float scale, int seq, int k_seq, int ca
     return hipGetLastError();
 }
 
-template <int HD, int U>
+template <int HD, int U, int NT>
 hipError_t launch_pv(dim3 g2, size_t p_lds, const float *scores, const float *vc, float *out, int n_head,
                      int n_kv_head, int ctx_stride, int sc_stride, const int32_t *pos_dev, int n_pos_fixed,
                      hipStream_t s)
 {
-    const void *fp = (const void *)k_attn_pv<HD, U>;
+    const void *fp = (const void *)k_attn_pv<HD, U, NT>;
     if (p_lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(fp, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p_lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((k_attn_pv<HD, U>), g2, dim3(256), p_lds, s, scores, vc, out, n_head, n_kv_head, ctx_stride,
-                       sc_stride, pos_dev, n_pos_fixed);
+    hipLaunchKernelGGL((k_attn_pv<HD, U, NT>), g2, dim3(NT), p_lds, s, scores, vc, out, n_head, n_kv_head,
+                       ctx_stride, sc_stride, pos_dev, n_pos_fixed);
     return hipGetLastError();
 }
 
 template <int HD>
-hipError_t launch_attn_hd(dim3 g1, dim3 g2, size_t q_lds, size_t p_lds, int U, const float *q, const float *kc,
+hipError_t launch_attn_hd(dim3 g1, dim3 g2, size_t q_lds, size_t p_lds, int U, int NT, const float *q, const float *kc,
                           const float *vc, float *out, float *scores, int n_head, int n_kv_head, int ctx_stride,
                           int sc_stride, const int32_t *pos_dev, int n_pos_fixed, int nblk, hipStream_t s)
 {
@@ -677,12 +678,21 @@ hipError_t launch_attn_hd(dim3 g1, dim3 g2, size_t q_lds, size_t p_lds, int U, c
                        sc_stride, pos_dev, n_pos_fixed, nblk);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    switch (U) {
-    case 4: return launch_pv<HD, 4>(g2, p_lds, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, s);
-    case 8: return launch_pv<HD, 8>(g2, p_lds, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, s);
-    case 12: return launch_pv<HD, 12>(g2, p_lds, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, s);
-    default: return launch_pv<HD, 16>(g2, p_lds, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, s);
+#define SMX_PV(U_, NT_) launch_pv<HD, U_, NT_>(g2, p_lds, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, s)
+    if (NT == 256) {
+        switch (U) {
+        case 4: return SMX_PV(4, 256);
+        case 8: return SMX_PV(8, 256);
+        case 12: return SMX_PV(12, 256);
+        default: return SMX_PV(16, 256);
+        }
     }
+    switch (U) {
+    case 16: return SMX_PV(16, 512);
+    case 24: return SMX_PV(24, 512);
+    default: return SMX_PV(36, 512);
+    }
+#undef SMX_PV
 }
 
 size_t attention_scores_floats(int n_head, int max_pos) { return (size_t)n_head * ((max_pos + 3) & ~3); }
@@ -699,12 +709,17 @@ hipError_t launch_attention_split(const float *q, const float *kc, const float *
     const size_t q_lds = (size_t)G * hd * 4, p_lds = (size_t)max_pos * 4;
     if (q_lds > 64 * 1024 || p_lds > 160 * 1024) return hipErrorInvalidValue;
     const dim3 g1((unsigned)(n_kv_head * nblk)), g2((unsigned)(n_head * (hd / kPvSlice)));
-    const int U = max_pos <= 256 ? 4 : max_pos <= 512 ? 8 : max_pos <= 768 ? 12 : 16;
+    // positions per lane sized to the session context so that every V row of the context is
+    // loaded in the first batch, all of its loads in flight: 256 threads (64 position lanes)
+    // up to 1024 positions, 512 threads (128 position lanes) up to 4608
+    const int NT = max_pos <= 1024 ? 256 : 512;
+    const int U = max_pos <= 256 ? 4 : max_pos <= 512 ? 8 : max_pos <= 768 ? 12 : max_pos <= 1024 ? 16
+                : max_pos <= 2048 ? 16 : max_pos <= 3072 ? 24 : 36;
     switch (hd) {
-    case 16: return launch_attn_hd<16>(g1, g2, q_lds, p_lds, U, q, kc, vc, out, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk, s);
-    case 32: return launch_attn_hd<32>(g1, g2, q_lds, p_lds, U, q, kc, vc, out, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk, s);
-    case 64: return launch_attn_hd<64>(g1, g2, q_lds, p_lds, U, q, kc, vc, out, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk, s);
-    case 128: return launch_attn_hd<128>(g1, g2, q_lds, p_lds, U, q, kc, vc, out, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk, s);
+    case 16: return launch_attn_hd<16>(g1, g2, q_lds, p_lds, U, NT, q, kc, vc, out, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk, s);
+    case 32: return launch_attn_hd<32>(g1, g2, q_lds, p_lds, U, NT, q, kc, vc, out, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk, s);
+    case 64: return launch_attn_hd<64>(g1, g2, q_lds, p_lds, U, NT, q, kc, vc, out, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk, s);
+    case 128: return launch_attn_hd<128>(g1, g2, q_lds, p_lds, U, NT, q, kc, vc, out, scores, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed, nblk, s);
     default: return hipErrorInvalidValue;
     }
 }

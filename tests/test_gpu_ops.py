@@ -59,7 +59,8 @@ def test_scale_mask_softmax(gpu, seq, kseq, off):
 @pytest.mark.parametrize("H,Hkv,hd,npos", [(32, 4, 64, 1), (32, 4, 64, 513), (12, 12, 64, 160),
                                            (32, 32, 64, 300), (8, 2, 128, 1000), (32, 4, 64, 4096),
                                            (12, 4, 32, 33), (16, 1, 16, 95), (4, 4, 128, 31),
-                                           (16, 2, 64, 767)])
+                                           (16, 2, 64, 767), (32, 4, 64, 1500), (8, 8, 64, 2500),
+                                           (32, 4, 64, 4608), (4, 2, 64, 5000)])
 def test_attention_decode_vs_oracle(gpu, H, Hkv, hd, npos):
     from smallmind_amd.quantization import attention_decode
     rng = np.random.default_rng(npos)
