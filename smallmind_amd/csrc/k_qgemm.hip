@@ -216,6 +216,31 @@ template <> struct QW<FMT_Q6_K> {
 };
 
 constexpr uint4 kZero4 = {0u, 0u, 0u, 0u};
+
+// acc + sc * (C - off * sum x) - m * sum x as two fused steps: acc + sc*C - (sc*off + m) * sum x
+// (cs = sc * off + m precomputed per row and sub-block).
+// Activation part p of (token tile tt, sub-block s) for this lane: a wave-uniform base plus the
+// lane's 32-bit byte offset, so each load is one scalar-base instruction with no per-lane
+// 64-bit address arithmetic.
+__device__ __forceinline__ uint4 ld_part(const uint8_t *xp, int tt, int nsb, int s, int p, uint32_t lane16)
+{
+    const uint8_t *base = xp + (((size_t)tt * nsb + s) * 3 + p) * 1024;
+    return *(const uint4 *)(base + lane16);
+}
+
+__device__ __forceinline__ float accumulate1(float acc, float sc, float cs, float c, float sx)
+{
+    return __builtin_fmaf(sc, c, __builtin_fmaf(-cs, sx, acc));
+}
+// Two 16-element halves with their own scales (Q6_K): acc + sc*(Ca - off*sa) + sc2*(Cb - off*sb).
+__device__ __forceinline__ float accumulate2(float acc, float sc, float sc2, float ca, float cb, float sa, float sb,
+                                             float off)
+{
+    acc = __builtin_fmaf(-(sc * off), sa, acc);
+    acc = __builtin_fmaf(-(sc2 * off), sb, acc);
+    acc = __builtin_fmaf(sc, ca, acc);
+    return __builtin_fmaf(sc2, cb, acc);
+}
 constexpr uint32_t kOnes = 0x3F803F80u;   // bf16 1.0 pair
 
 // Epilogue of one output value per (token, weight row); all lanes of the wave must call it
@@ -278,6 +303,7 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm(QgemmArgs a)
     const int wv = wave_id();
     const int lane = lane_id();
     const int g = lane >> 4, li = lane & 15;
+    const uint32_t lane16 = (uint32_t)lane * 16u;
     const uint32_t N = (uint32_t)w.rows;
     const int nsb = (int)(w.cols >> 5);
     const uint32_t row_base = blockIdx.x * (16 * RT);
@@ -314,7 +340,7 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm(QgemmArgs a)
                 const int tt = tt0 + t < ntt ? tt0 + t : ntt - 1;
 #pragma unroll
                 for (int p = 0; p < 3; p++)
-                    xa[u][t][p] = *(const uint4 *)(xp + (((size_t)tt * nsb + s) * 3 + p) * 1024 + lane * 16);
+                    xa[u][t][p] = ld_part(xp, tt, nsb, s, p, lane16);
             }
 #pragma unroll
             for (int r = 0; r < RT; r++) raw[u][r] = Q::load(w, wrow[r], s, g);
@@ -353,14 +379,15 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm(QgemmArgs a)
                         }
 #pragma unroll
                         for (int i = 0; i < 4; i++)
-                            acc[r][t][i] += ok * (sc[r].sc * (da[i] - Q::kOff * sa[i]) + sc[r].sc2 * (db[i] - Q::kOff * sb[i]));
+                            acc[r][t][i] = accumulate2(acc[r][t][i], ok * sc[r].sc, ok * sc[r].sc2, da[i], db[i], sa[i], sb[i],
+                                                       Q::kOff);
                     } else {
                         f32x4 dc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                         for (int p = 0; p < 3; p++) dc = mfma(xa[u][t][p], wc[r], dc);
+                        const float c = ok * sc[r].sc, cs = ok * (sc[r].sc * Q::kOff + sc[r].m);
 #pragma unroll
-                        for (int i = 0; i < 4; i++)
-                            acc[r][t][i] += ok * (sc[r].sc * (dc[i] - Q::kOff * sa[i]) - sc[r].m * sa[i]);
+                        for (int i = 0; i < 4; i++) acc[r][t][i] = accumulate1(acc[r][t][i], c, cs, dc[i], sa[i]);
                     }
                 }
             }
@@ -459,6 +486,7 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
     const int wv = wave_id();
     const int lane = lane_id();
     const int g = lane >> 4, li = lane & 15;
+    const uint32_t lane16 = (uint32_t)lane * 16u;
     const uint32_t N = (uint32_t)w.rows;
     const int nsb = (int)(w.cols >> 5), nsup = nsb >> 3;
     const uint32_t row_base = blockIdx.x * R16;
@@ -551,7 +579,7 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
                     const int tt = tt0 + t < ntt ? tt0 + t : ntt - 1;
 #pragma unroll
                     for (int p = 0; p < 3; p++)
-                        xa[u][t][p] = *(const uint4 *)(xp + (((size_t)tt * nsb + s) * 3 + p) * 1024 + lane * 16);
+                        xa[u][t][p] = ld_part(xp, tt, nsb, s, p, lane16);
                 }
             }
 #pragma unroll
@@ -586,14 +614,15 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
                             }
 #pragma unroll
                             for (int i = 0; i < 4; i++)
-                                acc[r][t][i] += sc[r].sc * (da[i] - Q::kOff * sa[i]) + sc[r].sc2 * (db[i] - Q::kOff * sb[i]);
+                                acc[r][t][i] = accumulate2(acc[r][t][i], sc[r].sc, sc[r].sc2, da[i], db[i], sa[i], sb[i],
+                                                           Q::kOff);
                         } else {
                             f32x4 dc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                             for (int p = 0; p < 3; p++) dc = mfma(xa[u][t][p], wc[r], dc);
+                            const float c = sc[r].sc, cs = sc[r].sc * Q::kOff + sc[r].m;
 #pragma unroll
-                            for (int i = 0; i < 4; i++)
-                                acc[r][t][i] += sc[r].sc * (dc[i] - Q::kOff * sa[i]) - sc[r].m * sa[i];
+                            for (int i = 0; i < 4; i++) acc[r][t][i] = accumulate1(acc[r][t][i], c, cs, dc[i], sa[i]);
                         }
                     }
                 }
