@@ -564,7 +564,7 @@ template <int HD>
 __global__ __launch_bounds__(AttnCfg<HD>::NT) void k_attention_tokens(
     const float *__restrict__ q, int64_t q_stride, float *const *__restrict__ kc_tok,
     float *const *__restrict__ vc_tok, int64_t layer_off, float *__restrict__ out, int64_t out_stride,
-    int n_head, int n_kv_head, int ctx_stride, const int32_t *__restrict__ tok_pos)
+    int n_head, int n_kv_head, int ctx_stride, const int32_t *__restrict__ tok_pos, uint8_t *__restrict__ out_parts)
 {
     constexpr int NT = AttnCfg<HD>::NT;
     extern __shared__ float4 smem4[];
@@ -576,7 +576,8 @@ __global__ __launch_bounds__(AttnCfg<HD>::NT) void k_attention_tokens(
     const int64_t off = layer_off + (int64_t)kvh * ctx_stride * HD;
     attention_head<HD, NT, AttnCfg<HD>::U>(q + (int64_t)t * q_stride + (int64_t)h * HD, kc_tok[t] + off,
                                            vc_tok[t] + off, out + (int64_t)t * out_stride + (int64_t)h * HD,
-                                           n_pos, ctx_stride, (float *)smem4, sm);
+                                           n_pos, ctx_stride, (float *)smem4, sm, out_parts, n_head * HD / 32, t,
+                                           h * HD);
 }
 
 // Argmax of each row of logits [M][n] (lowest index on ties); with `tok_arr`, appends the
@@ -781,8 +782,10 @@ hipError_t launch_embed_tokens(const WView &tok, const WView *posw, const int32_
 hipError_t launch_attention_tokens(const float *q, int64_t q_stride, float *const *kc_tok,
                                    float *const *vc_tok, int64_t layer_off, float *out,
                                    int64_t out_stride, int n_head, int n_kv_head, int hd,
-                                   int ctx_stride, const int32_t *tok_pos, int M, hipStream_t s)
+                                   int ctx_stride, const int32_t *tok_pos, int M, hipStream_t s,
+                                   uint8_t *out_parts)
 {
+    if (out_parts && (n_head * hd) % 32) return hipErrorInvalidValue;
     const size_t lds = (size_t)ctx_stride * 4;
     const void *fn = nullptr;
     switch (hd) {
@@ -797,7 +800,7 @@ hipError_t launch_attention_tokens(const float *q, int64_t q_stride, float *cons
         if (e != hipSuccess) return e;
     }
     const dim3 grid((unsigned)n_head, (unsigned)M);
-#define SMX_ATT_T(HD) hipLaunchKernelGGL(k_attention_tokens<HD>, grid, dim3(AttnCfg<HD>::NT), lds, s, q, q_stride, kc_tok, vc_tok, layer_off, out, out_stride, n_head, n_kv_head, ctx_stride, tok_pos)
+#define SMX_ATT_T(HD) hipLaunchKernelGGL(k_attention_tokens<HD>, grid, dim3(AttnCfg<HD>::NT), lds, s, q, q_stride, kc_tok, vc_tok, layer_off, out, out_stride, n_head, n_kv_head, ctx_stride, tok_pos, out_parts)
     switch (hd) {
     case 16: SMX_ATT_T(16); break;
     case 32: SMX_ATT_T(32); break;

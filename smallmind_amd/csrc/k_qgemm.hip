@@ -256,10 +256,17 @@ __device__ __forceinline__ void qgemm_epilogue(const QgemmArgs &a, float v, uint
     switch (a.epi) {
     case EPI_STORE: yr[row] = v; break;
     case EPI_RESID: yr[row] = yr[row] + v; break;
-    case EPI_GELU: yr[row] = gelu_pade(v); break;
+    case EPI_GELU:
+        if (a.yp) xp_store(a.yp, (int)(N >> 5), tok, (int)row, gelu_pade(v));
+        else yr[row] = gelu_pade(v);
+        break;
     case EPI_SILU:
         // rows interleave gate / up: out[i] = silu(gate_i) * up_i
-        if (!(row & 1)) yr[row >> 1] = silu_mul(v, nb);
+        if (!(row & 1)) {
+            const float y = silu_mul(v, nb);
+            if (a.yp) xp_store(a.yp, (int)(N >> 6), tok, (int)(row >> 1), y);
+            else yr[row >> 1] = y;
+        }
         break;
     case EPI_QKV: {
         if (row & 1) break;
@@ -658,12 +665,7 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
 
 // Activation parts: token m, sub-block s, part p -> Xp[m/16][s][p][g][m%16][perm] (bf16).
 // x = hi + mid + lo with hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid), each
-// rounded to nearest even; tokens beyond M (tile padding) are zero.
-__device__ __forceinline__ uint32_t bf16_rne(float f)
-{
-    const uint32_t u = __float_as_uint(f);
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
+// rounded to nearest even (bf16_rne, xp_store); tokens beyond M (tile padding) are zero.
 
 // Parts and stores of one item (8 elements of sub-block s, group g) of token row t of tile tt.
 __device__ __forceinline__ void qprep_store(const float *v, uint8_t *__restrict__ xp, int nsb, int tt, int t, int i)
@@ -918,10 +920,15 @@ hipError_t launch_qgemm(const QgemmArgs &a, const float *x, int64_t x_stride, in
     if ((uint64_t)a.w.rows * (uint64_t)a.w.nb * (uint64_t)fmt_main_bytes(a.w.fmt) >= (1ull << 32))
         return hipErrorInvalidValue;
     const int K = (int)a.w.cols;
+    if ((!x && pro != PRO_NONE) || (a.yp && (a.epi == EPI_SILU ? a.w.rows % 64 : a.w.rows % 32)) ||
+        (a.yp && a.epi != EPI_SILU && a.epi != EPI_GELU))
+        return hipErrorInvalidValue;
     const unsigned mp = (unsigned)((a.M + 15) / 16 * 16);
-    const int ipt = (K / 8 + 255) / 256;
+    int ipt = (K / 8 + 255) / 256;
 #define SMX_QPREP(KN) hipLaunchKernelGGL(KN, dim3(mp), dim3(256), 0, s, x, x_stride, a.M, K, pro, gamma, beta, eps, (uint8_t *)a.xp)
+    if (!x) ipt = -1;   // the parts are already in a.xp (written by the producing kernel)
     switch (ipt) {
+    case -1: break;
     case 1: SMX_QPREP(k_qprep<1>); break;
     case 2: SMX_QPREP(k_qprep<2>); break;
     case 3: SMX_QPREP(k_qprep<3>); break;

@@ -186,7 +186,8 @@ struct smx_model {
 struct TokBatch {
     int cap = 0, logits_rows = 0;
     float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
-    uint8_t *xp = nullptr;
+    uint8_t *xp = nullptr;    // activation parts prepared by k_qprep (QKV, gate/up, head)
+    uint8_t *xp2 = nullptr;   // activation parts written by the producing kernel (O, down)
     int32_t *ids = nullptr, *pos = nullptr;
     float **kc = nullptr, **vc = nullptr;
     int32_t **tok_arr = nullptr;
@@ -508,7 +509,7 @@ int check_abort(smx_session *S)
 void batch_free(TokBatch &B)
 {
     free_dev(B.x); free_dev(B.q); free_dev(B.att); free_dev(B.h); free_dev(B.logits);
-    free_dev(B.xp); free_dev(B.ids); free_dev(B.pos); free_dev(B.kc); free_dev(B.vc);
+    free_dev(B.xp); free_dev(B.xp2); free_dev(B.ids); free_dev(B.pos); free_dev(B.kc); free_dev(B.vc);
     free_dev(B.tok_arr);
     B = TokBatch{};
 }
@@ -525,6 +526,7 @@ int batch_alloc(const smx_model *m, TokBatch &B, int cap, int logits_rows)
     A((void **)&B.h, (size_t)cap * maxk * 4);
     A((void **)&B.logits, (size_t)logits_rows * c.vocab * 4);
     A((void **)&B.xp, qgemm_xp_bytes(cap, (int)maxk));
+    A((void **)&B.xp2, qgemm_xp_bytes(cap, (int)maxk));
     A((void **)&B.ids, (size_t)cap * 4);
     A((void **)&B.pos, (size_t)cap * 4);
     A((void **)&B.kc, (size_t)cap * sizeof(float *));
@@ -580,21 +582,22 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
         a.rope_cos = m->rope_cos;
         a.rope_sin = m->rope_sin;
         SMX_HIP(launch_qgemm(a, B.x, d, pro, L.d_attn_g, L.d_attn_b, c.norm_eps, s));
+        // attention writes the O projection's activation parts directly (no k_qprep launch)
         if (run && attention_prefill_supported(c.n_head, Hkv, hd))
             SMX_HIP(launch_attention_prefill(B.q, m->nqkv, run->kc + layer_off, run->vc + layer_off, B.att, d,
-                                             c.n_head, Hkv, hd, ctx_stride, run->p_first, M, s));
+                                             c.n_head, Hkv, hd, ctx_stride, run->p_first, M, s, B.xp2));
         else
             SMX_HIP(launch_attention_tokens(B.q, m->nqkv, B.kc, B.vc, layer_off, B.att, d, c.n_head, Hkv, hd,
-                                            ctx_stride, B.pos, M, s));
+                                            ctx_stride, B.pos, M, s, B.xp2));
         QgemmArgs o{};
         o.w = L.o.view();
-        o.xp = B.xp;
+        o.xp = B.xp2;
         o.M = M;
         o.y = B.x;
         o.y_stride = d;
         o.bias = L.d_bo;
         o.epi = EPI_RESID;
-        SMX_HIP(launch_qgemm(o, B.att, d, PRO_NONE, nullptr, nullptr, 0.0f, s));
+        SMX_HIP(launch_qgemm(o, nullptr, d, PRO_NONE, nullptr, nullptr, 0.0f, s));
         QgemmArgs g{};
         g.w = L.gu.view();
         g.xp = B.xp;
@@ -603,16 +606,17 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
         g.y_stride = m->hidden;
         g.bias = L.d_bgu;
         g.epi = m->llama ? EPI_SILU : EPI_GELU;
+        g.yp = B.xp2;   // the down projection's activation parts
         SMX_HIP(launch_qgemm(g, B.x, d, pro, L.d_ffn_g, L.d_ffn_b, c.norm_eps, s));
         QgemmArgs dn{};
         dn.w = L.down.view();
-        dn.xp = B.xp;
+        dn.xp = B.xp2;
         dn.M = M;
         dn.y = B.x;
         dn.y_stride = d;
         dn.bias = L.d_bdown;
         dn.epi = EPI_RESID;
-        SMX_HIP(launch_qgemm(dn, B.h, m->hidden, PRO_NONE, nullptr, nullptr, 0.0f, s));
+        SMX_HIP(launch_qgemm(dn, nullptr, m->hidden, PRO_NONE, nullptr, nullptr, 0.0f, s));
     }
     if (head_from < M) {
         QgemmArgs hq{};

@@ -28,11 +28,14 @@ struct AttnSmem {
 
 // sc: LDS scratch of at least n_pos floats.  All NT threads of the workgroup must call this.
 // U: positions per thread per P.V load batch (one batch = one round trip to memory).
+// With parts set, the output is written as activation parts of the next GEMM instead of out:
+// xp_store(parts, parts_nsb, parts_tok, parts_k0 + d, out[d]).
 template <int HD, int NT, int U = 8>
 __device__ __forceinline__ void attention_head(const float *__restrict__ qh, const float *__restrict__ K,
                                                const float *__restrict__ V, float *__restrict__ out,
                                                int n_pos, int ctx_stride, float *sc,
-                                               AttnSmem<HD, NT> &sm)
+                                               AttnSmem<HD, NT> &sm, uint8_t *parts = nullptr,
+                                               int parts_nsb = 0, int parts_tok = 0, int parts_k0 = 0)
 {
     constexpr int D4 = HD / 4;
     constexpr int NPL = NT / D4;
@@ -109,7 +112,15 @@ __device__ __forceinline__ void attention_head(const float *__restrict__ qh, con
             const float4 v = sm.part[p][tid];
             o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
         }
-        ((float4 *)out)[tid] = o;
+        if (parts) {
+            const int k = parts_k0 + 4 * tid;
+            xp_store(parts, parts_nsb, parts_tok, k, o.x);
+            xp_store(parts, parts_nsb, parts_tok, k + 1, o.y);
+            xp_store(parts, parts_nsb, parts_tok, k + 2, o.z);
+            xp_store(parts, parts_nsb, parts_tok, k + 3, o.w);
+        } else {
+            ((float4 *)out)[tid] = o;
+        }
     }
     __syncthreads();   // sm and sc may be reused by the caller right away
 }

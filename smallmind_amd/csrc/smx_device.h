@@ -154,6 +154,29 @@ __device__ __forceinline__ float wave_sum_uniform(float v)
     return (r0 + r1) + (r2 + r3);
 }
 
+// bf16 bits of f, rounded to nearest even.
+__device__ __forceinline__ uint32_t bf16_rne(float f)
+{
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Activation parts of the matrix-core GEMM (k_qgemm): f = hi + mid + lo, three bf16 values each
+// rounded to nearest even, stored for element k = 32 s + 8 g + 4 h + q of token m at
+// Xp[m / 16][s][part][g][m % 16] dword q, half h (2 bytes each; nsb = sub-blocks per token).
+__device__ __forceinline__ void xp_store(uint8_t *xp, int nsb, int m, int k, float f)
+{
+    const uint32_t hi = bf16_rne(f);
+    const float r1 = f - __uint_as_float(hi << 16);
+    const uint32_t mid = bf16_rne(r1);
+    const float r2 = r1 - __uint_as_float(mid << 16);
+    const int s = k >> 5, e = k & 31, g = e >> 3, j = e & 7;
+    uint8_t *b = xp + ((size_t)(m >> 4) * nsb + s) * 3 * 1024 + (g * 16 + (m & 15)) * 16 + (j & 3) * 4 + (j >> 2) * 2;
+    *(uint16_t *)b = (uint16_t)hi;
+    *(uint16_t *)(b + 1024) = (uint16_t)mid;
+    *(uint16_t *)(b + 2048) = (uint16_t)bf16_rne(r2);
+}
+
 // v_permlane32_swap_b32 (gfx950): lanes 32..63 of `a` trade places with lanes 0..31 of `b`;
 // .x is the new `a`, .y the new `b`.
 __device__ __forceinline__ float2 swap32(float a, float b)

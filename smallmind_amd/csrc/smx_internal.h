@@ -129,6 +129,9 @@ struct QgemmArgs {
     int64_t y_stride;
     const float *bias;          // [rows] or nullptr (interleaved like the rows for EPI_SILU)
     int epi;                    // EPI_STORE / EPI_RESID / EPI_GELU / EPI_SILU / EPI_QKV
+    // EPI_SILU / EPI_GELU: when set, the outputs go to yp as the activation parts of the next
+    // GEMM (qgemm_xp_bytes(M, width) bytes) instead of y
+    uint8_t *yp;
     // EPI_QKV
     int d_model, kv_dim, head_dim, use_rope, ctx_stride;
     int64_t layer_off;
@@ -140,7 +143,8 @@ struct QgemmArgs {
 // Scratch bytes of the activation parts for M tokens of K elements.
 size_t qgemm_xp_bytes(int M, int K);
 // Prepares the parts of the (normalised, PRO_RMS / PRO_LN) activations into xp, then runs the
-// GEMM.  a.xp must point at qgemm_xp_bytes(a.M, cols) bytes of scratch.
+// GEMM.  a.xp must point at qgemm_xp_bytes(a.M, cols) bytes of scratch.  With x == nullptr
+// (and PRO_NONE) a.xp already holds the parts, written by the producing kernel.
 hipError_t launch_qgemm(const QgemmArgs &a, const float *x, int64_t x_stride, int pro,
                         const float *gamma, const float *beta, float eps, hipStream_t s);
 
@@ -225,13 +229,16 @@ hipError_t launch_embed_tokens(const WView &tok, const WView *posw, const int32_
 // chunks) on the matrix cores: q [M][q_stride] (head h at h*hd), kc / vc the layer's cache
 // ([n_kv_head][hd][ctx_stride] / [n_kv_head][ctx_stride][hd]), out [M][out_stride].
 bool attention_prefill_supported(int n_head, int n_kv_head, int hd);
+// With out_parts set, the outputs are written as the activation parts of the next GEMM
+// (xp_store, token t, element h*hd + d) instead of out.
 hipError_t launch_attention_prefill(const float *q, int q_stride, const float *kc, const float *vc, float *out,
                                     int out_stride, int n_head, int n_kv_head, int hd, int ctx_stride,
-                                    int p_first, int M, hipStream_t s);
+                                    int p_first, int M, hipStream_t s, uint8_t *out_parts = nullptr);
 hipError_t launch_attention_tokens(const float *q, int64_t q_stride, float *const *kc_tok,
                                    float *const *vc_tok, int64_t layer_off, float *out,
                                    int64_t out_stride, int n_head, int n_kv_head, int hd,
-                                   int ctx_stride, const int32_t *tok_pos, int M, hipStream_t s);
+                                   int ctx_stride, const int32_t *tok_pos, int M, hipStream_t s,
+                                   uint8_t *out_parts = nullptr);
 hipError_t launch_argmax_rows(const float *x, int n, int64_t stride, int M, int32_t *tok_next,
                               int32_t *tok_pos, int32_t *const *tok_arr, hipStream_t s);
 
