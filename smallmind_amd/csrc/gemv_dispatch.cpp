@@ -17,6 +17,10 @@ hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s)
         return hipErrorInvalidValue;
     if ((uint64_t)a.w.rows * (uint64_t)a.w.nb * (uint64_t)fmt_main_bytes(a.w.fmt) >= (1ull << 32))
         return hipErrorInvalidValue;
+    // two partial activation vectors: staged paths only (K <= 16384), no fused norm, one row
+    if (a.x_parts > 2 || (a.x_parts == 2 && (m != 1 || a.pro != PRO_NONE || a.x_embed || a.w.cols > 8192 || a.epi == EPI_SILU || a.epi == EPI_QKV ||
+                               a.epi == EPI_ARGMAX)))
+        return hipErrorInvalidValue;
     switch (a.w.fmt) {
     case FMT_Q4_0: return launch_gemv_fmt0(a, m, s);
     case FMT_Q8_0: return launch_gemv_fmt1(a, m, s);

@@ -191,6 +191,8 @@ __device__ __forceinline__ float wg_sum(float v, float *slot, int w)
 // distinct banks across consecutive lanes.
 __device__ __forceinline__ int xs_pos(int c, int i) { return 8 * c + (i ^ (c & 7)); }
 
+// STG = 3 is STG = 1 with the activation vector given as two partial sums x + x[x_part_stride]
+// (no norm), added in that order while staging.
 // STG = 1 (K <= 8192) / 2 (K <= 16384, no norm): the workgroup loads the activation vector
 // with coalesced loads (thread t: float4 t, t+256, ...), applies the fused norm and stages it
 // in LDS; lanes then read their chunks from LDS.  STG = 0 (no norm, K > 16384): lanes read
@@ -220,6 +222,9 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
     // 1. activations (+ norm parameters): coalesced, issued first
     const int tid = STG ? opaque_tid() : 0;
     float4 xr[STG ? KPT : 1], gr[PRO != PRO_NONE ? KPT : 1], br[PRO == PRO_LN ? KPT : 1];
+    constexpr bool TWO = STG == 3;   // x = x + x[x_part_stride] (two partial sums)
+    static_assert(!TWO || PRO == PRO_NONE, "partial sums are added before any norm");
+    float4 x2[TWO ? KPT : 1];
     if constexpr (STG) {
 #pragma unroll
         for (int k = 0; k < KPT; k++) {
@@ -228,6 +233,13 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
                 xr[k] = ((const float4 *)x)[i4];
                 if constexpr (PRO != PRO_NONE) gr[k] = ((const float4 *)a.gamma)[i4];
                 if constexpr (PRO == PRO_LN) br[k] = ((const float4 *)a.beta)[i4];
+            }
+        }
+        if constexpr (TWO) {
+#pragma unroll
+            for (int k = 0; k < KPT; k++) {
+                const int i4 = tid + 256 * k;
+                if (i4 < K4) x2[k] = ((const float4 *)(x + a.x_part_stride))[i4];
             }
         }
     }
@@ -289,6 +301,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
             const int i4 = tid + 256 * k;
             if (i4 < K4) {
                 float4 v = xr[k];
+                if constexpr (TWO) { v.x += x2[k].x; v.y += x2[k].y; v.z += x2[k].z; v.w += x2[k].w; }
                 if constexpr (PRO == PRO_RMS) {   // RMSNormOps.cs:137-139: gamma * (x * invRms)
                     const float4 g = gr[k];
                     v.x = g.x * (v.x * sc); v.y = g.y * (v.y * sc);
@@ -425,6 +438,18 @@ template <int PRO, int EC>
 hipError_t launch_pe(const GemvArgs &a, int m, hipStream_t s)
 {
     const int64_t K = a.w.cols;
+    if constexpr (PRO == PRO_NONE && EC == EC_SIMPLE) {
+        // two partial activation vectors (STG 3: staged like STG 1, K <= 8192)
+        if (a.x_parts == 2) {
+            if (K > 8192) return hipErrorInvalidValue;
+            switch (gemv_shape(a.w.rows, K)) {
+            case GS_R4S1: return launch_v<4, 1, 1, PRO, EC, 3>(a, m, s);
+            case GS_R2S1: return launch_v<2, 1, 1, PRO, EC, 3>(a, m, s);
+            case GS_R2S2: return launch_v<2, 2, 1, PRO, EC, 3>(a, m, s);
+            default: return launch_v<2, 4, 1, PRO, EC, 3>(a, m, s);
+            }
+        }
+    }
     switch (gemv_shape(a.w.rows, K)) {
     case GS_WIDE:
         if constexpr (PRO == PRO_NONE && EC == EC_SIMPLE) {

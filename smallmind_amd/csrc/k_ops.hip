@@ -113,6 +113,7 @@ template <int HD> struct AttnCfg {
 //    P.V for its slice (V is position-major, so a position's slice is 64 contiguous bytes).
 constexpr int kScorePB = 32;    // positions per score workgroup
 constexpr int kPvSlice = 16;    // dimensions per P.V workgroup
+constexpr int kPvChunk = 2304;  // positions per workgroup of the two-chunk P.V (64 lanes x 36)
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q, const float *__restrict__ kc,
@@ -157,7 +158,11 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     }
 }
 
-template <int HD, int U, int NT>
+// NCH = 2: the positions are split over two workgroups per (head, slice), each taking its
+// half (NB positions) and writing a partial output at out + chunk * n_head * HD; the O
+// projection sums the two (GemvArgs::x_parts).  Both compute the softmax statistics over all
+// positions in the same order, so they use the same max, sum and weights.
+template <int HD, int U, int NT, int NCH>
 __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores, const float *__restrict__ vc,
                                                 float *__restrict__ out, int n_head, int n_kv_head,
                                                 int ctx_stride, int sc_stride, const int32_t *__restrict__ pos_dev,
@@ -175,8 +180,9 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
     __shared__ float4 part[NW][C4];
     // Workgroups are dealt to the 8 XCDs round-robin; consecutive (head, slice) indices are
     // grouped per XCD so that the query heads of one KV head share that XCD's L2.
-    const int T = n_head * NS, b = blockIdx.x;
-    const int L = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
+    const int T = n_head * NS * NCH, b = blockIdx.x;
+    const int Lc = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
+    const int L = Lc / NCH, chunk = Lc % NCH;
     const int h = L / NS, slice = L % NS;
     const int kvh = h / (n_head / n_kv_head);
     const int tid = threadIdx.x;
@@ -190,13 +196,21 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
     // all loaded up front, before the position is known, with indices clamped into the cache
     // row (valid memory; entries at or past n_pos are dropped by selection, never multiplied),
     // so the scores arrive first and V streams in while the softmax is computed.
-    const int j0 = pl * U;
-    float sv[U];
+    const int j0 = chunk * NB + pl * U;
+    // NCH = 1: the lane's own positions' scores; NCH = 2: positions tid + NT*u of both chunks
+    // for the statistics (NPT per thread)
+    constexpr int NPT = NCH == 1 ? U : 2 * NB / NT;
+    float sv[NPT];
+    if constexpr (NCH == 1) {
 #pragma unroll
-    for (int u = 0; u < U; u += 4) {
-        const int j = min(j0 + u, sc_stride - 4);   // sc_stride is a multiple of 4
-        const float4 t = *(const float4 *)(srow + j);
-        sv[u] = t.x; sv[u + 1] = t.y; sv[u + 2] = t.z; sv[u + 3] = t.w;
+        for (int u = 0; u < U; u += 4) {
+            const int j = min(j0 + u, sc_stride - 4);   // sc_stride is a multiple of 4
+            const float4 t = *(const float4 *)(srow + j);
+            sv[u] = t.x; sv[u + 1] = t.y; sv[u + 2] = t.z; sv[u + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < NPT; u++) sv[u] = srow[min(tid + NT * u, sc_stride - 1)];
     }
     __builtin_amdgcn_sched_barrier(0);
     float4 vv[U];
@@ -205,7 +219,30 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
     __builtin_amdgcn_sched_barrier(0);
     const int n_pos = pos_dev ? ld_uniform(pos_dev) + 1 : n_pos_fixed;
     float pu[U];
-    if (n_pos <= NB) {
+    if constexpr (NCH == 2) {
+        // statistics over all positions (the same order in every workgroup of the head), the
+        // weights of every position into LDS, then this lane's
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < NPT; u++)
+            if (tid + NT * u < n_pos) mx = fmaxf(mx, sv[u]);
+        mx = block_max<NW>(mx, red);
+        float sum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < NPT; u++) {
+            const float e = tid + NT * u < n_pos ? fastexp(sv[u] - mx) : 0.0f;
+            sv[u] = e;
+            sum += e;
+        }
+        sum = block_sum<NW>(sum, red);
+        const float inv = 1.0f / sum;
+#pragma unroll
+        for (int u = 0; u < NPT; u++)
+            if (tid + NT * u < n_pos) p[tid + NT * u] = sv[u] * inv;
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < U; u++) pu[u] = p[min(j0 + u, n_pos - 1)];   // j0 + u >= n_pos: dropped below
+    } else if (n_pos <= NB) {
         // Whole softmax in registers.  The C4 = 4 lanes of a position lane form a DPP quad
         // holding the same positions: lane c4 takes the exact max over its quarter, computes
         // FastExp for positions j0 + 4*c4 .. +3 and the quad shares the results; the sum runs
@@ -284,7 +321,7 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
     // loads (clamped into the row, dropped by selection) issued before the previous batch's
     // multiply-adds
     constexpr int U2 = 16;
-    if (n_pos > NB) {
+    if (NCH == 1 && n_pos > NB) {
         float4 v2[U2];
         auto load2 = [&](int jb) {
 #pragma unroll
@@ -328,7 +365,7 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
             const float4 v = part[i][tid];
             o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
         }
-        ((float4 *)(out + (int64_t)h * HD + slice * kPvSlice))[tid] = o;
+        ((float4 *)(out + (int64_t)chunk * n_head * HD + (int64_t)h * HD + slice * kPvSlice))[tid] = o;
     }
 }
 
@@ -655,18 +692,18 @@ hipError_t launch_softmax(float *scores, float scale, int seq, int k_seq, int ca
     return hipGetLastError();
 }
 
-template <int HD, int U, int NT>
+template <int HD, int U, int NT, int NCH = 1>
 hipError_t launch_pv(dim3 g2, size_t p_lds, const float *scores, const float *vc, float *out, int n_head,
                      int n_kv_head, int ctx_stride, int sc_stride, const int32_t *pos_dev, int n_pos_fixed,
                      hipStream_t s)
 {
-    const void *fp = (const void *)k_attn_pv<HD, U, NT>;
+    const void *fp = (const void *)k_attn_pv<HD, U, NT, NCH>;
     if (p_lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(fp, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p_lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((k_attn_pv<HD, U, NT>), g2, dim3(NT), p_lds, s, scores, vc, out, n_head, n_kv_head,
-                       ctx_stride, sc_stride, pos_dev, n_pos_fixed);
+    hipLaunchKernelGGL((k_attn_pv<HD, U, NT, NCH>), dim3(g2.x * NCH), dim3(NT), p_lds, s, scores, vc, out, n_head,
+                       n_kv_head, ctx_stride, sc_stride, pos_dev, n_pos_fixed);
     return hipGetLastError();
 }
 
@@ -688,19 +725,30 @@ hipError_t launch_attn_hd(dim3 g1, dim3 g2, size_t q_lds, size_t p_lds, int U, i
         default: return SMX_PV(16, 256);
         }
     }
-    switch (U) {
-    case 16: return SMX_PV(16, 512);
-    case 24: return SMX_PV(24, 512);
-    default: return SMX_PV(36, 512);
+    if (NT == 512) {
+        switch (U) {
+        case 16: return SMX_PV(16, 512);
+        case 24: return SMX_PV(24, 512);
+        default: return SMX_PV(36, 512);
+        }
     }
 #undef SMX_PV
+    // two workgroups per (head, slice), 256 threads, 36 positions per lane each
+    return launch_pv<HD, 36, 256, 2>(g2, p_lds, scores, vc, out, n_head, n_kv_head, ctx_stride, sc_stride, pos_dev,
+                                     n_pos_fixed, s);
 }
 
 size_t attention_scores_floats(int n_head, int max_pos) { return (size_t)n_head * ((max_pos + 3) & ~3); }
 
+int attention_pv_chunks(int max_pos, int max_chunks)
+{
+    return max_chunks >= 2 && max_pos > kPvChunk && max_pos <= 2 * kPvChunk ? 2 : 1;
+}
+
 hipError_t launch_attention_split(const float *q, const float *kc, const float *vc, float *out,
                                   float *scores, int n_head, int n_kv_head, int hd, int ctx_stride,
-                                  const int32_t *pos_dev, int n_pos_fixed, int max_pos, hipStream_t s)
+                                  const int32_t *pos_dev, int n_pos_fixed, int max_pos, hipStream_t s,
+                                  int max_chunks)
 {
     if (hd % kPvSlice || hd > 128 || n_head % n_kv_head || max_pos > ctx_stride || max_pos < 1)
         return hipErrorInvalidValue;
@@ -713,7 +761,8 @@ hipError_t launch_attention_split(const float *q, const float *kc, const float *
     // positions per lane sized to the session context so that every V row of the context is
     // loaded in the first batch, all of its loads in flight: 256 threads (64 position lanes)
     // up to 1024 positions, 512 threads (128 position lanes) up to 4608
-    const int NT = max_pos <= 1024 ? 256 : 512;
+    // (two workgroups per (head, slice), when the caller sums two partial outputs: NT 0)
+    const int NT = attention_pv_chunks(max_pos, max_chunks) == 2 ? 0 : max_pos <= 1024 ? 256 : 512;
     const int U = max_pos <= 256 ? 4 : max_pos <= 512 ? 8 : max_pos <= 768 ? 12 : max_pos <= 1024 ? 16
                 : max_pos <= 2048 ? 16 : max_pos <= 3072 ? 24 : 36;
     switch (hd) {

@@ -293,12 +293,16 @@ int enqueue_step(smx_session *S, bool with_head, bool with_embed, hipStream_t s)
         a.pos = S->pos;
         SMX_HIP(launch_gemv(a, 1, s));
 
+        // long contexts: two partial attention outputs, summed by the O projection's staging
+        const int att_parts = attention_pv_chunks(S->max_ctx, 2);
         SMX_HIP(launch_attention_split(S->q, a.k_cache, a.v_cache, S->att, S->scores, c.n_head, Hkv, hd,
-                                       S->max_ctx, S->pos, 0, S->max_ctx, s));
+                                       S->max_ctx, S->pos, 0, S->max_ctx, s, 2));
 
         GemvArgs o{};
         o.w = L.o.view();
         o.x = S->att;
+        o.x_parts = att_parts;
+        o.x_part_stride = (int64_t)c.n_head * hd;
         o.out = S->x;
         o.resid = S->x;
         o.bias = L.d_bo;
@@ -1197,7 +1201,7 @@ SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out)
     A((void **)&S->vc, cache);
     A((void **)&S->x, (size_t)c.d_model * 4);
     A((void **)&S->q, (size_t)m->nqkv * 4);
-    A((void **)&S->att, (size_t)c.d_model * 4);
+    A((void **)&S->att, (size_t)2 * c.d_model * 4);   // two partial outputs at long contexts
     A((void **)&S->scores, attention_scores_floats(c.n_head, max_ctx) * 4);
     A((void **)&S->h, maxv * 4);
     A((void **)&S->logits, (size_t)c.vocab * 4);

@@ -100,6 +100,11 @@ struct GemvArgs {
     // next decode step
     float *x_next;
     WView next_emb, next_embp;
+    // x_parts = 2 (m == 1, no norm): the activation vector is x + x[x_part_stride], two partial
+    // sums added in that order (the two-chunk decode attention output).  Kept last: the
+    // kernels read the leading fields first.
+    int x_parts;
+    int64_t x_part_stride;
 };
 
 hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s);
@@ -202,10 +207,15 @@ hipError_t launch_softmax(float *scores, float scale, int seq, int k_seq, int ca
 // into `scores` (attention_scores_floats(n_head, max_pos) floats: rows of max_pos rounded up
 // to a multiple of 4), then softmax + P.V per (head, 16-dimension slice).  Positions up to
 // max_pos (<= ctx_stride) are covered; pos_dev (if set) gives n_pos - 1.
+// With max_chunks >= 2, contexts of 2305..4608 positions run as two workgroups per (head,
+// slice) that write two partial outputs, out[0] and out[n_head * hd], to be summed by the
+// caller; attention_pv_chunks says how many partial outputs a call writes.
 size_t attention_scores_floats(int n_head, int max_pos);
+int attention_pv_chunks(int max_pos, int max_chunks);
 hipError_t launch_attention_split(const float *q, const float *kc, const float *vc, float *out,
                                   float *scores, int n_head, int n_kv_head, int hd, int ctx_stride,
-                                  const int32_t *pos_dev, int n_pos_fixed, int max_pos, hipStream_t s);
+                                  const int32_t *pos_dev, int n_pos_fixed, int max_pos, hipStream_t s,
+                                  int max_chunks = 1);
 hipError_t launch_silu_mul(const float *g, const float *u, float *y, int64_t n, hipStream_t s);
 hipError_t launch_gelu(const float *x, float *y, int64_t n, hipStream_t s);
 hipError_t launch_argmax(const float *x, int n, int32_t *out, int32_t *tokens, int32_t *pos,

@@ -257,3 +257,29 @@ def test_full_size_llama_q4k_short_prompt():
         tok = int(toks[i])
     s.close()
     gm.close()
+
+
+def test_long_context_decode_two_chunk_attention(gpu):
+    """Sessions of 2305..4608 positions decode with the attention's P.V split over two
+    workgroups per (head, 16-dimension slice), whose partial outputs the O projection sums while
+    staging its input; logits and greedy tokens against the oracle at ~2.4K positions."""
+    cfg = ModelConfig("llama", 1000, 2600, 256, 2, 4, 2, 512)
+    om, gm, _ = build_pair(cfg, O.Q4_K, O.Q6_K, O.Q6_K, seed=11)
+    try:
+        prompt = np.random.default_rng(3).integers(0, cfg.vocab_size, 2400).astype(np.int32)
+        sess = gm.create_session(2600)
+        toks, stats, logits = sess.generate_greedy(prompt, 8, return_logits=True)
+        osess = om.session(2600)
+        for p, t in enumerate(prompt[:-1]):
+            osess.step(int(t), p, want_logits=False)
+        tok = int(prompt[-1])
+        for i in range(8):
+            ref = osess.step(tok, len(prompt) - 1 + i)
+            err = rel_err(logits[i], ref)
+            assert err <= LOGIT_TOL, (i, err)
+            ref_tok = int(np.argmax(ref))
+            assert int(toks[i]) == ref_tok, (i, int(toks[i]), ref_tok)
+            tok = ref_tok
+        sess.close()
+    finally:
+        gm.close()
