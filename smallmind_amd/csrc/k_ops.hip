@@ -369,6 +369,146 @@ __global__ __launch_bounds__(NT) void k_attn_pv(const float *__restrict__ scores
     }
 }
 
+// Decode attention of contexts up to NT * P <= 1024 positions in one launch (HD <= 64, cache
+// rows 16-byte aligned: ctx_stride % 4 == 0): the workgroup = (query head, slice of 16
+// dimensions) of k_attn_pv computes its head's scores itself instead of reading them from a
+// previous launch.  Score phase: thread (dimension quarter dq, position group pg) loads, for
+// each of P passes of NT positions, the keys of positions 4pg..4pg+3 over its HD/4
+// dimensions as float4 rows of the dimension-major cache (a wave's load of one dimension is
+// 1 KB contiguous) and forms four partial dot products with q read through the scalar
+// cache; the quarters are added in LDS in a fixed order and scaled by 1/sqrt(HD).  Every key
+// and V row of the workgroup is requested at entry, except with three passes, whose last
+// pass's keys reuse the registers of the first.  Few large-register threads beat many small ones here:
+// at the same context a workgroup of 1024 threads takes ~2.5 us longer than one of 256.
+// Every workgroup of a head reads the head's K (n_pos * HD * 4 bytes; L2 serves all but the
+// first).
+template <int HD, int NT, int P>
+__global__ __launch_bounds__(NT) void k_attn_dec(const float *__restrict__ q, const float *__restrict__ kc,
+                                                 const float *__restrict__ vc, float *__restrict__ out,
+                                                 int n_head, int n_kv_head, int ctx_stride,
+                                                 const int32_t *__restrict__ pos_dev, int n_pos_fixed)
+{
+    constexpr int NW = NT / 64;
+    constexpr int NS = HD / kPvSlice;   // slices per head
+    constexpr int C4 = kPvSlice / 4;    // float4 columns per slice
+    constexpr int U = 4 * P;            // consecutive positions per P.V lane (NT / C4 lanes)
+    constexpr int NPG = NT / 4;         // position groups per pass
+    constexpr int DQ = HD / 4;          // dimensions per quarter
+    constexpr int NP = NT * P;          // positions covered
+    static_assert(HD <= 64 && NP <= 1024 && NT % 256 == 0, "short-context decode attention");
+    __shared__ __align__(16) float ps[4][NP];
+    __shared__ __align__(16) float p[NP];
+    __shared__ float red[16];
+    __shared__ float4 part[NW][C4];
+    const int T = n_head * NS, b = blockIdx.x;
+    const int L = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;   // heads of a KV head share an XCD
+    const int h = L / NS, slice = L % NS;
+    const int kvh = h / (n_head / n_kv_head);
+    const int tid = opaque_tid();
+    const int c4 = tid % C4, j0 = (tid / C4) * U;
+    const int dq = __builtin_amdgcn_readfirstlane(tid / NPG), pg = tid % NPG;
+    const char *Kb = (const char *)(kc + (int64_t)kvh * HD * ctx_stride + (int64_t)dq * DQ * ctx_stride);
+    const char *Vb = (const char *)(vc + (int64_t)kvh * ctx_stride * HD + slice * kPvSlice);
+    // every load is issued before the position is known, with indices clamped into the cache
+    // row (valid memory); entries at or past n_pos are dropped by selection, never multiplied
+    const int lastg = ctx_stride / 4 - 1;
+    auto kload = [&](float4 *kv, int pass) {
+        const uint32_t pc = 4u * (uint32_t)min(pg + NPG * pass, lastg);
+#pragma unroll
+        for (int e = 0; e < DQ; e++) kv[e] = *(const float4 *)(Kb + 4u * ((uint32_t)e * (uint32_t)ctx_stride + pc));
+    };
+    const float *qd = q + (int64_t)h * HD + dq * DQ;
+    auto kdot = [&](const float4 *kv, int pass) {
+        float4 sp = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int e = 0; e < DQ; e++) {
+            const float qe = ld_uniform(qd + e);
+            sp.x = __builtin_fmaf(qe, kv[e].x, sp.x);
+            sp.y = __builtin_fmaf(qe, kv[e].y, sp.y);
+            sp.z = __builtin_fmaf(qe, kv[e].z, sp.z);
+            sp.w = __builtin_fmaf(qe, kv[e].w, sp.w);
+        }
+        *(float4 *)&ps[dq][4 * (pg + NPG * pass)] = sp;
+    };
+    constexpr int PA = P <= 2 ? P : P - 1;   // passes loaded at entry (registers: 16 * DQ * PA)
+    float4 kv[PA][DQ];
+#pragma unroll
+    for (int i = 0; i < PA; i++) kload(kv[i], i);
+    float4 vv[U];
+#pragma unroll
+    for (int u = 0; u < U; u++)
+        vv[u] = *(const float4 *)(Vb + 4u * ((uint32_t)min(j0 + u, ctx_stride - 1) * HD + 4u * (uint32_t)c4));
+    __builtin_amdgcn_sched_barrier(0);
+    const int n_pos = pos_dev ? ld_uniform(pos_dev) + 1 : n_pos_fixed;
+    kdot(kv[0], 0);
+    if constexpr (PA < P) {
+        __builtin_amdgcn_sched_barrier(0);
+        kload(kv[0], P - 1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 1; i < PA; i++) kdot(kv[i], i);
+    if constexpr (PA < P) kdot(kv[0], P - 1);
+    __syncthreads();
+    float sc[P], mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+        const int j = tid + NT * i;
+        float s = ps[0][j];
+#pragma unroll
+        for (int k = 1; k < 4; k++) s += ps[k][j];
+        sc[i] = s * (1.0f / sqrtf((float)HD));   // MultiHeadAttention.cs:686
+        if (j < n_pos) mx = fmaxf(mx, sc[i]);
+    }
+    mx = block_max<NW>(mx, red);
+    float ev[P], sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+        ev[i] = tid + NT * i < n_pos ? fastexp(sc[i] - mx) : 0.0f;
+        sum += ev[i];
+    }
+    sum = block_sum<NW>(sum, red);
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int i = 0; i < P; i++) p[tid + NT * i] = ev[i] * inv;
+    __syncthreads();
+    float pu[U];
+#pragma unroll
+    for (int u = 0; u < U; u += 4) {
+        const float4 pq = *(const float4 *)&p[j0 + u];
+        pu[u] = pq.x; pu[u + 1] = pq.y; pu[u + 2] = pq.z; pu[u + 3] = pq.w;
+    }
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        if (j0 + u < n_pos) {
+            acc.x = __builtin_fmaf(pu[u], vv[u].x, acc.x);
+            acc.y = __builtin_fmaf(pu[u], vv[u].y, acc.y);
+            acc.z = __builtin_fmaf(pu[u], vv[u].z, acc.z);
+            acc.w = __builtin_fmaf(pu[u], vv[u].w, acc.w);
+        }
+    }
+#pragma unroll
+    for (int m = C4; m < 64; m <<= 1) {
+        acc.x += __shfl_xor(acc.x, m);
+        acc.y += __shfl_xor(acc.y, m);
+        acc.z += __shfl_xor(acc.z, m);
+        acc.w += __shfl_xor(acc.w, m);
+    }
+    const int w = tid >> 6;
+    if ((tid & 63) < C4) part[w][c4] = acc;
+    __syncthreads();
+    if (tid < C4) {
+        float4 o = part[0][tid];
+#pragma unroll
+        for (int i = 1; i < NW; i++) {
+            const float4 v = part[i][tid];
+            o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+        }
+        ((float4 *)(out + (int64_t)h * HD + slice * kPvSlice))[tid] = o;
+    }
+}
+
 __global__ void k_silu_mul(const float *__restrict__ g, const float *__restrict__ u,
                            float *__restrict__ y, int64_t n)
 {
@@ -738,6 +878,40 @@ hipError_t launch_attn_hd(dim3 g1, dim3 g2, size_t q_lds, size_t p_lds, int U, i
                                      n_pos_fixed, s);
 }
 
+template <int HD, int NT, int P>
+hipError_t launch_dec(dim3 g, const float *q, const float *kc, const float *vc, float *out, int n_head,
+                      int n_kv_head, int ctx_stride, const int32_t *pos_dev, int n_pos_fixed, hipStream_t s)
+{
+    hipLaunchKernelGGL((k_attn_dec<HD, NT, P>), g, dim3(NT), 0, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride,
+                       pos_dev, n_pos_fixed);
+    return hipGetLastError();
+}
+
+// One launch for contexts up to 1024 positions: 256 threads with 1-3 passes of 256
+// positions, 512 threads with two passes above 768 positions
+template <int HD>
+hipError_t launch_dec_hd(dim3 g, int max_pos, const float *q, const float *kc, const float *vc, float *out,
+                         int n_head, int n_kv_head, int ctx_stride, const int32_t *pos_dev, int n_pos_fixed,
+                         hipStream_t s)
+{
+    if (max_pos <= 256) return launch_dec<HD, 256, 1>(g, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
+    if (max_pos <= 512) return launch_dec<HD, 256, 2>(g, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
+    if (max_pos <= 768) return launch_dec<HD, 256, 3>(g, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
+    return launch_dec<HD, 512, 2>(g, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
+}
+
+hipError_t launch_attn_dec(dim3 g, int max_pos, int hd, const float *q, const float *kc, const float *vc,
+                           float *out, int n_head, int n_kv_head, int ctx_stride, const int32_t *pos_dev,
+                           int n_pos_fixed, hipStream_t s)
+{
+    switch (hd) {
+    case 16: return launch_dec_hd<16>(g, max_pos, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
+    case 32: return launch_dec_hd<32>(g, max_pos, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
+    case 64: return launch_dec_hd<64>(g, max_pos, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 size_t attention_scores_floats(int n_head, int max_pos) { return (size_t)n_head * ((max_pos + 3) & ~3); }
 
 int attention_pv_chunks(int max_pos, int max_chunks)
@@ -758,6 +932,8 @@ hipError_t launch_attention_split(const float *q, const float *kc, const float *
     const size_t q_lds = (size_t)G * hd * 4, p_lds = (size_t)max_pos * 4;
     if (q_lds > 64 * 1024 || p_lds > 160 * 1024) return hipErrorInvalidValue;
     const dim3 g1((unsigned)(n_kv_head * nblk)), g2((unsigned)(n_head * (hd / kPvSlice)));
+    if (hd <= 64 && max_pos <= 1024 && ctx_stride % 4 == 0) return launch_attn_dec(g2, max_pos, hd, q, kc, vc, out, n_head, n_kv_head,
+                                                             ctx_stride, pos_dev, n_pos_fixed, s);
     // positions per lane sized to the session context so that every V row of the context is
     // loaded in the first batch, all of its loads in flight: 256 threads (64 position lanes)
     // up to 1024 positions, 512 threads (128 position lanes) up to 4608

@@ -80,6 +80,35 @@ def test_attention_decode_vs_oracle(gpu, H, Hkv, hd, npos):
     assert rel_err(got.reshape(H, hd), ref) < 1e-5
 
 
+@pytest.mark.parametrize("H,Hkv,hd,npos,ctx", [(32, 4, 64, 1, 4), (32, 4, 64, 160, 160), (12, 12, 64, 255, 256),
+                                               (32, 4, 64, 256, 260), (8, 2, 64, 257, 512), (32, 4, 64, 511, 512),
+                                               (32, 4, 64, 700, 768), (32, 4, 64, 768, 768), (16, 4, 64, 769, 1024),
+                                               (32, 8, 64, 1024, 1024), (12, 4, 32, 600, 604), (16, 1, 16, 95, 100),
+                                               (4, 4, 32, 1000, 1000)])
+def test_attention_decode_one_launch_vs_oracle(gpu, H, Hkv, hd, npos, ctx):
+    """Contexts up to 1024 positions with 16-byte aligned cache rows (ctx % 4 == 0) run as one
+    launch that computes the scores inside the P.V workgroups.  Cache entries past n_pos hold
+    NaN: they must never reach the output."""
+    from smallmind_amd.quantization import attention_decode
+    rng = np.random.default_rng(npos * 3 + hd)
+    q = rng.normal(0, 1, (H, hd)).astype(np.float32)
+    kc = rng.normal(0, 1, (Hkv, ctx, hd)).astype(np.float32)
+    vc = rng.normal(0, 1, (Hkv, ctx, hd)).astype(np.float32)
+    kc[:, npos:] = np.nan
+    vc[:, npos:] = np.nan
+    kt = np.ascontiguousarray(kc.transpose(0, 2, 1))
+    got = attention_decode(_dev(q), _dev(kt), _dev(vc), H, Hkv, hd, ctx, npos).cpu().numpy().reshape(H, hd)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    ref = np.empty((H, hd), np.float32)
+    for h in range(H):
+        kv = h // (H // Hkv)
+        sc = (kc[kv, :npos].astype(np.float64) @ q[h].astype(np.float64)).astype(np.float32)[None]
+        p = O.scale_mask_softmax(sc, float(scale), cache_off=npos - 1)[0]
+        ref[h] = p.astype(np.float64) @ vc[kv, :npos].astype(np.float64)
+    assert np.isfinite(got).all()
+    assert rel_err(got, ref) < 1e-5
+
+
 @pytest.mark.parametrize("H,Hkv,p0,n", [(32, 4, 0, 37), (32, 4, 300, 64), (12, 12, 5, 33),
                                         (16, 1, 0, 20), (8, 8, 1000, 17), (4, 2, 0, 1),
                                         (32, 32, 255, 256), (32, 4, 3840, 256), (2, 2, 16, 48)])
