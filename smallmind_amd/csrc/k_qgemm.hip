@@ -55,6 +55,17 @@ __device__ __forceinline__ uint32_t pack_hi16(float lo, float hi)
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
+// (a & m) | (b & ~m) and the bf16 pair 128 + (e & m) per 16-bit half, one v_bitop3_b32 each
+// (truth-table index = 4 * bit of the first operand + 2 * second + third)
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b)
+{
+    return __builtin_amdgcn_bitop3_b32(a, m, b, 0xE2);   // m ? a : b
+}
+__device__ __forceinline__ uint32_t code_pair(uint32_t e, uint32_t m)
+{
+    return __builtin_amdgcn_bitop3_b32(e, m, 0x43004300u, 0xEA);   // (e & m) | 0x43004300
+}
+
 // ---- per-format weight operand --------------------------------------------------------------
 // load(): the raw words of (row, sub-block s, k-group g) -- codes and scale fields -- issued
 // one sub-block ahead of use; codes(): 4 bf16 pairs (element p, element p + 4) of the group's
@@ -166,13 +177,14 @@ template <> struct QW<FMT_Q5_K> {
     }
     __device__ __forceinline__ static uint4 codes(const RawQ &r, int g)
     {
-        // the high bit of element 8g + 2k + p sits at bit 8k + 2g + p of H
-        const uint32_t v = r.v, H = r.H;
-        const uint32_t h0 = H >> (2 * g), h1 = H >> (2 * g + 1), h2 = H >> (2 * g + 8), h3 = H >> (2 * g + 9);
-        return make_uint4((v & 0x000F000Fu) | ((h0 & 0x00010001u) << 4) | 0x43004300u,
-                          ((v >> 4) & 0x000F000Fu) | ((h1 & 0x00010001u) << 4) | 0x43004300u,
-                          ((v >> 8) & 0x000F000Fu) | ((h2 & 0x00010001u) << 4) | 0x43004300u,
-                          ((v >> 12) & 0x000F000Fu) | ((h3 & 0x00010001u) << 4) | 0x43004300u);
+        // The high bit of element 8g + 2k + p sits at bit 8k + 2g + p of H, so hg = H >> 2g
+        // holds it at bit 8k + p.  e0 / e1 = the 5-bit codes of the even / odd elements
+        // 2k / 2k + 1 in bits 0-4 of byte k (bits 5-7 are don't-care); pair q = (element q,
+        // element q + 4) is then bytes 0 and 2 of e_{q%2} >> 8(q/2).
+        const uint32_t v = r.v, hg = r.H >> (2 * g);
+        const uint32_t e0 = bfi(0x0F0F0F0Fu, v, hg << 4), e1 = bfi(0x0F0F0F0Fu, v >> 4, hg << 3);
+        return make_uint4(code_pair(e0, 0x001F001Fu), code_pair(e1, 0x001F001Fu), code_pair(e0 >> 8, 0x001F001Fu),
+                          code_pair(e1 >> 8, 0x001F001Fu));
     }
     __device__ __forceinline__ static Scl scale(const RawQ &r, int s)
     {
@@ -200,13 +212,14 @@ template <> struct QW<FMT_Q6_K> {
     }
     __device__ __forceinline__ static uint4 codes(const RawQ &r, int g)
     {
-        // the two high bits of element 8g + 2k + p sit at bits 8k + 2g of D_p
+        // The two high bits of element 8g + 2k + p sit at bits 8k + 2g of D_p, so
+        // dp = D_p >> 2g holds them at bits 8k, 8k + 1: e_p = the 6-bit codes of the elements
+        // 2k + p in bits 0-5 of byte k, and pair q = bytes 0 and 2 of e_{q%2} >> 8(q/2).
         const uint32_t v = r.v;
-        const uint32_t e0 = r.H >> (2 * g), e1 = r.H2 >> (2 * g), e2 = r.H >> (2 * g + 8), e3 = r.H2 >> (2 * g + 8);
-        return make_uint4((v & 0x000F000Fu) | ((e0 & 0x00030003u) << 4) | 0x43004300u,
-                          ((v >> 4) & 0x000F000Fu) | ((e1 & 0x00030003u) << 4) | 0x43004300u,
-                          ((v >> 8) & 0x000F000Fu) | ((e2 & 0x00030003u) << 4) | 0x43004300u,
-                          ((v >> 12) & 0x000F000Fu) | ((e3 & 0x00030003u) << 4) | 0x43004300u);
+        const uint32_t e0 = bfi(0x0F0F0F0Fu, v, (r.H >> (2 * g)) << 4);
+        const uint32_t e1 = bfi(0x0F0F0F0Fu, v >> 4, (r.H2 >> (2 * g)) << 4);
+        return make_uint4(code_pair(e0, 0x003F003Fu), code_pair(e1, 0x003F003Fu), code_pair(e0 >> 8, 0x003F003Fu),
+                          code_pair(e1 >> 8, 0x003F003Fu));
     }
     __device__ __forceinline__ static Scl scale(const RawQ &r, int)
     {
