@@ -897,7 +897,7 @@ template <int F>
 hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
 {
     // Rows of whole 256-element super-blocks: LDS-staged weight tiles.  Up to 16 tokens: one
-    // token tile per workgroup; more: tiles of 64 tokens x 32 rows per wave, 8 waves splitting
+    // token tile per workgroup (16 waves splitting K from 8192 up); more: tiles of 64 tokens x 32 rows per wave, 8 waves splitting
     // long K (or short K over few rows), else 4 waves (K-quants: 64 rows x 32 tokens on tall
     // matrices; Q6_K 16 rows).  Chosen by measurement over the prefill shapes of the five
     // formats at 256 tokens.
@@ -910,6 +910,8 @@ hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
             if constexpr (F == FMT_Q6_K) return launch_st<F, 1, 4, 8>(a, s);
             return launch_st<F, 2, 4, 4>(a, s);
         }
+        if constexpr (F != FMT_Q6_K)   // 16 waves of >= 2 super-blocks (Q6_K would spill at 128 registers)
+            if (a.w.cols >= 8192) return launch_st<F, 1, 1, 16>(a, s);
         return tall ? launch_st<F, 2, 1, 4>(a, s) : launch_st<F, 1, 1, 8>(a, s);
     }
     // Up to 16 tokens: one token tile, 16 waves per workgroup splitting K, 4 sub-blocks per

@@ -89,7 +89,7 @@ def test_matmul_m_rows_equals_gemv_rows(gpu, name):
 @pytest.mark.parametrize("name", list(TYPES))
 @pytest.mark.parametrize("m,N,K", [(4, 272, 512), (16, 2560, 2048), (37, 300, 768),
                                    (64, 1000, 2048), (100, 48, 5632), (16, 40, 160),
-                                   (20, 8200, 256)])
+                                   (20, 8200, 256), (9, 300, 8192)])
 def test_matmul_matrix_core_path_vs_oracle(gpu, name, m, N, K):
     """m >= 4 rows: bf16 MFMA on exact integer codes and three-part activations; held to the
     same bounds as the GEMV, row by row (ragged m and N exercise the tile padding)."""
