@@ -258,17 +258,29 @@ constexpr uint32_t kOnes = 0x3F803F80u;   // bf16 1.0 pair
 
 // Epilogue of one output value per (token, weight row); all lanes of the wave must call it
 // (adjacent weight rows are exchanged with DPP for the paired SwiGLU / RoPE epilogues).
-__device__ __forceinline__ void qgemm_epilogue(const QgemmArgs &a, float v, uint32_t row, int tok, bool live)
+// Returns the new residual value for EPI_RESID with a.np set (0 for rows / tokens outside the
+// output), else 0.  With pre, EPI_RESID takes the residual and the next norm's gamma from
+// pres / pg (loaded by the caller at kernel entry) instead of loading them here.
+__device__ __forceinline__ float qgemm_epilogue(const QgemmArgs &a, float v, uint32_t row, int tok, bool live,
+                                                bool pre = false, float pres = 0.0f, float pg = 0.0f)
 {
     const uint32_t N = (uint32_t)a.w.rows;
     if (a.bias && row < N) v = v + a.bias[row];
     // value of the neighbouring weight row (lane li ^ 1 holds row ^ 1)
     const float nb = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
-    if (!live || row >= N || tok >= a.M) return;
+    if (!live || row >= N || tok >= a.M) return 0.0f;
     float *yr = a.y + (int64_t)tok * a.y_stride;
     switch (a.epi) {
     case EPI_STORE: yr[row] = v; break;
-    case EPI_RESID: yr[row] = yr[row] + v; break;
+    case EPI_RESID: {
+        const float xn = (pre ? pres : yr[row]) + v;
+        yr[row] = xn;
+        if (a.np) {   // the next GEMM's parts of gamma (.) x (RMSNormOps.cs:137-139 up to the factor r)
+            xp_store(a.np, (int)(N >> 5), tok, (int)row, (pre ? pg : a.ngamma[row]) * xn);
+            return xn;
+        }
+        break;
+    }
     case EPI_GELU:
         if (a.yp) xp_store(a.yp, (int)(N >> 5), tok, (int)row, gelu_pade(v));
         else yr[row] = gelu_pade(v);
@@ -310,6 +322,7 @@ __device__ __forceinline__ void qgemm_epilogue(const QgemmArgs &a, float v, uint
     }
     default: break;
     }
+    return 0.0f;
 }
 
 template <int F, int RT, int TT, int NW, int SB>
@@ -526,6 +539,36 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
                                     : make_uint4(kOnes, kOnes, kOnes, kOnes);
     const uint4 ones_b = g >= 2 ? make_uint4(kOnes, kOnes, kOnes, kOnes) : kZero4;
 
+    // Folded RMSNorm (one token tile): the tile sums of x^2 of wave wv's tokens wv + NW*j are
+    // requested here and reduced after the main loop.
+    constexpr int RJ = TT == 1 ? (16 + NW - 1) / NW : 1, RP = 4;   // tokens per wave, sums per lane
+    __shared__ float s_r[16];
+    float rl[RJ][RP];
+    const bool fold = TT == 1 && a.rss != nullptr;
+    if (fold) {
+#pragma unroll
+        for (int j = 0; j < RJ; j++) {
+            const int tk = min(tt0 * 16 + wv + NW * j, M - 1);
+#pragma unroll
+            for (int q = 0; q < RP; q++) {
+                const int p = lane + 64 * q;
+                rl[j][q] = p < a.rss_n ? a.rss[(int64_t)p * M + tk] : 0.0f;
+            }
+        }
+    }
+
+    // EPI_RESID with one 16 x 16 tile per wave: wave 0's residual values (and the next norm's
+    // gamma) are requested at entry, so the epilogue waits for no load
+    constexpr bool PRE = TT == 1 && RT == 1;
+    const bool pre = PRE && a.epi == EPI_RESID;
+    float pres[4] = {0.0f, 0.0f, 0.0f, 0.0f}, pg = 0.0f;
+    if (pre && wv == 0) {
+        const uint32_t rc = min(row_base + (uint32_t)li, N - 1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) pres[i] = a.y[(int64_t)min(tt0 * 16 + 4 * g + i, M - 1) * a.y_stride + rc];
+        if (a.np) pg = a.ngamma[rc];
+    }
+
     // staging loads of one super-block: piece p -> (row p / (kBytes/16), 16-byte column)
     uint4 wp[NPC];
     uint4 dp = kZero4;
@@ -650,6 +693,16 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
         }
     }
 
+    if (fold) {   // r = 1 / sqrt(sum x^2 / K + eps) (RMSNormOps.cs:114)
+#pragma unroll
+        for (int j = 0; j < RJ; j++) {
+            float t = rl[j][0];
+#pragma unroll
+            for (int q = 1; q < RP; q++) t += rl[j][q];
+            t = wave_sum_uniform(t);
+            if (lane == 0 && wv + NW * j < 16) s_r[wv + NW * j] = 1.0f / sqrtf(t / (float)w.cols + a.r_eps);
+        }
+    }
     // sum the NW waves' partial tiles in a fixed order; wave 0 applies the epilogue
     if (wv > 0) {
 #pragma unroll
@@ -659,8 +712,15 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
     }
     __syncthreads();
     if (wv != 0) return;
+    float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if (fold) {
 #pragma unroll
-    for (int r = 0; r < RT; r++)
+        for (int i = 0; i < 4; i++) rs[i] = s_r[4 * g + i];
+    }
+    const bool emit = TT == 1 && a.np != nullptr;   // producer of a folded norm
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        float sq[TT][4];
 #pragma unroll
         for (int t = 0; t < TT; t++) {
             f32x4 v = acc[r][t];
@@ -672,8 +732,20 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
             }
             const uint32_t row = row_base + 16 * r + li;
 #pragma unroll
-            for (int i = 0; i < 4; i++) qgemm_epilogue(a, v[i], row, (tt0 + t) * 16 + 4 * g + i, true);
+            for (int i = 0; i < 4; i++) {
+                const float xn = qgemm_epilogue(a, v[i] * rs[i], row, (tt0 + t) * 16 + 4 * g + i, true, pre, pres[i], pg);
+                sq[t][i] = xn * xn;
+            }
         }
+        if (emit) {   // x^2 summed over the tile's 16 rows (the 16 lanes of a row of lanes)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float t = row16_sum(sq[0][i]);
+                const int tok = tt0 * 16 + 4 * g + i;
+                if (li == 0 && tok < M) a.nss[(int64_t)(row_base / 16 + r) * M + tok] = t;
+            }
+        }
+    }
 }
 
 // Activation parts: token m, sub-block s, part p -> Xp[m/16][s][p][g][m%16][perm] (bf16).
@@ -938,6 +1010,10 @@ hipError_t launch_qgemm(const QgemmArgs &a, const float *x, int64_t x_stride, in
     if ((!x && pro != PRO_NONE) || (a.yp && (a.epi == EPI_SILU ? a.w.rows % 64 : a.w.rows % 32)) ||
         (a.yp && a.epi != EPI_SILU && a.epi != EPI_GELU))
         return hipErrorInvalidValue;
+    // folded RMSNorm: one token tile on the staged path
+    if ((a.rss || a.np) && (a.M > 16 || K % 256 != 0)) return hipErrorInvalidValue;
+    if (a.rss && (x || pro != PRO_NONE || a.rss_n < 1 || a.rss_n > 256)) return hipErrorInvalidValue;
+    if (a.np && (a.epi != EPI_RESID || a.w.rows % 32 != 0 || !a.ngamma || !a.nss)) return hipErrorInvalidValue;
     const unsigned mp = (unsigned)((a.M + 15) / 16 * 16);
     int ipt = (K / 8 + 255) / 256;
 #define SMX_QPREP(KN) hipLaunchKernelGGL(KN, dim3(mp), dim3(256), 0, s, x, x_stride, a.M, K, pro, gamma, beta, eps, (uint8_t *)a.xp)

@@ -188,6 +188,7 @@ struct TokBatch {
     float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
     uint8_t *xp = nullptr;    // activation parts prepared by k_qprep (QKV, gate/up, head)
     uint8_t *xp2 = nullptr;   // activation parts written by the producing kernel (O, down)
+    float *ss = nullptr;      // folded RMSNorm: per-16-row-tile sums of x^2 [d_model / 16][cap]
     int32_t *ids = nullptr, *pos = nullptr;
     float **kc = nullptr, **vc = nullptr;
     int32_t **tok_arr = nullptr;
@@ -513,7 +514,7 @@ int check_abort(smx_session *S)
 void batch_free(TokBatch &B)
 {
     free_dev(B.x); free_dev(B.q); free_dev(B.att); free_dev(B.h); free_dev(B.logits);
-    free_dev(B.xp); free_dev(B.xp2); free_dev(B.ids); free_dev(B.pos); free_dev(B.kc); free_dev(B.vc);
+    free_dev(B.xp); free_dev(B.xp2); free_dev(B.ss); free_dev(B.ids); free_dev(B.pos); free_dev(B.kc); free_dev(B.vc);
     free_dev(B.tok_arr);
     B = TokBatch{};
 }
@@ -531,6 +532,7 @@ int batch_alloc(const smx_model *m, TokBatch &B, int cap, int logits_rows)
     A((void **)&B.logits, (size_t)logits_rows * c.vocab * 4);
     A((void **)&B.xp, qgemm_xp_bytes(cap, (int)maxk));
     A((void **)&B.xp2, qgemm_xp_bytes(cap, (int)maxk));
+    A((void **)&B.ss, (size_t)((c.d_model + 15) / 16) * cap * 4);
     A((void **)&B.ids, (size_t)cap * 4);
     A((void **)&B.pos, (size_t)cap * 4);
     A((void **)&B.kc, (size_t)cap * sizeof(float *));
@@ -561,10 +563,15 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
     const smx_model_config &c = m->cfg;
     const int d = c.d_model, hd = m->hd, Hkv = c.n_kv_head;
     const int pro = m->llama ? PRO_RMS : PRO_LN;
+    // Up to 16 tokens, RMSNorm is folded into the GEMMs around it: the O and down projections
+    // write the next norm's input as parts of gamma (.) x plus per-tile sums of x^2, and the
+    // QKV (after layer 0) and gate/up GEMMs scale by 1 / rms -- no k_qprep launch per norm.
+    const bool fold = m->llama && M <= 16 && d % 256 == 0 && m->hidden % 256 == 0;
     WView posw = m->pos.view();
     SMX_HIP(launch_embed_tokens(m->tok.view(), m->llama ? nullptr : &posw, B.ids, B.pos, B.x, d, M, s));
     for (int l = 0; l < c.n_layer; l++) {
         const Layer &L = m->layers[l];
+        const bool fold_in = fold && l > 0;   // QKV parts written by the previous down projection
         const int64_t layer_off = (int64_t)l * Hkv * ctx_stride * hd;
         QgemmArgs a{};
         a.w = L.qkv.view();
@@ -585,7 +592,14 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
         a.tok_pos = B.pos;
         a.rope_cos = m->rope_cos;
         a.rope_sin = m->rope_sin;
-        SMX_HIP(launch_qgemm(a, B.x, d, pro, L.d_attn_g, L.d_attn_b, c.norm_eps, s));
+        if (fold_in) {
+            a.rss = B.ss;
+            a.rss_n = d / 16;
+            a.r_eps = c.norm_eps;
+            SMX_HIP(launch_qgemm(a, nullptr, d, PRO_NONE, nullptr, nullptr, 0.0f, s));
+        } else {
+            SMX_HIP(launch_qgemm(a, B.x, d, pro, L.d_attn_g, L.d_attn_b, c.norm_eps, s));
+        }
         // attention writes the O projection's activation parts directly (no k_qprep launch)
         if (run && attention_prefill_supported(c.n_head, Hkv, hd))
             SMX_HIP(launch_attention_prefill(B.q, m->nqkv, run->kc + layer_off, run->vc + layer_off, B.att, d,
@@ -601,6 +615,11 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
         o.y_stride = d;
         o.bias = L.d_bo;
         o.epi = EPI_RESID;
+        if (fold) {
+            o.np = B.xp;
+            o.ngamma = L.d_ffn_g;
+            o.nss = B.ss;
+        }
         SMX_HIP(launch_qgemm(o, nullptr, d, PRO_NONE, nullptr, nullptr, 0.0f, s));
         QgemmArgs g{};
         g.w = L.gu.view();
@@ -611,7 +630,14 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
         g.bias = L.d_bgu;
         g.epi = m->llama ? EPI_SILU : EPI_GELU;
         g.yp = B.xp2;   // the down projection's activation parts
-        SMX_HIP(launch_qgemm(g, B.x, d, pro, L.d_ffn_g, L.d_ffn_b, c.norm_eps, s));
+        if (fold) {
+            g.rss = B.ss;
+            g.rss_n = d / 16;
+            g.r_eps = c.norm_eps;
+            SMX_HIP(launch_qgemm(g, nullptr, d, PRO_NONE, nullptr, nullptr, 0.0f, s));
+        } else {
+            SMX_HIP(launch_qgemm(g, B.x, d, pro, L.d_ffn_g, L.d_ffn_b, c.norm_eps, s));
+        }
         QgemmArgs dn{};
         dn.w = L.down.view();
         dn.xp = B.xp2;
@@ -620,6 +646,11 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
         dn.y_stride = d;
         dn.bias = L.d_bdown;
         dn.epi = EPI_RESID;
+        if (fold && l + 1 < c.n_layer) {
+            dn.np = B.xp;
+            dn.ngamma = m->layers[l + 1].d_attn_g;
+            dn.nss = B.ss;
+        }
         SMX_HIP(launch_qgemm(dn, nullptr, m->hidden, PRO_NONE, nullptr, nullptr, 0.0f, s));
     }
     if (head_from < M) {

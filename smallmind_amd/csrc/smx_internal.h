@@ -144,6 +144,19 @@ struct QgemmArgs {
     float *const *vc_tok;
     const int32_t *tok_pos;
     const float *rope_cos, *rope_sin;
+    // RMSNorm folded across two GEMMs (up to 16 tokens, rows of whole 256-element super-blocks):
+    // RMSNorm(x) W^T = r (.) ((gamma (.) x) W^T), r = 1 / sqrt(sum x^2 / K + eps) per token.
+    // Producer (EPI_RESID): with np set, the new residual x also goes to np as the activation
+    // parts of gamma (.) x (ngamma = the next norm's gamma) and the per-token sums of x^2 over
+    // each 16-row tile to nss[tile][M].  Consumer: with rss set, xp holds those parts and each
+    // token's products are scaled by r before the epilogue, with sum x^2 = the rss_n tile sums
+    // rss[p][tok] added in order.
+    uint8_t *np;
+    const float *ngamma;
+    float *nss;
+    const float *rss;
+    int rss_n;
+    float r_eps;
 };
 // Scratch bytes of the activation parts for M tokens of K elements.
 size_t qgemm_xp_bytes(int M, int K);

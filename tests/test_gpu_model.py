@@ -86,6 +86,9 @@ def test_forward_api_matches_nocache_reference(pairs, key):
     sess.reset_kv_cache()
     got = sess.forward(toks[:5], 0)            # restart after ResetKVCache
     assert rel_err(got, full[4]) <= LOGIT_TOL
+    sess.reset_kv_cache()
+    got = sess.forward(toks[:12], 0)           # one token tile (folded RMSNorm on llama)
+    assert rel_err(got, full[11]) <= LOGIT_TOL
     sess.close()
 
 
@@ -171,16 +174,18 @@ def test_prefill_across_chunks_matches_reference():
     gm.close()
 
 
+@pytest.mark.parametrize("n_sess", [17, 12])
 @pytest.mark.parametrize("key", ["smollm-q5k", "llama-q4k", "gpt2-q8_0"])
-def test_batch_generate_lockstep_matches_single_sessions_and_reference(pairs, key):
+def test_batch_generate_lockstep_matches_single_sessions_and_reference(pairs, key, n_sess):
     """several sessions stepping together (smx_batch_generate) produce, per
     session, the greedy tokens of the reference run alone; prompts of different lengths, so
-    every step mixes positions."""
+    every step mixes positions.  Up to 16 sessions (one token tile), the RMSNorms of the
+    llama-style models are folded into the GEMMs around them."""
     from smallmind_amd.model import GpuInferenceSession
     om, gm = _pair(pairs, key)
     cfg = SMALL[key][0]
     rng = np.random.default_rng(9)
-    lens = [1, 5, 12, 20, 9, 30, 2, 17, 11, 40, 3, 25, 7, 15, 33, 19, 6]
+    lens = [1, 5, 12, 20, 9, 30, 2, 17, 11, 40, 3, 25, 7, 15, 33, 19, 6][:n_sess]
     prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.int32) for n in lens]
     n_new = 24
     sess = [gm.create_session(96) for _ in lens]
