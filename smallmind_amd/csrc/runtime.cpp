@@ -197,6 +197,9 @@ struct TokBatch {
 struct smx_session {
     smx_model *m = nullptr;
     int max_ctx = 0;
+    // KV cache row length: max_ctx rounded up to 4 positions, so K rows are 16-byte aligned
+    // (the one-launch decode attention reads them as float4)
+    int ctx_stride = 0;
     float *kc = nullptr, *vc = nullptr;
     float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
     float *scores = nullptr;   // decode attention scores [n_head][max_ctx]
@@ -266,7 +269,7 @@ int enqueue_step(smx_session *S, bool with_head, bool with_embed, hipStream_t s)
     smx_model *m = S->m;
     const smx_model_config &c = m->cfg;
     const int Hkv = c.n_kv_head, hd = m->hd;
-    const size_t layer_cache = (size_t)Hkv * S->max_ctx * hd;
+    const size_t layer_cache = (size_t)Hkv * S->ctx_stride * hd;
     WView posw = m->pos.view();
     if (with_embed)
         SMX_HIP(launch_embed(m->tok.view(), m->llama ? nullptr : &posw, S->tokens, S->pos, S->x, s));
@@ -285,7 +288,7 @@ int enqueue_step(smx_session *S, bool with_head, bool with_embed, hipStream_t s)
         a.d_model = c.d_model;
         a.kv_dim = m->kvdim;
         a.head_dim = hd;
-        a.ctx_stride = S->max_ctx;
+        a.ctx_stride = S->ctx_stride;
         a.use_rope = m->llama ? 1 : 0;
         a.k_cache = S->kc + l * layer_cache;
         a.v_cache = S->vc + l * layer_cache;
@@ -297,7 +300,7 @@ int enqueue_step(smx_session *S, bool with_head, bool with_embed, hipStream_t s)
         // long contexts: two partial attention outputs, summed by the O projection's staging
         const int att_parts = attention_pv_chunks(S->max_ctx, 2);
         SMX_HIP(launch_attention_split(S->q, a.k_cache, a.v_cache, S->att, S->scores, c.n_head, Hkv, hd,
-                                       S->max_ctx, S->pos, 0, S->max_ctx, s, 2));
+                                       S->ctx_stride, S->pos, 0, S->max_ctx, s, 2));
 
         GemvArgs o{};
         o.w = L.o.view();
@@ -396,7 +399,7 @@ int setup_persistent(smx_session *S)
     const int grid = decode_grid(fmt, m->hd, lds, m->ctx->device);
     if (grid <= 0) return SMX_OK;
     const smx_model_config &c = m->cfg;
-    const size_t layer_cache = (size_t)c.n_kv_head * S->max_ctx * m->hd;
+    const size_t layer_cache = (size_t)c.n_kv_head * S->ctx_stride * m->hd;
     std::vector<LayerDesc> hl((size_t)c.n_layer);
     for (int l = 0; l < c.n_layer; l++) {
         const Layer &L = m->layers[l];
@@ -434,7 +437,7 @@ int setup_persistent(smx_session *S)
     a.nqkv = m->nqkv;
     a.hidden = m->hidden;
     a.vocab = c.vocab;
-    a.max_ctx = S->max_ctx;
+    a.max_ctx = S->ctx_stride;   // the kernel uses it as the cache row length
     a.eps = c.norm_eps;
     a.tok = m->tok.view();
     a.posw = m->llama ? WView{} : m->pos.view();
@@ -697,7 +700,7 @@ int prefill_tokens(smx_session *S, const int32_t *tokens_host, int n, int p0, bo
         SMX_HIP(hipMemcpyAsync(B.pos, pos.data(), (size_t)M * 4, hipMemcpyHostToDevice, s));
         const bool last = i0 + M == n;
         const PrefillRun run{S->kc, S->vc, p0 + i0};
-        int rc = run_tokens(m, B, M, S->max_ctx, (want_head && last) ? M - 1 : M, s, &run);
+        int rc = run_tokens(m, B, M, S->ctx_stride, (want_head && last) ? M - 1 : M, s, &run);
         if (rc != SMX_OK) return rc;
         // the host arrays are reused by the next chunk: let this chunk's copies finish
         SMX_HIP(hipStreamSynchronize(s));
@@ -1222,9 +1225,10 @@ SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out)
     smx_session *S = new smx_session();
     S->m = m;
     S->max_ctx = max_ctx;
+    S->ctx_stride = (max_ctx + 3) & ~3;
     m->sessions.fetch_add(1);
     const smx_model_config &c = m->cfg;
-    const size_t cache = (size_t)c.n_layer * c.n_kv_head * max_ctx * m->hd * 4;
+    const size_t cache = (size_t)c.n_layer * c.n_kv_head * S->ctx_stride * m->hd * 4;
     const size_t maxv = (size_t)(m->hidden > c.d_model ? m->hidden : c.d_model);
     hipError_t e = hipSuccess;
     auto A = [&](void **p, size_t n) { if (e == hipSuccess) e = hipMalloc(p, n); };
@@ -1464,7 +1468,7 @@ SMX_API int smx_batch_generate(smx_session *const *sessions, int n_sessions, con
     // capture one lockstep step: all layers for the n tokens, head, argmax (appends each
     // session's token at pos + 1 and advances pos on the device)
     SMX_BHIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    rc = run_tokens(m, D, n, max_ctx, 0, s, nullptr);
+    rc = run_tokens(m, D, n, sessions[0]->ctx_stride, 0, s, nullptr);
     if (rc == SMX_OK) {
         const hipError_t e = launch_argmax_rows(D.logits, V, V, n, D.ids, D.pos, D.tok_arr, s);
         if (e != hipSuccess) { set_error(hipGetErrorString(e)); rc = SMX_EDEVICE; }

@@ -172,6 +172,7 @@ struct LayerDesc {
     const float *attn_g, *attn_b, *ffn_g, *ffn_b;
     const float *bqkv, *bo, *bgu, *bdown;
     float *kc, *vc;             // this layer's K [n_kv_head][hd][max_ctx] and V [n_kv_head][max_ctx][hd]
+                                // (max_ctx here = the session's cache row length)
 };
 
 struct DecodeArgs {

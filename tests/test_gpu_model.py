@@ -69,6 +69,35 @@ def test_greedy_64_tokens_and_logits(pairs, key, mode, monkeypatch):
     sess.close()
 
 
+@pytest.mark.parametrize("mode", ["graph", "persistent"])
+def test_session_context_not_a_multiple_of_four(pairs, mode, monkeypatch):
+    """A session of 83 positions keeps its KV cache rows padded to 84 (16-byte aligned K rows
+    for the one-launch decode attention); prefill, decode and a lockstep batch at that stride
+    match the reference."""
+    from smallmind_amd.model import GpuInferenceSession
+    om, gm = _pair(pairs, "llama-q4k")
+    cfg = SMALL["llama-q4k"][0]
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab_size, 21).astype(np.int32)
+    monkeypatch.setenv("SMX_DECODE", mode)
+    sess = gm.create_session(83)
+    toks, _, logits = sess.generate_greedy(prompt, 62, return_logits=True)
+    osess = om.session(83)
+    for p, t in enumerate(prompt[:-1]):
+        osess.step(int(t), p, want_logits=False)
+    tok = int(prompt[-1])
+    for i in range(62):
+        ref = osess.step(tok, len(prompt) - 1 + i)
+        assert rel_err(logits[i], ref) <= LOGIT_TOL, (i, rel_err(logits[i], ref))
+        assert int(toks[i]) == int(np.argmax(ref)), i
+        tok = int(toks[i])
+    sess.close()
+    sb = [gm.create_session(83) for _ in range(3)]
+    bt, _ = GpuInferenceSession.generate_greedy_batch(sb, [prompt, prompt[:7], prompt[:13]], 8)
+    assert np.array_equal(bt[0], toks[:8])
+    for x in sb:
+        x.close()
+
+
 @pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0"])
 def test_forward_api_matches_nocache_reference(pairs, key):
     """GpuInferenceSession.forward mirrors TransformerModel.Forward(idx, positionOffset) with the
