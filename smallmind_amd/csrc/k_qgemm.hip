@@ -969,10 +969,10 @@ template <int F>
 hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
 {
     // Rows of whole 256-element super-blocks: LDS-staged weight tiles.  Up to 16 tokens: one
-    // token tile per workgroup (16 waves splitting K from 8192 up); more: tiles of 64 tokens x 32 rows per wave, 8 waves splitting
-    // long K (or short K over few rows), else 4 waves (K-quants: 64 rows x 32 tokens on tall
-    // matrices; Q6_K 16 rows).  Chosen by measurement over the prefill shapes of the five
-    // formats at 256 tokens.
+    // token tile per workgroup (16 waves splitting K from 8192 up).  More: tiles of 64 tokens x
+    // 32 rows per wave, 8 waves splitting long K (or short K over few rows), else 4 waves
+    // (K-quants: 64 rows x 32 tokens on tall matrices; Q6_K 16 rows).  Chosen by measurement
+    // over the prefill shapes of the five formats at 256 tokens.
     if (a.w.cols % 256 == 0) {
         const bool tall = a.w.rows >= 8192;
         if (a.M > 16) {
