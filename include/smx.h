@@ -180,6 +180,17 @@ SMX_API int smx_model_upload_tensor(smx_model *m, const char *name, int type,
 /* Validates the tensor set and ties output.weight to token_embd.weight when absent
  * (GgufModelLoader.HandleWeightTying, GgufModelLoader.cs:1126-1147). */
 SMX_API int smx_model_finalize(smx_model *m);
+/* Loads a GGUF v2/v3 file (GgufReader.ReadModelInfo, GgufReader.cs:39-97, through
+ * GgufModelLoader, GgufModelLoader.cs:63-77): the configuration from its metadata as
+ * ModelConfig.FromGgufMetadata derives it (ModelConfig.cs:142-214: llama, mistral*, phi*,
+ * gpt2), then every tensor uploaded from a read-only memory map of the file and the model
+ * finalized.  Tensor data is read at the data section + each tensor entry's offset (GGUF
+ * specification).  SMX_EINVAL for a malformed or unreadable file, SMX_EUNSUPPORTED for other
+ * architectures, versions or tensor types. */
+SMX_API int smx_model_load_gguf(smx_context *ctx, const char *path, smx_model **out);
+/* Parses a GGUF file's header, metadata and tensor table and returns the derived
+ * configuration and the tensor count; no device work. */
+SMX_API int smx_gguf_read_config(const char *path, smx_model_config *cfg, int64_t *n_tensors);
 SMX_API int smx_model_weight_bytes(const smx_model *m, int64_t *bytes);
 SMX_API int smx_model_destroy(smx_model *m);
 

@@ -58,6 +58,15 @@ class ModelConfig:
         return c
 
 
+def read_gguf_config(path: str) -> ModelConfig:
+    """The ModelConfig a GGUF file's metadata describes (smx_gguf_read_config; no device work)."""
+    c = ModelConfigC()
+    n = ctypes.c_int64()
+    call("smx_gguf_read_config", str(path).encode(), ctypes.byref(c), ctypes.byref(n))
+    return ModelConfig("gpt2" if c.arch == ARCH_GPT2 else "llama", c.vocab, c.ctx, c.d_model, c.n_layer,
+                       c.n_head, c.n_kv_head, c.d_ff, float(c.rope_theta), float(c.norm_eps))
+
+
 class GpuContext:
     def __init__(self, device: int = 0):
         load()
@@ -82,6 +91,27 @@ class GpuTransformerModel:
         self._h = ctypes.c_void_p()
         call("smx_model_create", self.context._h, ctypes.byref(self._cfg), ctypes.byref(self._h))
         self._sessions = []
+
+    @classmethod
+    def from_gguf(cls, path: str, context: GpuContext | None = None, device: int = 0) -> "GpuTransformerModel":
+        """Loads a GGUF file (GgufModelLoader, GgufModelLoader.cs:63-77): configuration from the
+        metadata (ModelConfig.FromGgufMetadata, ModelConfig.cs:142-214), every tensor uploaded
+        from a memory map of the file, the model finalized (smx_model_load_gguf)."""
+        config = read_gguf_config(path)
+        self = cls.__new__(cls)
+        self.config = config
+        self.context = context or GpuContext(device)
+        self._own_ctx = context is None
+        self._cfg = config.to_c()
+        self._h = ctypes.c_void_p()
+        self._sessions = []
+        try:
+            call("smx_model_load_gguf", self.context._h, str(path).encode(), ctypes.byref(self._h))
+        except Exception:
+            if self._own_ctx:
+                self.context.close()
+            raise
+        return self
 
     def load_tensor(self, name: str, qtype: int, dims, data):
         """Uploads one GGUF tensor.  dims are GGUF order (ne0 first).  data is a host buffer

@@ -98,6 +98,35 @@ def test_session_context_not_a_multiple_of_four(pairs, mode, monkeypatch):
         x.close()
 
 
+@pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0", "smollm-q5k"])
+def test_model_from_gguf_equals_direct_upload(key, tmp_path):
+    """A model written to a GGUF file (64-byte alignment, so Q8_0 tensors are padded) and loaded
+    with smx_model_load_gguf generates the same tokens and bit-identical logits as the same
+    tensors uploaded one by one."""
+    from smallmind_amd import gguf as G
+    from smallmind_amd.model import GpuTransformerModel
+    cfg, lt, et, ht = SMALL[key]
+    om, gm, tensors = build_pair(cfg, lt, et, ht, seed=77)
+    p = tmp_path / "m.gguf"
+    G.write_gguf(str(p), G.model_metadata(cfg), [(n, q, d, x) for n, (q, d, x) in tensors.items()], alignment=64)
+    gg = GpuTransformerModel.from_gguf(str(p))
+    c = gg.config
+    assert (c.architecture, c.vocab_size, c.context_length, c.embedding_length, c.block_count, c.head_count,
+            c.head_count_kv, c.feed_forward_length) == (cfg.architecture, cfg.vocab_size, cfg.context_length,
+                                                        cfg.embedding_length, cfg.block_count, cfg.head_count,
+                                                        cfg.head_count_kv, cfg.feed_forward_length)
+    assert gg.weight_bytes() == gm.weight_bytes()
+    prompt = np.random.default_rng(8).integers(0, cfg.vocab_size, 14).astype(np.int32)
+    s1, s2 = gm.create_session(64), gg.create_session(64)
+    t1, _, l1 = s1.generate_greedy(prompt, 16, return_logits=True)
+    t2, _, l2 = s2.generate_greedy(prompt, 16, return_logits=True)
+    assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
+    s1.close()
+    s2.close()
+    gg.close()
+    gm.close()
+
+
 @pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0"])
 def test_forward_api_matches_nocache_reference(pairs, key):
     """GpuInferenceSession.forward mirrors TransformerModel.Forward(idx, positionOffset) with the
