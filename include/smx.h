@@ -180,7 +180,7 @@ SMX_API int smx_model_upload_tensor(smx_model *m, const char *name, int type,
 /* Validates the tensor set and ties output.weight to token_embd.weight when absent
  * (GgufModelLoader.HandleWeightTying, GgufModelLoader.cs:1126-1147). */
 SMX_API int smx_model_finalize(smx_model *m);
-/* Loads a GGUF v2/v3 file (GgufReader.ReadModelInfo, GgufReader.cs:39-97, through
+/* Loads a GGUF v2/v3 file (GgufReader.ReadModelInfo, GgufReader.cs:39-102, through
  * GgufModelLoader, GgufModelLoader.cs:63-77): the configuration from its metadata as
  * ModelConfig.FromGgufMetadata derives it (ModelConfig.cs:142-214: llama, mistral*, phi*,
  * gpt2), then every tensor uploaded from a read-only memory map of the file and the model

@@ -2,13 +2,13 @@
 // read-only memory map, the model configuration derived from the metadata, and every tensor
 // uploaded through smx_model_upload_tensor straight from the mapping (no host copy).
 //
-// Format (GgufReader.ReadModelInfo, GgufReader.cs:39-97): "GGUF", u32 version (2..3),
+// Format (GgufReader.ReadModelInfo, GgufReader.cs:39-102): "GGUF", u32 version (2..3),
 // u64 tensor count, u64 metadata count, metadata entries (GGUF string key, u32 value type,
 // value), tensor entries (name, u32 n_dims, u64 dims[n_dims] fastest first, u32 type,
 // u64 offset), then the data section at the next multiple of general.alignment (default 32).
 // Tensor data sits at data section + the entry's offset, as the GGUF specification and
 // llama.cpp's writer lay it out.  (GgufReader instead re-derives the offsets as a running sum
-// of tensor sizes, GgufReader.cs:91-96, which agrees only when no tensor needs alignment
+// of tensor sizes, GgufReader.cs:94-100, which agrees only when no tensor needs alignment
 // padding; the files written by smallmind_amd.gguf.write_gguf satisfy both readings when every
 // tensor size is a multiple of the alignment.)
 //

@@ -1,11 +1,11 @@
 """GGUF v3 writer for fixtures and model export.
 
-Writes the layout GgufReader reads (GgufReader.cs:39-97): "GGUF", version 3, tensor and
+Writes the layout GgufReader reads (GgufReader.cs:39-102): "GGUF", version 3, tensor and
 metadata counts, metadata entries (GGUF string key, u32 value type, value), tensor entries
 (name, n_dims, dims fastest first, GGML type, offset), and the data section at the next
 multiple of general.alignment.  Each tensor starts at an offset aligned to that alignment (the
 GGUF specification); with tensor sizes that are multiples of the alignment the offsets also
-equal GgufReader's running sum of sizes (GgufReader.cs:91-96).  Reading is done by the
+equal GgufReader's running sum of sizes (GgufReader.cs:94-100).  Reading is done by the
 backend (smx_model_load_gguf / smx_gguf_read_config).
 """
 from __future__ import annotations

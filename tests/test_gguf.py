@@ -1,7 +1,7 @@
 """GGUF files: the writer (smallmind_amd.gguf) and the backend's reader (smx_gguf_read_config,
 the parsing half of smx_model_load_gguf), checked on the CPU.  The derived configuration
 follows ModelConfig.FromGgufMetadata (ModelConfig.cs:142-214); the header / metadata / tensor
-table layout follows GgufReader.ReadModelInfo (GgufReader.cs:39-97)."""
+table layout follows GgufReader.ReadModelInfo (GgufReader.cs:39-102)."""
 import struct
 
 import numpy as np
