@@ -135,6 +135,27 @@ SMX_API int smx_gelu(const float *x_dev, float *y_dev, int64_t n, void *stream);
 /* Greedy next-token selection (replaces the T->0 limit of InferenceSession.cs:565-606):
  * index of the maximum, lowest index on ties. */
 SMX_API int smx_argmax(const float *x_dev, int n, int32_t *out_dev, void *stream);
+/* Next-token sampling options (ProductionInferenceOptions.cs:19-87); each stage is skipped at
+ * its neutral value. */
+typedef struct smx_sampling {
+    float temperature;          /* Temperature: logits * (1 / T); 1 = off */
+    int32_t top_k;              /* TopK: keep logits >= the k-th largest; 0 = off */
+    float top_p;                /* TopP: nucleus; >= 1 = off */
+    float min_p;                /* MinP: drop p < max p * min_p; 0 = off */
+    float repetition_penalty;   /* RepetitionPenalty: l > 0 ? l / r : l * r; 1 = off */
+    float presence_penalty;     /* PresencePenalty: l - presence */
+    float frequency_penalty;    /* FrequencyPenalty: l - count * frequency */
+    int32_t repetition_window;  /* RepetitionWindow: recent tokens penalised; 0 = min(n, 256) */
+} smx_sampling;
+/* The reference's sampling pipeline on the device (InferenceSession.cs:565-606: penalties ->
+ * temperature -> top-k -> softmax -> top-p -> min-p -> inverse-CDF draw, with the stages of
+ * :628-936 and SampleFromProbs :708-724).  logits (n floats) and context (n_context token ids,
+ * oldest first) are device memory; u in [0, 1) is the uniform draw the reference takes from
+ * Random.NextDouble.  probs (n floats, device) receives the final distribution and token
+ * (device) the sampled id.  Ties at the top-k / top-p cutoffs are all kept. */
+SMX_API int smx_sample(const float *logits_dev, int n, const int32_t *context_dev, int n_context,
+                       const smx_sampling *params, double u, float *probs_dev, int32_t *token_dev,
+                       void *stream);
 
 /* ---- model / session level --------------------------------------------------------------- */
 typedef struct smx_context smx_context;

@@ -59,6 +59,9 @@ def lib():
         L.smxo_gelu.argtypes = [vp, vp, ctypes.c_int]
         L.smxo_silu_mul.argtypes = [vp, vp, vp, ctypes.c_int]
         L.smxo_argmax.argtypes = [vp, ctypes.c_int]
+        L.smxo_sample.argtypes = [vp, ctypes.c_int, vp, ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_double,
+                                  ctypes.c_double, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_int,
+                                  ctypes.c_double, vp]
         L.smxo_fill_normal.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_float, vp]
         L.smxo_model_create.restype = vp
         L.smxo_model_create.argtypes = [ctypes.c_int] * 8 + [ctypes.c_float, ctypes.c_float]
@@ -198,6 +201,18 @@ def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     y = np.empty_like(g)
     lib().smxo_silu_mul(_p(g), _p(u), _p(y), g.size)
     return y
+
+
+def sample(logits: np.ndarray, u: float, context=(), temperature: float = 1.0, top_k: int = 0,
+           top_p: float = 1.0, min_p: float = 0.0, repetition_penalty: float = 1.0,
+           presence_penalty: float = 0.0, frequency_penalty: float = 0.0, window: int = 0):
+    """(token, final probabilities) of the reference's sampling pipeline at the draw u."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    ctx = np.ascontiguousarray(np.asarray(context, np.int32))
+    probs = np.empty_like(lg)
+    tok = lib().smxo_sample(_p(lg), lg.size, _p(ctx) if ctx.size else None, ctx.size, temperature, top_k, top_p,
+                            min_p, repetition_penalty, presence_penalty, frequency_penalty, window, u, _p(probs))
+    return int(tok), probs
 
 
 def fill_normal(seed: int, n: int, std: float) -> np.ndarray:

@@ -28,6 +28,10 @@
  *   smxo_forward_nocache    T=1 reduces to V-row pass-through; causal invariance; numpy
  *                           float64 forward built from torch/numpy library ops
  *   smxo_session_step       equals smxo_forward_nocache row by row (cache == no-cache)
+ *   smxo_sample             neutral options = plain softmax draw; top_k = 1 and tiny top_p
+ *                           give the argmax; penalties, temperature, top-k, top-p, min-p each
+ *                           against a numpy restatement of the stage on chosen logits; the
+ *                           draw against the inverse CDF
  */
 #include "smx_oracle.h"
 
@@ -687,6 +691,119 @@ int smxo_argmax(const float *v, int n)
     int best = 0;
     for (int i = 1; i < n; i++) if (v[i] > v[best]) best = i;
     return best;
+}
+
+/* ---- next-token sampling (InferenceSession.cs:565-606) ------------------------------------ */
+static int cmp_float_asc(const void *a, const void *b)
+{
+    const float x = *(const float *)a, y = *(const float *)b;
+    return (x > y) - (x < y);
+}
+
+typedef struct { float p; int i; } smxo_pi;
+static int cmp_prob_desc(const void *a, const void *b)
+{
+    const smxo_pi *x = (const smxo_pi *)a, *y = (const smxo_pi *)b;
+    if (x->p != y->p) return x->p < y->p ? 1 : -1;
+    return x->i - y->i;   /* ties by index (the reference's sort leaves their order open) */
+}
+
+/* NormalizeProbabilities (InferenceSession.cs:969-1010): p * (1 / sum) when sum > 0. */
+static void smxo_normalize(float *p, int n)
+{
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) sum += p[i];
+    if (sum > 0.0f) {
+        const float inv = 1.0f / sum;
+        for (int i = 0; i < n; i++) p[i] = p[i] * inv;
+    }
+}
+
+/* The whole pipeline: penalties (:765-843), temperature (:741-763), top-k (:628-664), softmax
+ * (:666-706), top-p (:845-912), min-p (:914-936), SampleFromProbs (:708-724) with the draw u.
+ * probs_out receives the final distribution; returns the sampled id. */
+int smxo_sample(const float *logits, int n, const int32_t *ctx, int n_ctx, float temperature, int top_k,
+                double top_p, double min_p, float rep, float presence, float frequency, int window, double u,
+                float *probs_out)
+{
+    float *l = (float *)malloc((size_t)n * sizeof(float));
+    memcpy(l, logits, (size_t)n * sizeof(float));
+    if (rep != 1.0f || presence != 0.0f || frequency != 0.0f) {
+        const int win = window > 0 ? window : (n_ctx < 256 ? n_ctx : 256);
+        const int start = n_ctx - win > 0 ? n_ctx - win : 0;
+        const int aw = n_ctx - start;
+        int *ids = (int *)malloc((size_t)(aw > 0 ? aw : 1) * sizeof(int));
+        int *cnt = (int *)malloc((size_t)(aw > 0 ? aw : 1) * sizeof(int));
+        int seen = 0;
+        for (int i = start; i < n_ctx; i++) {
+            int f = -1;
+            for (int j = 0; j < seen; j++)
+                if (ids[j] == ctx[i]) { f = j; break; }
+            if (f >= 0) cnt[f]++;
+            else { ids[seen] = ctx[i]; cnt[seen] = 1; seen++; }
+        }
+        for (int j = 0; j < seen; j++) {
+            const int t = ids[j];
+            if (t < 0 || t >= n) continue;
+            if (rep != 1.0f) l[t] = l[t] > 0 ? l[t] / rep : l[t] * rep;
+            if (presence != 0.0f) l[t] -= presence;
+            if (frequency != 0.0f) l[t] -= (float)cnt[j] * frequency;
+        }
+        free(ids);
+        free(cnt);
+    }
+    if (temperature != 1.0f) {
+        const float inv = 1.0f / temperature;
+        for (int i = 0; i < n; i++) l[i] *= inv;
+    }
+    if (top_k > 0 && top_k < n) {
+        float *srt = (float *)malloc((size_t)n * sizeof(float));
+        memcpy(srt, l, (size_t)n * sizeof(float));
+        qsort(srt, (size_t)n, sizeof(float), cmp_float_asc);
+        const float kth = srt[n - 1 - (top_k - 1)];   /* descending order, index k - 1 */
+        for (int i = 0; i < n; i++) l[i] = l[i] >= kth ? l[i] : -INFINITY;
+        free(srt);
+    }
+    float *p = probs_out;
+    float mx = -INFINITY;
+    for (int i = 0; i < n; i++)
+        if (l[i] != -INFINITY) mx = fmaxf(mx, l[i]);
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) {
+        p[i] = l[i] != -INFINITY ? expf(l[i] - mx) : 0.0f;
+        sum += p[i];
+    }
+    if (sum > 0.0f)
+        for (int i = 0; i < n; i++) p[i] /= sum;
+    if (top_p < 1.0) {
+        smxo_pi *o = (smxo_pi *)malloc((size_t)n * sizeof(smxo_pi));
+        for (int i = 0; i < n; i++) { o[i].p = p[i]; o[i].i = i; }
+        qsort(o, (size_t)n, sizeof(smxo_pi), cmp_prob_desc);
+        float cum = 0.0f;
+        int cut = n;
+        for (int i = 0; i < n; i++) {
+            cum += o[i].p;
+            if (cum >= top_p) { cut = i + 1; break; }
+        }
+        for (int i = cut; i < n; i++) p[o[i].i] = 0.0f;
+        free(o);
+        smxo_normalize(p, n);
+    }
+    if (min_p > 0.0) {
+        float pm = -INFINITY;
+        for (int i = 0; i < n; i++) pm = fmaxf(pm, p[i]);
+        const float thr = pm * (float)min_p;
+        for (int i = 0; i < n; i++)
+            if (p[i] < thr) p[i] = 0.0f;
+        smxo_normalize(p, n);
+    }
+    free(l);
+    double cum = 0.0;
+    for (int i = 0; i < n; i++) {
+        cum += p[i];
+        if (cum >= u) return i;
+    }
+    return n - 1;
 }
 
 static uint64_t splitmix64(uint64_t z)

@@ -93,6 +93,10 @@ int smxo_generate_greedy(smxo_model *m, const int32_t *prompt, int n_prompt, int
                          int32_t *out_tokens, int64_t *prefill_ns, int64_t *decode_ns);
 
 int smxo_argmax(const float *v, int n);
+/* Next-token sampling (InferenceSession.cs:565-606); returns the id drawn at u. */
+int smxo_sample(const float *logits, int n, const int32_t *ctx, int n_ctx, float temperature, int top_k,
+                double top_p, double min_p, float rep, float presence, float frequency, int window, double u,
+                float *probs_out);
 
 /* Deterministic N(0, std) fill (splitmix64 + Box-Muller), the oracle twin of smx_fill_normal. */
 void smxo_fill_normal(uint64_t seed, int64_t n, float std, float *out);

@@ -28,7 +28,7 @@ EXPORTS = [
     "smx_context_create", "smx_context_destroy", "smx_model_create", "smx_model_upload_tensor",
     "smx_model_finalize", "smx_model_weight_bytes", "smx_model_destroy", "smx_session_create",
     "smx_session_forward", "smx_session_generate", "smx_batch_generate", "smx_session_reset",
-    "smx_session_destroy", "smx_model_load_gguf", "smx_gguf_read_config",
+    "smx_session_destroy", "smx_model_load_gguf", "smx_gguf_read_config", "smx_sample",
 ]
 
 
@@ -44,6 +44,13 @@ class ModelConfigC(ctypes.Structure):
                 ("n_head", ctypes.c_int32), ("n_kv_head", ctypes.c_int32),
                 ("d_ff", ctypes.c_int32), ("rope_theta", ctypes.c_float),
                 ("norm_eps", ctypes.c_float), ("reserved", ctypes.c_int32 * 6)]
+
+
+class SamplingC(ctypes.Structure):
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int32), ("top_p", ctypes.c_float),
+                ("min_p", ctypes.c_float), ("repetition_penalty", ctypes.c_float),
+                ("presence_penalty", ctypes.c_float), ("frequency_penalty", ctypes.c_float),
+                ("repetition_window", ctypes.c_int32)]
 
 
 class GenStatsC(ctypes.Structure):
@@ -97,6 +104,7 @@ def load() -> ctypes.CDLL:
         "smx_silu_mul": (i32, [vp, vp, vp, i64, vp]),
         "smx_gelu": (i32, [vp, vp, i64, vp]),
         "smx_argmax": (i32, [vp, i32, vp, vp]),
+        "smx_sample": (i32, [vp, i32, vp, i32, ctypes.POINTER(SamplingC), ctypes.c_double, vp, vp, vp]),
         "smx_context_create": (i32, [i32, pp]),
         "smx_context_destroy": (i32, [vp]),
         "smx_model_create": (i32, [vp, ctypes.POINTER(ModelConfigC), pp]),

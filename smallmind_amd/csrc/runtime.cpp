@@ -978,6 +978,17 @@ SMX_API int smx_argmax(const float *x, int n, int32_t *out, void *stream)
     return SMX_OK;
 }
 
+SMX_API int smx_sample(const float *logits, int n, const int32_t *context, int n_context, const smx_sampling *p,
+                       double u, float *probs, int32_t *token, void *stream)
+{
+    if (!logits || !probs || !token || !p || n <= 0 || n_context < 0 || (n_context > 0 && !context))
+        SMX_FAIL(SMX_EINVAL, "smx_sample: bad arguments");
+    if (!(p->temperature > 0.0f) || p->top_k < 0 || p->repetition_window < 0 || !(u >= 0.0 && u < 1.0))
+        SMX_FAIL(SMX_EINVAL, "smx_sample: need temperature > 0, top_k >= 0, repetition_window >= 0, 0 <= u < 1");
+    SMX_HIP(launch_sample(logits, n, context, n_context, *p, u, probs, token, (hipStream_t)stream));
+    return SMX_OK;
+}
+
 // ---- context / model ----------------------------------------------------------------------------
 SMX_API int smx_context_create(int device, smx_context **out)
 {

@@ -230,6 +230,8 @@ hipError_t launch_attention_split(const float *q, const float *kc, const float *
                                   float *scores, int n_head, int n_kv_head, int hd, int ctx_stride,
                                   const int32_t *pos_dev, int n_pos_fixed, int max_pos, hipStream_t s,
                                   int max_chunks = 1);
+hipError_t launch_sample(const float *logits, int n, const int32_t *ctx, int n_ctx, const smx_sampling &sp,
+                         double u, float *probs, int32_t *out, hipStream_t s);
 hipError_t launch_silu_mul(const float *g, const float *u, float *y, int64_t n, hipStream_t s);
 hipError_t launch_gelu(const float *x, float *y, int64_t n, hipStream_t s);
 hipError_t launch_argmax(const float *x, int n, int32_t *out, int32_t *tokens, int32_t *pos,

@@ -233,6 +233,24 @@ def argmax(x) -> int:
     return int(out.item())
 
 
+def sample(logits, u: float, context=None, temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0,
+           min_p: float = 0.0, repetition_penalty: float = 1.0, presence_penalty: float = 0.0,
+           frequency_penalty: float = 0.0, repetition_window: int = 0):
+    """Next-token sampling in InferenceSession's order (InferenceSession.cs:565-606) on the
+    device: (token, final probabilities).  logits and context (int32 token ids, oldest first)
+    are cuda tensors; u in [0, 1) is the uniform draw (Random.NextDouble in the reference)."""
+    torch = _torch()
+    _require_cuda(logits)
+    p = _lib.SamplingC(temperature, top_k, top_p, min_p, repetition_penalty, presence_penalty,
+                       frequency_penalty, repetition_window)
+    probs = torch.empty_like(logits)
+    out = torch.empty(1, dtype=torch.int32, device=logits.device)
+    n_ctx = 0 if context is None else context.numel()
+    call("smx_sample", _ptr(logits), logits.numel(), _ptr(context) if n_ctx else None, n_ctx, ctypes.byref(p),
+         float(u), _ptr(probs), _ptr(out), _stream())
+    return int(out.item()), probs
+
+
 __all__ = ["GgufTensorType", "GpuWeightTensor", "SmxError", "dequantize", "quantize", "fill_normal",
            "rmsnorm", "layernorm", "rope_tables", "rope_", "scale_mask_softmax_", "attention_decode",
-           "silu_mul", "gelu", "argmax", "row_bytes", "BLOCK_ELEMS", "BLOCK_BYTES"]
+           "silu_mul", "gelu", "argmax", "sample", "row_bytes", "BLOCK_ELEMS", "BLOCK_BYTES"]
