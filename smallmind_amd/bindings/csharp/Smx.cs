@@ -1,0 +1,166 @@
+// Smx.cs -- P/Invoke binding of libsmx.so (include/smx.h) for SmallMind (C#/.NET).
+// Not compiled in this repository (no .NET toolchain); tests/test_bindings.py checks every
+// declaration below against include/smx.h (names, parameter counts and type mapping).
+// The backend classes follow the reference's interfaces: IWeightTensor
+// (src/SmallMind.Quantization/Tensors/IWeightTensor.cs:7-42), TransformerModel.Forward with the
+// KV cache (TransformerModel.cs:272-344, ResetKVCache :476-506), InferenceSession's sampling
+// options (ProductionInferenceOptions.cs:19-87).
+using System;
+using System.Runtime.InteropServices;
+
+namespace SmallMind.Backends.Rocm
+{
+    internal static unsafe class Smx
+    {
+        const string Lib = "smx";   // resolves libsmx.so
+
+        public const int OK = 0, EINVAL = -1, ENOMEM = -2, EDEVICE = -3, EBUSY = -4,
+                         EUNSUPPORTED = -5, ESTATE = -6, ERANGE = -7;
+        public const int F32 = 0, F16 = 1, Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14;
+
+        [StructLayout(LayoutKind.Sequential)]
+        public struct ModelConfig            // smx_model_config; ModelConfig.cs:142-258
+        {
+            public int Arch, Vocab, Ctx, DModel, NLayer, NHead, NKvHead, DFf;
+            public float RopeTheta, NormEps;
+            public fixed int Reserved[6];
+        }
+
+        [StructLayout(LayoutKind.Sequential)]
+        public struct GenStats { public double PrefillMs, DecodeMs; public int NPrefill, NDecode; }
+
+        [StructLayout(LayoutKind.Sequential)]
+        public struct Sampling               // smx_sampling; ProductionInferenceOptions.cs:19-87
+        {
+            public float Temperature; public int TopK; public float TopP, MinP,
+                RepetitionPenalty, PresencePenalty, FrequencyPenalty; public int RepetitionWindow;
+        }
+
+        // library and block formats
+        [DllImport(Lib)] public static extern IntPtr smx_version();
+        [DllImport(Lib)] public static extern IntPtr smx_last_error();
+        [DllImport(Lib)] public static extern int smx_type_block_elems(int type);
+        [DllImport(Lib)] public static extern int smx_type_block_bytes(int type);
+        [DllImport(Lib)] public static extern long smx_type_row_bytes(int type, long k);
+        [DllImport(Lib)] public static extern int smx_dequant(int type, void* blocksDev, long n, float* outDev, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_quantize(int type, float* xDev, long n, void* blocksDev, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_fill_normal(ulong seed, long n, float std, float* outDev, IntPtr stream);
+
+        // weights (IWeightTensor)
+        [DllImport(Lib)] public static extern int smx_weight_create(int type, long rows, long cols, void* blocks,
+            int blocksOnDevice, out IntPtr w);
+        [DllImport(Lib)] public static extern int smx_weight_info(IntPtr w, out int type, out long rows, out long cols);
+        [DllImport(Lib)] public static extern int smx_weight_matmul(IntPtr w, float* actDev, float* outDev, int m,
+            int k, int n, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_weight_to_float32(IntPtr w, float* outDev, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_weight_destroy(IntPtr w);
+
+        // operators
+        [DllImport(Lib)] public static extern int smx_rmsnorm(float* xDev, float* gammaDev, float* yDev, int rows, int n,
+            float eps, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_layernorm(float* xDev, float* gammaDev, float* betaDev, float* yDev,
+            int rows, int n, float eps, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_rope_tables(int maxPos, int headDim, float theta, float* cosHost,
+            float* sinHost);
+        [DllImport(Lib)] public static extern int smx_rope(float* dataDev, int nHeads, int seq, int headDim, int pos0,
+            float* cosDev, float* sinDev, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_scale_mask_softmax(float* scoresDev, float scale, int seq,
+            int kSeq, int cacheOffset, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_attention_decode(float* qDev, float* kCacheDev, float* vCacheDev,
+            float* outDev, int nHead, int nKvHead, int headDim, int ctxStride, int nPos, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_attention_prefill(float* qDev, float* kCacheDev, float* vCacheDev,
+            float* outDev, int nHead, int nKvHead, int headDim, int ctxStride, int pFirst, int nTok, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_silu_mul(float* gateDev, float* upDev, float* yDev, long n, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_gelu(float* xDev, float* yDev, long n, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_argmax(float* xDev, int n, int* outDev, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_sample(float* logitsDev, int n, int* contextDev, int nContext,
+            in Sampling p, double u, float* probsDev, int* tokenDev, IntPtr stream);
+
+        // model and sessions
+        [DllImport(Lib)] public static extern int smx_context_create(int device, out IntPtr ctx);
+        [DllImport(Lib)] public static extern int smx_context_destroy(IntPtr ctx);
+        [DllImport(Lib)] public static extern int smx_model_create(IntPtr ctx, in ModelConfig cfg, out IntPtr model);
+        [DllImport(Lib)] public static extern int smx_model_upload_tensor(IntPtr model,
+            [MarshalAs(UnmanagedType.LPUTF8Str)] string name, int ggmlType, long* dims, int ndims, void* bytes,
+            nuint nbytes, int bytesOnDevice);
+        [DllImport(Lib)] public static extern int smx_model_finalize(IntPtr model);
+        [DllImport(Lib)] public static extern int smx_model_load_gguf(IntPtr ctx,
+            [MarshalAs(UnmanagedType.LPUTF8Str)] string path, out IntPtr model);
+        [DllImport(Lib)] public static extern int smx_gguf_read_config([MarshalAs(UnmanagedType.LPUTF8Str)] string path,
+            out ModelConfig cfg, out long nTensors);
+        [DllImport(Lib)] public static extern int smx_model_weight_bytes(IntPtr model, out long bytes);
+        [DllImport(Lib)] public static extern int smx_model_destroy(IntPtr model);
+        [DllImport(Lib)] public static extern int smx_session_create(IntPtr model, int maxCtx, out IntPtr session);
+        [DllImport(Lib)] public static extern int smx_session_forward(IntPtr session, int* tokens, int nTokens,
+            int posOffset, float* logitsOut);
+        [DllImport(Lib)] public static extern int smx_session_generate(IntPtr session, int* prompt, int nPrompt, int nNew,
+            int* outTokens, float* logitsOut, GenStats* stats);
+        [DllImport(Lib)] public static extern int smx_batch_generate(IntPtr* sessions, int nSessions, int* prompts,
+            int* promptLens, int nNew, int* outTokens, GenStats* stats);
+        [DllImport(Lib)] public static extern int smx_session_reset(IntPtr session);
+        [DllImport(Lib)] public static extern int smx_session_destroy(IntPtr session);
+
+        // Status -> the exception the reference throws at the same point.
+        public static void Check(int rc)
+        {
+            if (rc == OK) return;
+            string msg = Marshal.PtrToStringUTF8(smx_last_error()) ?? "libsmx error";
+            throw rc switch
+            {
+                EINVAL => new ArgumentException(msg),            // Q8WeightTensor.cs:43-48
+                ERANGE => new ArgumentOutOfRangeException(msg),  // TransformerModel.cs:282-285
+                EBUSY => new InvalidOperationException(msg),     // InferenceSession.cs:127-144
+                _ => new InvalidOperationException(msg),
+            };
+        }
+    }
+
+    // The model on the device: loaded from a GGUF file in one call, or tensor by tensor.
+    internal sealed unsafe class GpuTransformerBackend : IDisposable
+    {
+        readonly IntPtr _ctx, _model;
+
+        public GpuTransformerBackend(string ggufPath, int device = 0)
+        {
+            Smx.Check(Smx.smx_context_create(device, out _ctx));
+            Smx.Check(Smx.smx_model_load_gguf(_ctx, ggufPath, out _model));
+        }
+
+        public GpuSession CreateSession(int maxCtx) => new GpuSession(_model, maxCtx);
+
+        public void Dispose()
+        {
+            Smx.smx_model_destroy(_model);
+            Smx.smx_context_destroy(_ctx);
+        }
+    }
+
+    // TransformerModel.Forward(idx[1,T], positionOffset) with the KV cache, for one
+    // InferenceSession.  Not thread-safe, like the session it serves (SMX_EBUSY otherwise).
+    internal sealed unsafe class GpuSession : IDisposable
+    {
+        readonly IntPtr _s;
+
+        public GpuSession(IntPtr model, int maxCtx) => Smx.Check(Smx.smx_session_create(model, maxCtx, out _s));
+
+        public void ForwardLastRow(ReadOnlySpan<int> tokens, int positionOffset, Span<float> logits)
+        {
+            fixed (int* t = tokens)
+            fixed (float* l = logits)
+                Smx.Check(Smx.smx_session_forward(_s, t, tokens.Length, positionOffset, l));
+        }
+
+        public int[] GenerateGreedy(ReadOnlySpan<int> prompt, int nNew)
+        {
+            var outTokens = new int[nNew];
+            fixed (int* p = prompt)
+            fixed (int* o = outTokens)
+                Smx.Check(Smx.smx_session_generate(_s, p, prompt.Length, nNew, o, null, null));
+            return outTokens;
+        }
+
+        public void ResetKVCache() => Smx.Check(Smx.smx_session_reset(_s));
+
+        public void Dispose() => Smx.smx_session_destroy(_s);
+    }
+}
