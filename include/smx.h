@@ -225,6 +225,14 @@ SMX_API int smx_session_forward(smx_session *s, const int32_t *tokens, int n_tok
  * out_tokens (host, n_new).  logits_out (host, n_new*vocab) may be NULL. */
 SMX_API int smx_session_generate(smx_session *s, const int32_t *prompt, int n_prompt, int n_new,
                                  int32_t *out_tokens, float *logits_out, smx_gen_stats *stats);
+/* Generation with the reference's sampling pipeline (InferenceSession.GenerateNextTokenAsync,
+ * InferenceSession.cs:478-606) on the device: as smx_session_generate, but every new token is
+ * drawn by the stages of smx_sample over the context so far (prompt and generated tokens), with
+ * draw i = the top 53 bits of splitmix64(seed + i) as a double in [0, 1) (the reference draws
+ * from System.Random, which is not reproduced).  SMX_EINVAL on a persistent-decode session. */
+SMX_API int smx_session_generate_sampled(smx_session *s, const int32_t *prompt, int n_prompt, int n_new,
+                                         const smx_sampling *params, uint64_t seed, int32_t *out_tokens,
+                                         float *logits_out, smx_gen_stats *stats);
 /* Greedy generation for n_sessions sessions of one model in lockstep: each session's prompt
  * is prefilled, then every decode step advances all sessions by one token, reading each weight
  * once per step for all of them (the reference serves sessions one at a time:

@@ -29,6 +29,7 @@ EXPORTS = [
     "smx_model_finalize", "smx_model_weight_bytes", "smx_model_destroy", "smx_session_create",
     "smx_session_forward", "smx_session_generate", "smx_batch_generate", "smx_session_reset",
     "smx_session_destroy", "smx_model_load_gguf", "smx_gguf_read_config", "smx_sample",
+    "smx_session_generate_sampled",
 ]
 
 
@@ -119,6 +120,8 @@ def load() -> ctypes.CDLL:
         "smx_session_forward": (i32, [vp, vp, i32, i32, vp]),
         "smx_session_generate": (i32, [vp, vp, i32, i32, vp, vp, ctypes.POINTER(GenStatsC)]),
         "smx_batch_generate": (i32, [vp, i32, vp, vp, i32, vp, ctypes.POINTER(GenStatsC)]),
+        "smx_session_generate_sampled": (i32, [vp, vp, i32, i32, ctypes.POINTER(SamplingC), ctypes.c_uint64, vp, vp,
+                                               ctypes.POINTER(GenStatsC)]),
         "smx_session_reset": (i32, [vp]),
         "smx_session_destroy": (i32, [vp]),
     }

@@ -95,6 +95,8 @@ namespace SmallMind.Backends.Rocm
             int posOffset, float* logitsOut);
         [DllImport(Lib)] public static extern int smx_session_generate(IntPtr session, int* prompt, int nPrompt, int nNew,
             int* outTokens, float* logitsOut, GenStats* stats);
+        [DllImport(Lib)] public static extern int smx_session_generate_sampled(IntPtr session, int* prompt,
+            int nPrompt, int nNew, in Sampling p, ulong seed, int* outTokens, float* logitsOut, GenStats* stats);
         [DllImport(Lib)] public static extern int smx_batch_generate(IntPtr* sessions, int nSessions, int* prompts,
             int* promptLens, int nNew, int* outTokens, GenStats* stats);
         [DllImport(Lib)] public static extern int smx_session_reset(IntPtr session);

@@ -64,9 +64,9 @@ __device__ void renorm(float *probs, int n, float s, float *red)
     __syncthreads();
 }
 
-__global__ __launch_bounds__(kT) void k_sample(const float *__restrict__ logits, int n,
-                                               const int32_t *__restrict__ ctx, int n_ctx, smx_sampling sp,
-                                               double u, float *__restrict__ probs, int32_t *__restrict__ out)
+// The pipeline; every thread of the workgroup calls it, and thread 0 receives the token.
+__device__ int sample_pipeline(const float *__restrict__ logits, int n, const int32_t *__restrict__ ctx, int n_ctx,
+                               const smx_sampling &sp, double u, float *__restrict__ probs)
 {
     __shared__ float redf[kW];
     __shared__ uint32_t redu[kW];
@@ -188,7 +188,34 @@ __global__ __launch_bounds__(kT) void k_sample(const float *__restrict__ logits,
                 if (run >= u) { tok = i; break; }
             }
         }
-        *out = tok;
+        return tok;
+    }
+    return 0;
+}
+
+__global__ __launch_bounds__(kT) void k_sample(const float *__restrict__ logits, int n,
+                                               const int32_t *__restrict__ ctx, int n_ctx, smx_sampling sp,
+                                               double u, float *__restrict__ probs, int32_t *__restrict__ out)
+{
+    const int tok = sample_pipeline(logits, n, ctx, n_ctx, sp, u, probs);
+    if (threadIdx.x == 0) *out = tok;
+}
+
+// End of a sampled decode step: the context is tokens[0..pos] (prompt and generated so far),
+// u = the st->counter-th draw of the stream seeded by st->seed; the token is appended at
+// tokens[pos + 1], the position advanced and the draw counter incremented.
+__global__ __launch_bounds__(kT) void k_sample_step(const float *__restrict__ logits, int n,
+                                                    int32_t *__restrict__ tokens, int32_t *__restrict__ pos,
+                                                    SampleState *__restrict__ st, float *__restrict__ probs)
+{
+    const int p = *pos;
+    const smx_sampling sp = st->params;
+    const double u = uniform_draw(st->seed, st->counter);
+    const int tok = sample_pipeline(logits, n, tokens, p + 1, sp, u, probs);
+    if (threadIdx.x == 0) {
+        tokens[p + 1] = tok;
+        *pos = p + 1;
+        st->counter = st->counter + 1;
     }
 }
 
@@ -198,6 +225,13 @@ hipError_t launch_sample(const float *logits, int n, const int32_t *ctx, int n_c
                          double u, float *probs, int32_t *out, hipStream_t s)
 {
     hipLaunchKernelGGL(k_sample, dim3(1), dim3(kT), 0, s, logits, n, ctx, n_ctx, sp, u, probs, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_sample_step(const float *logits, int n, int32_t *tokens, int32_t *pos, SampleState *st,
+                              float *probs, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_sample_step, dim3(1), dim3(kT), 0, s, logits, n, tokens, pos, st, probs);
     return hipGetLastError();
 }
 

@@ -213,6 +213,11 @@ struct smx_session {
     // kDecodeBlock chained decode steps in one graph: one launch per block of tokens when no
     // per-step logits are copied out
     hipGraphExec_t g_decode_block = nullptr;
+    // sampled generation: the step graph (embedding, layers, head logits, sampling), its device
+    // state and the probability scratch, made on first use
+    hipGraphExec_t g_sample = nullptr;
+    SampleState *samp = nullptr;
+    float *probs = nullptr;
     TokBatch pb;            // prefill chunks on the matrix cores (allocated on first use)
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     std::atomic<int> busy{0};
@@ -264,7 +269,7 @@ int parse_layer(const char *name, std::string &rest)
 // Builds the step's kernel sequence on stream s (captured into a graph by the caller).
 // with_embed = false: x already holds the step's embedding row, written by the previous decode
 // step's argmax (a step with a head folds the next step's embedding lookup into its argmax).
-int enqueue_step(smx_session *S, bool with_head, bool with_embed, hipStream_t s)
+int enqueue_step(smx_session *S, bool with_head, bool with_embed, hipStream_t s, bool sample = false)
 {
     smx_model *m = S->m;
     const smx_model_config &c = m->cfg;
@@ -336,7 +341,19 @@ int enqueue_step(smx_session *S, bool with_head, bool with_embed, hipStream_t s)
         dn.epi = EPI_RESID;
         SMX_HIP(launch_gemv(dn, 1, s));
     }
-    if (with_head) {
+    if (with_head && sample) {   // logits, then the sampling pipeline appends the token
+        GemvArgs hgt{};
+        hgt.w = m->head.view();
+        hgt.x = S->x;
+        hgt.out = S->logits;
+        hgt.gamma = m->d_out_g;
+        hgt.beta = m->d_out_b;
+        hgt.eps = c.norm_eps;
+        hgt.pro = m->llama ? PRO_RMS : PRO_LN;
+        hgt.epi = EPI_STORE;
+        SMX_HIP(launch_gemv(hgt, 1, s));
+        SMX_HIP(launch_sample_step(S->logits, c.vocab, S->tokens, S->pos, S->samp, S->probs, s));
+    } else if (with_head) {
         GemvArgs hgt{};
         hgt.w = m->head.view();
         hgt.x = S->x;
@@ -364,13 +381,14 @@ int enqueue_step(smx_session *S, bool with_head, bool with_embed, hipStream_t s)
 constexpr int kDecodeBlock = 8;
 
 // Captures `steps` consecutive steps (steps > 1: chained decode steps) into one graph.
-int capture_step(smx_session *S, bool with_head, bool with_embed, hipGraphExec_t *out, int steps = 1)
+int capture_step(smx_session *S, bool with_head, bool with_embed, hipGraphExec_t *out, int steps = 1,
+                 bool sample = false)
 {
     hipStream_t s = S->m->ctx->stream;
     hipGraph_t graph = nullptr;
     SMX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     int rc = SMX_OK;
-    for (int i = 0; i < steps && rc == SMX_OK; i++) rc = enqueue_step(S, with_head, with_embed, s);
+    for (int i = 0; i < steps && rc == SMX_OK; i++) rc = enqueue_step(S, with_head, with_embed, s, sample);
     hipError_t e = hipStreamEndCapture(s, &graph);
     if (rc != SMX_OK) {
         if (graph) (void)hipGraphDestroy(graph);
@@ -1388,6 +1406,64 @@ SMX_API int smx_session_generate(smx_session *S, const int32_t *prompt, int n_pr
     return SMX_OK;
 }
 
+SMX_API int smx_session_generate_sampled(smx_session *S, const int32_t *prompt, int n_prompt, int n_new,
+                                         const smx_sampling *params, uint64_t seed, int32_t *out_tokens,
+                                         float *logits_out, smx_gen_stats *stats)
+{
+    if (!S || !prompt || !out_tokens || !params || n_prompt <= 0 || n_new <= 0)
+        SMX_FAIL(SMX_EINVAL, "smx_session_generate_sampled: bad arguments");
+    if (!(params->temperature > 0.0f) || params->top_k < 0 || params->repetition_window < 0)
+        SMX_FAIL(SMX_EINVAL, "smx_session_generate_sampled: need temperature > 0, top_k >= 0, repetition_window >= 0");
+    BusyGuard guard(S->busy);
+    if (!guard.ok) SMX_FAIL(SMX_EBUSY, "smx_session_generate_sampled: session in use on another thread");
+    if ((int64_t)n_prompt + n_new - 1 > S->max_ctx)
+        SMX_FAIL(SMX_ERANGE, "prompt %d + new tokens %d exceed the session context %d", n_prompt, n_new, S->max_ctx);
+    if (S->persistent)
+        SMX_FAIL(SMX_EINVAL, "smx_session_generate_sampled: not available on a persistent-decode session");
+    int rc = check_tokens(S, prompt, n_prompt);
+    if (rc != SMX_OK) return rc;
+    SMX_HIP(hipSetDevice(S->m->ctx->device));
+    hipStream_t s = S->m->ctx->stream;
+    const int V = S->m->cfg.vocab;
+    if (!S->samp) {
+        SMX_HIP(hipMalloc((void **)&S->samp, sizeof(SampleState)));
+        SMX_HIP(hipMalloc((void **)&S->probs, (size_t)V * 4));
+    }
+    if (!S->g_sample && (rc = capture_step(S, true, true, &S->g_sample, 1, true)) != SMX_OK) return rc;
+    const SampleState st{*params, seed, 0};
+    const int32_t zero = 0;
+    SMX_HIP(hipMemcpyAsync(S->samp, &st, sizeof(st), hipMemcpyHostToDevice, s));
+    SMX_HIP(hipMemcpyAsync(S->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s));
+    SMX_HIP(hipMemcpyAsync(S->pos, &zero, 4, hipMemcpyHostToDevice, s));
+    SMX_HIP(hipEventRecord(S->ev[0], s));
+    if (n_prompt - 1 >= kPrefillMin) {
+        if ((rc = prefill_tokens(S, prompt, n_prompt - 1, 0, false, s)) != SMX_OK) return rc;
+        const int32_t plast = n_prompt - 1;
+        SMX_HIP(hipMemcpyAsync(S->pos, &plast, 4, hipMemcpyHostToDevice, s));
+    } else {
+        for (int i = 0; i + 1 < n_prompt; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
+    }
+    SMX_HIP(hipEventRecord(S->ev[1], s));
+    for (int i = 0; i < n_new; i++) {
+        SMX_HIP(hipGraphLaunch(S->g_sample, s));
+        if (logits_out)
+            SMX_HIP(hipMemcpyAsync(logits_out + (size_t)i * V, S->logits, (size_t)V * 4, hipMemcpyDeviceToHost, s));
+    }
+    SMX_HIP(hipEventRecord(S->ev[2], s));
+    SMX_HIP(hipMemcpyAsync(out_tokens, S->tokens + n_prompt, (size_t)n_new * 4, hipMemcpyDeviceToHost, s));
+    SMX_HIP(hipStreamSynchronize(s));
+    if (stats) {
+        float a = 0.0f, b = 0.0f;
+        SMX_HIP(hipEventElapsedTime(&a, S->ev[0], S->ev[1]));
+        SMX_HIP(hipEventElapsedTime(&b, S->ev[1], S->ev[2]));
+        stats->prefill_ms = a;
+        stats->decode_ms = b;
+        stats->n_prefill_steps = n_prompt - 1;
+        stats->n_decode_steps = n_new;
+    }
+    return SMX_OK;
+}
+
 // Upper bound on sessions per lockstep batch (one token tile of the GEMM per 16 sessions).
 constexpr int kMaxBatchSessions = 256;
 
@@ -1533,13 +1609,14 @@ SMX_API int smx_session_destroy(smx_session *S)
     if (S->g_decode) (void)hipGraphExecDestroy(S->g_decode);
     if (S->g_decode_next) (void)hipGraphExecDestroy(S->g_decode_next);
     if (S->g_decode_block) (void)hipGraphExecDestroy(S->g_decode_block);
+    if (S->g_sample) (void)hipGraphExecDestroy(S->g_sample);
     for (hipEvent_t e : S->ev) if (e) (void)hipEventDestroy(e);
     free_dev(S->kc); free_dev(S->vc); free_dev(S->x); free_dev(S->q); free_dev(S->att); free_dev(S->scores);
     free_dev(S->h); free_dev(S->logits); free_dev(S->tokens); free_dev(S->pos); free_dev(S->amax);
     free_dev(S->head_val); free_dev(S->head_idx);
     batch_free(S->pb);
     free_dev(S->d_layers); free_dev(S->bar); free_dev(S->abort_flag); free_dev(S->wg_val);
-    free_dev(S->wg_idx); free_dev(S->logits_all); free_dev(S->trace);
+    free_dev(S->wg_idx); free_dev(S->logits_all); free_dev(S->trace); free_dev(S->samp); free_dev(S->probs);
     S->m->sessions.fetch_sub(1);
     delete S;
     return SMX_OK;

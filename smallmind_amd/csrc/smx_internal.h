@@ -232,6 +232,24 @@ hipError_t launch_attention_split(const float *q, const float *kc, const float *
                                   int max_chunks = 1);
 hipError_t launch_sample(const float *logits, int n, const int32_t *ctx, int n_ctx, const smx_sampling &sp,
                          double u, float *probs, int32_t *out, hipStream_t s);
+// Device state of a sampled generation: the options, the seed of the draw stream and the
+// number of draws taken.  Draw i is uniform_draw(seed, i).
+struct SampleState {
+    smx_sampling params;
+    uint64_t seed;
+    uint64_t counter;
+};
+// splitmix64(seed + i) scaled to a double in [0, 1) (the top 53 bits)
+__host__ __device__ inline double uniform_draw(uint64_t seed, uint64_t i)
+{
+    uint64_t z = seed + i + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z = z ^ (z >> 31);
+    return (double)(z >> 11) * (1.0 / 9007199254740992.0);
+}
+hipError_t launch_sample_step(const float *logits, int n, int32_t *tokens, int32_t *pos, SampleState *st,
+                              float *probs, hipStream_t s);
 hipError_t launch_silu_mul(const float *g, const float *u, float *y, int64_t n, hipStream_t s);
 hipError_t launch_gelu(const float *x, float *y, int64_t n, hipStream_t s);
 hipError_t launch_argmax(const float *x, int n, int32_t *out, int32_t *tokens, int32_t *pos,

@@ -17,6 +17,16 @@ import numpy as np
 from ._lib import ARCH_GPT2, ARCH_LLAMA, GenStatsC, ModelConfigC, call, load
 
 
+def uniform_draw(seed: int, i: int) -> float:
+    """Draw i of smx_session_generate_sampled's stream: splitmix64(seed + i), top 53 bits."""
+    m = (1 << 64) - 1
+    z = (seed + i + 0x9E3779B97F4A7C15) & m
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+    z ^= z >> 31
+    return (z >> 11) / 9007199254740992.0
+
+
 @dataclass
 class ModelConfig:
     """Fields of SmallMind's ModelConfig (ModelConfig.cs:142-258) the forward path reads."""
@@ -184,6 +194,28 @@ class GpuInferenceSession:
         st = GenStatsC()
         call("smx_session_generate", self._h, p.ctypes.data_as(ctypes.c_void_p), p.size,
              max_new_tokens, toks.ctypes.data_as(ctypes.c_void_p),
+             logits.ctypes.data_as(ctypes.c_void_p) if return_logits else None, ctypes.byref(st))
+        stats = {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
+                 "prefill_steps": st.n_prefill_steps, "decode_steps": st.n_decode_steps}
+        return (toks, stats, logits) if return_logits else (toks, stats)
+
+    def generate_sampled(self, prompt, max_new_tokens: int, seed: int = 0, temperature: float = 0.8,
+                         top_k: int = 40, top_p: float = 0.95, min_p: float = 0.0, repetition_penalty: float = 1.0,
+                         presence_penalty: float = 0.0, frequency_penalty: float = 0.0, repetition_window: int = 0,
+                         return_logits: bool = False):
+        """Prefill + decode with the reference's sampling pipeline on the device (defaults of
+        ProductionInferenceOptions.cs:19-87); draw i is uniform_draw(seed, i).  Returns
+        (tokens, stats[, logits])."""
+        from ._lib import SamplingC
+        p = np.ascontiguousarray(prompt, dtype=np.int32).reshape(-1)
+        toks = np.empty(max_new_tokens, np.int32)
+        logits = (np.empty((max_new_tokens, self.model.config.vocab_size), np.float32)
+                  if return_logits else None)
+        sp = SamplingC(temperature, top_k, top_p, min_p, repetition_penalty, presence_penalty, frequency_penalty,
+                       repetition_window)
+        st = GenStatsC()
+        call("smx_session_generate_sampled", self._h, p.ctypes.data_as(ctypes.c_void_p), p.size, max_new_tokens,
+             ctypes.byref(sp), ctypes.c_uint64(seed), toks.ctypes.data_as(ctypes.c_void_p),
              logits.ctypes.data_as(ctypes.c_void_p) if return_logits else None, ctypes.byref(st))
         stats = {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
                  "prefill_steps": st.n_prefill_steps, "decode_steps": st.n_decode_steps}

@@ -98,6 +98,40 @@ def test_session_context_not_a_multiple_of_four(pairs, mode, monkeypatch):
         x.close()
 
 
+@pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0"])
+def test_sampled_generation_follows_the_reference_pipeline(pairs, key):
+    """smx_session_generate_sampled: at every step the drawn token is the oracle pipeline's
+    draw on that step's logits, over the context so far, at the same u (splitmix64 stream);
+    with top_k = 1 it is greedy generation."""
+    from smallmind_amd.model import uniform_draw
+    om, gm = _pair(pairs, key)
+    cfg = SMALL[key][0]
+    prompt = np.random.default_rng(12).integers(0, cfg.vocab_size, 11).astype(np.int32)
+    opts = dict(temperature=0.8, top_k=40, top_p=0.95, min_p=0.02, repetition_penalty=1.2,
+                presence_penalty=0.1, frequency_penalty=0.05)
+    s = gm.create_session(96)
+    toks, stats, logits = s.generate_sampled(prompt, 40, seed=1234, return_logits=True, **opts)
+    assert stats["decode_steps"] == 40
+    okw = {k: v for k, v in opts.items()}
+    checked = 0
+    for i in range(40):
+        ctx = np.concatenate([prompt, toks[:i]]).astype(np.int32)
+        u = uniform_draw(1234, i)
+        otok, op = O.sample(logits[i], u, context=ctx, **okw)
+        cdf = np.cumsum(op.astype(np.float64))
+        if np.min(np.abs(cdf - u)) > 2e-4:
+            assert int(toks[i]) == otok, (i, int(toks[i]), otok)
+            checked += 1
+    assert checked >= 30
+    # the first step's logits are the model's (sampling does not change the forward)
+    g, _, gl = gm.create_session(96).generate_greedy(prompt, 1, return_logits=True)
+    assert np.array_equal(gl[0], logits[0])
+    t1, _ = gm.create_session(96).generate_sampled(prompt, 16, seed=7, top_k=1)
+    t2, _ = gm.create_session(96).generate_greedy(prompt, 16)
+    assert np.array_equal(t1, t2)
+    s.close()
+
+
 @pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0", "smollm-q5k"])
 def test_model_from_gguf_equals_direct_upload(key, tmp_path):
     """A model written to a GGUF file (64-byte alignment, so Q8_0 tensors are padded) and loaded
