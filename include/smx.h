@@ -215,6 +215,26 @@ SMX_API int smx_gguf_read_config(const char *path, smx_model_config *cfg, int64_
 SMX_API int smx_model_weight_bytes(const smx_model *m, int64_t *bytes);
 SMX_API int smx_model_destroy(smx_model *m);
 
+/* Continuous batching.  The reference's BatchedInferenceEngine groups queued requests
+ * (BatchedInferenceEngine.cs:186-200) and then runs each request of a group on its own
+ * (ProcessBatchPrefillOnlyAsync, :241-259); here the members share every weight read.  A batcher
+ * holds up to max_members sessions of one model, all created with max_ctx.  smx_batcher_add
+ * prefills the session's prompt and makes it a member; the session stays marked in use
+ * (SMX_EBUSY for its own calls and for smx_session_destroy) until smx_batcher_remove or
+ * smx_batcher_destroy, which leave it as smx_session_generate would.  smx_batcher_step runs
+ * n_steps greedy steps for all members at once (one token each, at each member's own position)
+ * and writes out_tokens[member][n_steps] in member order: members keep the order they were added
+ * in, a removal closes the gap.  Members may join and leave between steps.  The model cannot be
+ * destroyed while a batcher exists. */
+typedef struct smx_batcher smx_batcher;
+SMX_API int smx_batcher_create(smx_model *m, int max_members, int max_ctx, smx_batcher **out);
+SMX_API int smx_batcher_add(smx_batcher *b, smx_session *s, const int32_t *prompt, int n_prompt);
+SMX_API int smx_batcher_remove(smx_batcher *b, smx_session *s);
+/* Returns the number of members (>= 0), or a negative status. */
+SMX_API int smx_batcher_count(const smx_batcher *b);
+SMX_API int smx_batcher_step(smx_batcher *b, int n_steps, int32_t *out_tokens);
+SMX_API int smx_batcher_destroy(smx_batcher *b);
+
 SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out);
 /* TransformerModel.Forward(idx[1,T], positionOffset) with the KV cache enabled: runs
  * n_tokens tokens at positions pos_offset.. and writes the last row's logits (vocab floats,

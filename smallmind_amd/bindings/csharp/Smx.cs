@@ -99,6 +99,14 @@ namespace SmallMind.Backends.Rocm
             int nPrompt, int nNew, in Sampling p, ulong seed, int* outTokens, float* logitsOut, GenStats* stats);
         [DllImport(Lib)] public static extern int smx_batch_generate(IntPtr* sessions, int nSessions, int* prompts,
             int* promptLens, int nNew, int* outTokens, GenStats* stats);
+        [DllImport(Lib)] public static extern int smx_batcher_create(IntPtr model, int maxMembers, int maxCtx,
+            out IntPtr batcher);
+        [DllImport(Lib)] public static extern int smx_batcher_add(IntPtr batcher, IntPtr session, int* prompt,
+            int nPrompt);
+        [DllImport(Lib)] public static extern int smx_batcher_remove(IntPtr batcher, IntPtr session);
+        [DllImport(Lib)] public static extern int smx_batcher_count(IntPtr batcher);
+        [DllImport(Lib)] public static extern int smx_batcher_step(IntPtr batcher, int nSteps, int* outTokens);
+        [DllImport(Lib)] public static extern int smx_batcher_destroy(IntPtr batcher);
         [DllImport(Lib)] public static extern int smx_session_reset(IntPtr session);
         [DllImport(Lib)] public static extern int smx_session_destroy(IntPtr session);
 

@@ -15,6 +15,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <map>
 #include <memory>
 #include <string>
 #include <vector>
@@ -1225,7 +1226,7 @@ SMX_API int smx_model_weight_bytes(const smx_model *m, int64_t *bytes)
 SMX_API int smx_model_destroy(smx_model *m)
 {
     if (!m) return SMX_OK;
-    if (m->sessions.load() != 0) SMX_FAIL(SMX_ESTATE, "smx_model_destroy: sessions still open");
+    if (m->sessions.load() != 0) SMX_FAIL(SMX_ESTATE, "smx_model_destroy: sessions or batchers still open");
     (void)hipSetDevice(m->ctx->device);
     if (!m->head_tied) m->head.release();
     m->tok.release();
@@ -1589,6 +1590,188 @@ SMX_API int smx_batch_generate(smx_session *const *sessions, int n_sessions, con
     return SMX_OK;
 }
 
+// Continuous batching: sessions join (after their own prefill) and leave between steps; every
+// step runs all current members through the layers as one token batch (one token each, each at
+// its own position) and appends each member's greedy token.  One captured graph per member
+// count, made on first use.
+struct smx_batcher {
+    smx_model *m = nullptr;
+    int cap = 0, max_ctx = 0;
+    TokBatch D;
+    std::vector<smx_session *> slot;
+    std::vector<int32_t> id, pos;   // per member: token to process next and its position
+    std::map<int, hipGraphExec_t> graphs;
+    bool dirty = true;              // member arrays on the device are stale
+    std::atomic<int> busy{0};
+};
+
+SMX_API int smx_batcher_create(smx_model *m, int max_members, int max_ctx, smx_batcher **out)
+{
+    if (!m || !out || max_members <= 0 || max_ctx <= 0) SMX_FAIL(SMX_EINVAL, "smx_batcher_create: bad arguments");
+    if (max_members > kMaxBatchSessions)
+        SMX_FAIL(SMX_EINVAL, "smx_batcher_create: %d members exceed the limit %d", max_members, kMaxBatchSessions);
+    *out = nullptr;
+    SMX_HIP(hipSetDevice(m->ctx->device));
+    auto *B = new smx_batcher();
+    B->m = m;
+    B->cap = max_members;
+    B->max_ctx = max_ctx;
+    int rc = batch_alloc(m, B->D, max_members, max_members);
+    if (rc != SMX_OK) {
+        batch_free(B->D);
+        delete B;
+        return rc;
+    }
+    m->sessions.fetch_add(1);   // the model outlives its batchers as it outlives its sessions
+    *out = B;
+    return SMX_OK;
+}
+
+SMX_API int smx_batcher_add(smx_batcher *B, smx_session *S, const int32_t *prompt, int n_prompt)
+{
+    if (!B || !S || !prompt || n_prompt <= 0) SMX_FAIL(SMX_EINVAL, "smx_batcher_add: bad arguments");
+    BusyGuard guard(B->busy);
+    if (!guard.ok) SMX_FAIL(SMX_EBUSY, "smx_batcher_add: batcher in use on another thread");
+    if (S->m != B->m) SMX_FAIL(SMX_EINVAL, "smx_batcher_add: session belongs to another model");
+    if (S->max_ctx != B->max_ctx) SMX_FAIL(SMX_EINVAL, "smx_batcher_add: session max_ctx %d, batcher %d", S->max_ctx, B->max_ctx);
+    if ((int)B->slot.size() >= B->cap) SMX_FAIL(SMX_ERANGE, "smx_batcher_add: all %d member slots in use", B->cap);
+    if (n_prompt > S->max_ctx) SMX_FAIL(SMX_ERANGE, "smx_batcher_add: prompt %d exceeds the context %d", n_prompt, S->max_ctx);
+    int rc = check_tokens(S, prompt, n_prompt);
+    if (rc != SMX_OK) return rc;
+    // the session stays marked in use while it is a member
+    int expected = 0;
+    if (!S->busy.compare_exchange_strong(expected, 1))
+        SMX_FAIL(SMX_EBUSY, "smx_batcher_add: session in use (on another thread or in a batcher)");
+    auto release = [&]() { S->busy.store(0); };
+    hipStream_t s = B->m->ctx->stream;
+    hipError_t e = hipSetDevice(B->m->ctx->device);
+    if (e == hipSuccess) e = hipMemcpyAsync(S->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) {
+        release();
+        SMX_HIP(e);
+    }
+    if (n_prompt > 1 && (rc = prefill_tokens(S, prompt, n_prompt - 1, 0, false, s)) != SMX_OK) {
+        release();
+        return rc;
+    }
+    B->slot.push_back(S);
+    B->id.push_back(prompt[n_prompt - 1]);
+    B->pos.push_back(n_prompt - 1);
+    B->dirty = true;
+    return SMX_OK;
+}
+
+// Leaves the session where smx_session_generate would: its position is that of its last token.
+SMX_API int smx_batcher_remove(smx_batcher *B, smx_session *S)
+{
+    if (!B || !S) SMX_FAIL(SMX_EINVAL, "smx_batcher_remove: bad arguments");
+    BusyGuard guard(B->busy);
+    if (!guard.ok) SMX_FAIL(SMX_EBUSY, "smx_batcher_remove: batcher in use on another thread");
+    size_t i = 0;
+    while (i < B->slot.size() && B->slot[i] != S) i++;
+    if (i == B->slot.size()) SMX_FAIL(SMX_EINVAL, "smx_batcher_remove: session is not a member");
+    SMX_HIP(hipSetDevice(B->m->ctx->device));
+    hipStream_t s = B->m->ctx->stream;
+    const int32_t p = B->pos[i];
+    SMX_HIP(hipMemcpyAsync(S->pos, &p, 4, hipMemcpyHostToDevice, s));
+    SMX_HIP(hipStreamSynchronize(s));
+    B->slot.erase(B->slot.begin() + (std::ptrdiff_t)i);
+    B->id.erase(B->id.begin() + (std::ptrdiff_t)i);
+    B->pos.erase(B->pos.begin() + (std::ptrdiff_t)i);
+    B->dirty = true;
+    S->busy.store(0);
+    return SMX_OK;
+}
+
+SMX_API int smx_batcher_count(const smx_batcher *B)
+{
+    if (!B) SMX_FAIL(SMX_EINVAL, "smx_batcher_count: null batcher");
+    return (int)B->slot.size();
+}
+
+SMX_API int smx_batcher_step(smx_batcher *B, int n_steps, int32_t *out_tokens)
+{
+    if (!B || !out_tokens || n_steps <= 0) SMX_FAIL(SMX_EINVAL, "smx_batcher_step: bad arguments");
+    BusyGuard guard(B->busy);
+    if (!guard.ok) SMX_FAIL(SMX_EBUSY, "smx_batcher_step: batcher in use on another thread");
+    const int n = (int)B->slot.size();
+    if (n == 0) SMX_FAIL(SMX_EINVAL, "smx_batcher_step: no members");
+    for (int i = 0; i < n; i++)
+        if ((int64_t)B->pos[(size_t)i] + n_steps > B->max_ctx)
+            SMX_FAIL(SMX_ERANGE, "smx_batcher_step: member %d at position %d + %d steps exceeds the context %d", i,
+                     B->pos[(size_t)i], n_steps, B->max_ctx);
+    smx_model *m = B->m;
+    SMX_HIP(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    TokBatch &D = B->D;
+    if (B->dirty) {
+        std::vector<float *> kc((size_t)n), vc((size_t)n);
+        std::vector<int32_t *> ta((size_t)n);
+        for (int i = 0; i < n; i++) {
+            kc[(size_t)i] = B->slot[(size_t)i]->kc;
+            vc[(size_t)i] = B->slot[(size_t)i]->vc;
+            ta[(size_t)i] = B->slot[(size_t)i]->tokens;
+        }
+        SMX_HIP(hipMemcpyAsync(D.ids, B->id.data(), (size_t)n * 4, hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(D.pos, B->pos.data(), (size_t)n * 4, hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(D.kc, kc.data(), (size_t)n * sizeof(float *), hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(D.vc, vc.data(), (size_t)n * sizeof(float *), hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(D.tok_arr, ta.data(), (size_t)n * sizeof(int32_t *), hipMemcpyHostToDevice, s));
+        SMX_HIP(hipStreamSynchronize(s));
+        B->dirty = false;
+    }
+    hipGraphExec_t &exec = B->graphs[n];
+    if (!exec) {
+        hipGraph_t graph = nullptr;
+        SMX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        int rc = run_tokens(m, D, n, B->slot[0]->ctx_stride, 0, s, nullptr);
+        if (rc == SMX_OK) {
+            const hipError_t e = launch_argmax_rows(D.logits, m->cfg.vocab, m->cfg.vocab, n, D.ids, D.pos, D.tok_arr, s);
+            if (e != hipSuccess) { set_error(hipGetErrorString(e)); rc = SMX_EDEVICE; }
+        }
+        const hipError_t ce = hipStreamEndCapture(s, &graph);
+        if (rc == SMX_OK && ce == hipSuccess) {
+            const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            if (ie != hipSuccess) { exec = nullptr; set_error(hipGetErrorString(ie)); rc = SMX_EDEVICE; }
+        } else if (rc == SMX_OK) {
+            set_error(hipGetErrorString(ce));
+            rc = SMX_EDEVICE;
+        }
+        if (graph) (void)hipGraphDestroy(graph);
+        if (rc != SMX_OK) {
+            B->graphs.erase(n);
+            return rc;
+        }
+    }
+    for (int k = 0; k < n_steps; k++) SMX_HIP(hipGraphLaunch(exec, s));
+    for (int i = 0; i < n; i++)
+        SMX_HIP(hipMemcpyAsync(out_tokens + (size_t)i * n_steps, B->slot[(size_t)i]->tokens + B->pos[(size_t)i] + 1,
+                               (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
+    SMX_HIP(hipStreamSynchronize(s));
+    for (int i = 0; i < n; i++) {
+        B->pos[(size_t)i] += n_steps;
+        B->id[(size_t)i] = out_tokens[(size_t)i * n_steps + n_steps - 1];
+    }
+    return SMX_OK;
+}
+
+SMX_API int smx_batcher_destroy(smx_batcher *B)
+{
+    if (!B) return SMX_OK;
+    (void)hipSetDevice(B->m->ctx->device);
+    (void)hipStreamSynchronize(B->m->ctx->stream);
+    for (auto &g : B->graphs) if (g.second) (void)hipGraphExecDestroy(g.second);
+    for (size_t i = 0; i < B->slot.size(); i++) {
+        const int32_t p = B->pos[i];
+        (void)hipMemcpy(B->slot[i]->pos, &p, 4, hipMemcpyHostToDevice);
+        B->slot[i]->busy.store(0);
+    }
+    batch_free(B->D);
+    B->m->sessions.fetch_sub(1);
+    delete B;
+    return SMX_OK;
+}
+
 SMX_API int smx_session_reset(smx_session *S)
 {
     if (!S) SMX_FAIL(SMX_EINVAL, "smx_session_reset: null session");
@@ -1604,6 +1787,8 @@ SMX_API int smx_session_reset(smx_session *S)
 SMX_API int smx_session_destroy(smx_session *S)
 {
     if (!S) return SMX_OK;
+    if (S->busy.load() != 0)
+        SMX_FAIL(SMX_EBUSY, "smx_session_destroy: session in use (on another thread or in a batcher)");
     (void)hipSetDevice(S->m->ctx->device);
     if (S->g_prefill) (void)hipGraphExecDestroy(S->g_prefill);
     if (S->g_decode) (void)hipGraphExecDestroy(S->g_decode);

@@ -154,6 +154,9 @@ class GpuTransformerModel:
         return s
 
     def close(self):
+        for b in getattr(self, "_batchers", []):
+            b.close()
+        self._batchers = []
         for s in self._sessions:
             s.close()
         self._sessions = []
@@ -249,3 +252,79 @@ class GpuInferenceSession:
         if getattr(self, "_h", None) and self._h.value:
             call("smx_session_destroy", self._h)
             self._h = ctypes.c_void_p()
+
+
+class ContinuousBatcher:
+    """Continuous batching over sessions of one model (smx_batcher_*): members join after their
+    own prefill and leave between steps; each step advances every member by one greedy token
+    with one pass over the weights.  The reference's BatchedInferenceEngine groups requests
+    (BatchedInferenceEngine.cs:186-200) but runs each one on its own (:241-259)."""
+
+    def __init__(self, model: "GpuTransformerModel", max_members: int, max_ctx: int):
+        self.model = model
+        self.max_ctx = max_ctx
+        self._h = ctypes.c_void_p()
+        call("smx_batcher_create", model._h, max_members, max_ctx, ctypes.byref(self._h))
+        self.members: list = []
+        if not hasattr(model, "_batchers"):
+            model._batchers = []
+        model._batchers.append(self)
+
+    def add(self, session: "GpuInferenceSession", prompt):
+        p = np.ascontiguousarray(prompt, dtype=np.int32).reshape(-1)
+        call("smx_batcher_add", self._h, session._h, p.ctypes.data_as(ctypes.c_void_p), p.size)
+        self.members.append(session)
+
+    def remove(self, session: "GpuInferenceSession"):
+        call("smx_batcher_remove", self._h, session._h)
+        self.members.remove(session)
+
+    def __len__(self):
+        n = load().smx_batcher_count(self._h)
+        if n < 0:
+            call("smx_batcher_count", self._h)   # raises with the library's message
+        return n
+
+    def step(self, n_steps: int = 1) -> np.ndarray:
+        """Tokens [n_members][n_steps], members in the order they were added."""
+        out = np.empty((len(self.members), n_steps), np.int32)
+        call("smx_batcher_step", self._h, n_steps, out.ctypes.data_as(ctypes.c_void_p))
+        return out
+
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            call("smx_batcher_destroy", self._h)
+            self._h = ctypes.c_void_p()
+            self.members = []
+
+
+def serve_continuous(model: "GpuTransformerModel", prompts, max_new_tokens, max_members: int, max_ctx: int,
+                     eos_token: int | None = None):
+    """Greedy generation for a queue of requests with continuous batching: at most max_members
+    requests decode together; a request leaves as soon as it has its tokens (or emits
+    eos_token) and the next queued request takes its place before the next step.  Returns one
+    token array per request, in request order."""
+    lim = [max_new_tokens] * len(prompts) if np.isscalar(max_new_tokens) else list(max_new_tokens)
+    out = [[] for _ in prompts]
+    b = ContinuousBatcher(model, max_members, max_ctx)
+    free = [model.create_session(max_ctx) for _ in range(min(max_members, len(prompts)))]
+    active = {}    # session -> request index
+    queue = list(range(len(prompts)))
+    try:
+        while queue or active:
+            while queue and free:
+                r = queue.pop(0)
+                s = free.pop()
+                b.add(s, prompts[r])
+                active[s] = r
+            toks = b.step(1)
+            for s, t in zip(list(b.members), toks[:, 0]):
+                r = active[s]
+                out[r].append(int(t))
+                if len(out[r]) >= lim[r] or (eos_token is not None and int(t) == eos_token):
+                    b.remove(s)
+                    del active[s]
+                    free.append(s)
+    finally:
+        b.close()
+    return [np.array(o, np.int32) for o in out]

@@ -302,6 +302,85 @@ def test_batch_generate_lockstep_matches_single_sessions_and_reference(pairs, ke
         s.close()
 
 
+def _ref_greedy(om, prompt, n_new):
+    osess = om.session(96)
+    for q, t in enumerate(prompt[:-1]):
+        osess.step(int(t), q, want_logits=False)
+    tok, out = int(prompt[-1]), []
+    for k in range(n_new):
+        tok = int(np.argmax(osess.step(tok, len(prompt) - 1 + k)))
+        out.append(tok)
+    return out
+
+
+@pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0", "smollm-q5k"])
+def test_continuous_batching_matches_reference_per_request(pairs, key):
+    """Continuous batching (smx_batcher_*): 11 queued requests of different prompt lengths and
+    token budgets, at most 4 decoding together; requests leave when done and queued ones join
+    between steps, so members change while others are mid-generation.  Each request's tokens
+    are the reference's greedy tokens for it alone."""
+    from smallmind_amd.model import serve_continuous
+    om, gm = _pair(pairs, key)
+    cfg = SMALL[key][0]
+    rng = np.random.default_rng(21)
+    lens = [3, 17, 1, 9, 30, 5, 12, 2, 21, 7, 14]
+    budgets = [6, 11, 4, 9, 3, 12, 7, 5, 8, 10, 6]
+    prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.int32) for n in lens]
+    outs = serve_continuous(gm, prompts, budgets, max_members=4, max_ctx=96)
+    for i, p in enumerate(prompts):
+        assert outs[i].tolist() == _ref_greedy(om, p, budgets[i]), i
+
+
+def test_batcher_membership_rules(pairs):
+    from smallmind_amd.model import ContinuousBatcher
+    from smallmind_amd.quantization import SmxError
+    om, gm = _pair(pairs, "llama-q4k")
+    cfg = SMALL["llama-q4k"][0]
+    rng = np.random.default_rng(5)
+    pa, pb = (rng.integers(0, cfg.vocab_size, n).astype(np.int32) for n in (8, 13))
+    b = ContinuousBatcher(gm, 2, 96)
+    sa, sb, sc, sd = (gm.create_session(n) for n in (96, 96, 64, 96))
+    with pytest.raises(SmxError) as e:
+        b.step(1)
+    assert e.value.code == -1                       # no members
+    b.add(sa, pa)
+    with pytest.raises(SmxError) as e:
+        sa.generate_greedy(pa, 2)                   # a member is in use
+    assert e.value.code == -4
+    with pytest.raises(SmxError) as e:
+        sa.close()
+    assert e.value.code == -4
+    with pytest.raises(SmxError) as e:
+        b.add(sa, pa)                               # already a member
+    assert e.value.code == -4
+    with pytest.raises(SmxError) as e:
+        b.add(sc, pa)                               # other max_ctx
+    assert e.value.code == -1
+    t1 = b.step(3)
+    b.add(sb, pb)                                   # joins while sa is mid-generation
+    with pytest.raises(SmxError) as e:
+        b.add(sd, pa)                               # both member slots taken
+    assert e.value.code == -7
+    t2 = b.step(2)
+    assert len(b) == 2 and t2.shape == (2, 2)
+    assert np.concatenate([t1[0], t2[0]]).tolist() == _ref_greedy(om, pa, 5)
+    assert t2[1].tolist() == _ref_greedy(om, pb, 2)
+    b.remove(sa)
+    # sa continues where generate would leave it: forward at the next position
+    nxt = sa.forward(np.array([t2[0, -1]], np.int32), len(pa) + 4)
+    full = om.forward_nocache(np.concatenate([pa, t1[0], t2[0]]), all_rows=False)
+    assert rel_err(nxt, full) <= LOGIT_TOL
+    with pytest.raises(SmxError) as e:
+        b.step(96)                                  # sb would run past its context
+    assert e.value.code == -7
+    t3 = b.step(1)
+    assert t3.shape == (1, 1) and t3[0, 0] == _ref_greedy(om, pb, 3)[-1]
+    b.close()
+    sb.generate_greedy(pb, 2)                       # released by destroy
+    for s in (sa, sb, sc, sd):
+        s.close()
+
+
 def test_batch_generate_errors(pairs):
     from smallmind_amd.model import GpuInferenceSession
     from smallmind_amd.quantization import SmxError
