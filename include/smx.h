@@ -222,13 +222,17 @@ SMX_API int smx_model_destroy(smx_model *m);
  * prefills the session's prompt and makes it a member; the session stays marked in use
  * (SMX_EBUSY for its own calls and for smx_session_destroy) until smx_batcher_remove or
  * smx_batcher_destroy, which leave it as smx_session_generate would.  smx_batcher_step runs
- * n_steps greedy steps for all members at once (one token each, at each member's own position)
+ * n_steps steps for all members at once (one token each, at each member's own position)
  * and writes out_tokens[member][n_steps] in member order: members keep the order they were added
  * in, a removal closes the gap.  Members may join and leave between steps.  The model cannot be
  * destroyed while a batcher exists. */
 typedef struct smx_batcher smx_batcher;
 SMX_API int smx_batcher_create(smx_model *m, int max_members, int max_ctx, smx_batcher **out);
 SMX_API int smx_batcher_add(smx_batcher *b, smx_session *s, const int32_t *prompt, int n_prompt);
+/* As smx_batcher_add, but each of this member's tokens is drawn by the sampling pipeline of
+ * smx_session_generate_sampled (same options, same draw stream for this seed) instead of argmax. */
+SMX_API int smx_batcher_add_sampled(smx_batcher *b, smx_session *s, const int32_t *prompt, int n_prompt,
+                                    const smx_sampling *params, uint64_t seed);
 SMX_API int smx_batcher_remove(smx_batcher *b, smx_session *s);
 /* Returns the number of members (>= 0), or a negative status. */
 SMX_API int smx_batcher_count(const smx_batcher *b);

@@ -29,7 +29,7 @@ EXPORTS = [
     "smx_model_finalize", "smx_model_weight_bytes", "smx_model_destroy", "smx_session_create",
     "smx_session_forward", "smx_session_generate", "smx_batch_generate", "smx_session_reset",
     "smx_session_destroy", "smx_model_load_gguf", "smx_gguf_read_config", "smx_sample",
-    "smx_session_generate_sampled", "smx_batcher_create", "smx_batcher_add", "smx_batcher_remove",
+    "smx_session_generate_sampled", "smx_batcher_create", "smx_batcher_add", "smx_batcher_add_sampled", "smx_batcher_remove",
     "smx_batcher_count", "smx_batcher_step", "smx_batcher_destroy",
 ]
 
@@ -125,6 +125,7 @@ def load() -> ctypes.CDLL:
                                                ctypes.POINTER(GenStatsC)]),
         "smx_batcher_create": (i32, [vp, i32, i32, pp]),
         "smx_batcher_add": (i32, [vp, vp, vp, i32]),
+        "smx_batcher_add_sampled": (i32, [vp, vp, vp, i32, ctypes.POINTER(SamplingC), ctypes.c_uint64]),
         "smx_batcher_remove": (i32, [vp, vp]),
         "smx_batcher_count": (i32, [vp]),
         "smx_batcher_step": (i32, [vp, i32, vp]),

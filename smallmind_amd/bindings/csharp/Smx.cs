@@ -103,6 +103,8 @@ namespace SmallMind.Backends.Rocm
             out IntPtr batcher);
         [DllImport(Lib)] public static extern int smx_batcher_add(IntPtr batcher, IntPtr session, int* prompt,
             int nPrompt);
+        [DllImport(Lib)] public static extern int smx_batcher_add_sampled(IntPtr batcher, IntPtr session,
+            int* prompt, int nPrompt, in Sampling p, ulong seed);
         [DllImport(Lib)] public static extern int smx_batcher_remove(IntPtr batcher, IntPtr session);
         [DllImport(Lib)] public static extern int smx_batcher_count(IntPtr batcher);
         [DllImport(Lib)] public static extern int smx_batcher_step(IntPtr batcher, int nSteps, int* outTokens);

@@ -219,7 +219,37 @@ __global__ __launch_bounds__(kT) void k_sample_step(const float *__restrict__ lo
     }
 }
 
+// Members of a lockstep step (one logits row each), after k_argmax_rows has appended each
+// member's greedy token at tokens[pos] and advanced pos: a member with sampling on replaces
+// that token (and the next step's input id) with the pipeline's draw over tokens[0..pos-1].
+__global__ __launch_bounds__(kT) void k_sample_rows(const float *__restrict__ logits, int n, int64_t stride,
+                                                    int32_t *const *__restrict__ tok_arr,
+                                                    const int32_t *__restrict__ pos, int32_t *__restrict__ ids,
+                                                    SampleState *__restrict__ st, const int32_t *__restrict__ on,
+                                                    float *__restrict__ probs)
+{
+    const int r = blockIdx.x;
+    if (!on[r]) return;   // the same for the whole workgroup
+    const int p = pos[r];
+    const smx_sampling sp = st[r].params;
+    const double u = uniform_draw(st[r].seed, st[r].counter);
+    const int tok = sample_pipeline(logits + (size_t)r * stride, n, tok_arr[r], p, sp, u, probs + (size_t)r * n);
+    if (threadIdx.x == 0) {
+        tok_arr[r][p] = tok;
+        ids[r] = tok;
+        st[r].counter = st[r].counter + 1;
+    }
+}
+
 }  // namespace
+
+hipError_t launch_sample_rows(const float *logits, int n, int64_t stride, int M, int32_t *const *tok_arr,
+                              const int32_t *pos, int32_t *ids, SampleState *st, const int32_t *on, float *probs,
+                              hipStream_t s)
+{
+    hipLaunchKernelGGL(k_sample_rows, dim3(M), dim3(kT), 0, s, logits, n, stride, tok_arr, pos, ids, st, on, probs);
+    return hipGetLastError();
+}
 
 hipError_t launch_sample(const float *logits, int n, const int32_t *ctx, int n_ctx, const smx_sampling &sp,
                          double u, float *probs, int32_t *out, hipStream_t s)

@@ -1600,7 +1600,12 @@ struct smx_batcher {
     TokBatch D;
     std::vector<smx_session *> slot;
     std::vector<int32_t> id, pos;   // per member: token to process next and its position
-    std::map<int, hipGraphExec_t> graphs;
+    std::vector<SampleState> samp;  // per member: sampling options, seed and draws taken
+    std::vector<int32_t> on;        // per member: 1 = sampled, 0 = greedy
+    SampleState *d_samp = nullptr;  // device copies, max_members entries
+    int32_t *d_on = nullptr;
+    float *d_probs = nullptr;       // sampling scratch, max_members x vocab
+    std::map<int, hipGraphExec_t> graphs;   // key: 2 * members + (any member sampled)
     bool dirty = true;              // member arrays on the device are stale
     std::atomic<int> busy{0};
 };
@@ -1617,19 +1622,28 @@ SMX_API int smx_batcher_create(smx_model *m, int max_members, int max_ctx, smx_b
     B->cap = max_members;
     B->max_ctx = max_ctx;
     int rc = batch_alloc(m, B->D, max_members, max_members);
-    if (rc != SMX_OK) {
+    hipError_t e = hipSuccess;
+    if (rc == SMX_OK) e = hipMalloc((void **)&B->d_samp, (size_t)max_members * sizeof(SampleState));
+    if (rc == SMX_OK && e == hipSuccess) e = hipMalloc((void **)&B->d_on, (size_t)max_members * 4);
+    if (rc == SMX_OK && e == hipSuccess) e = hipMalloc((void **)&B->d_probs, (size_t)max_members * m->cfg.vocab * 4);
+    if (rc != SMX_OK || e != hipSuccess) {
         batch_free(B->D);
+        free_dev(B->d_samp); free_dev(B->d_on); free_dev(B->d_probs);
         delete B;
-        return rc;
+        if (rc != SMX_OK) return rc;
+        SMX_FAIL(SMX_ENOMEM, "smx_batcher_create: %s", hipGetErrorString(e));
     }
     m->sessions.fetch_add(1);   // the model outlives its batchers as it outlives its sessions
     *out = B;
     return SMX_OK;
 }
 
-SMX_API int smx_batcher_add(smx_batcher *B, smx_session *S, const int32_t *prompt, int n_prompt)
+static int batcher_add(smx_batcher *B, smx_session *S, const int32_t *prompt, int n_prompt,
+                       const smx_sampling *params, uint64_t seed)
 {
     if (!B || !S || !prompt || n_prompt <= 0) SMX_FAIL(SMX_EINVAL, "smx_batcher_add: bad arguments");
+    if (params && (!(params->temperature > 0.0f) || params->top_k < 0 || params->repetition_window < 0))
+        SMX_FAIL(SMX_EINVAL, "smx_batcher_add_sampled: need temperature > 0, top_k >= 0, repetition_window >= 0");
     BusyGuard guard(B->busy);
     if (!guard.ok) SMX_FAIL(SMX_EBUSY, "smx_batcher_add: batcher in use on another thread");
     if (S->m != B->m) SMX_FAIL(SMX_EINVAL, "smx_batcher_add: session belongs to another model");
@@ -1657,8 +1671,22 @@ SMX_API int smx_batcher_add(smx_batcher *B, smx_session *S, const int32_t *promp
     B->slot.push_back(S);
     B->id.push_back(prompt[n_prompt - 1]);
     B->pos.push_back(n_prompt - 1);
+    B->samp.push_back(params ? SampleState{*params, seed, 0} : SampleState{});
+    B->on.push_back(params ? 1 : 0);
     B->dirty = true;
     return SMX_OK;
+}
+
+SMX_API int smx_batcher_add(smx_batcher *B, smx_session *S, const int32_t *prompt, int n_prompt)
+{
+    return batcher_add(B, S, prompt, n_prompt, nullptr, 0);
+}
+
+SMX_API int smx_batcher_add_sampled(smx_batcher *B, smx_session *S, const int32_t *prompt, int n_prompt,
+                                    const smx_sampling *params, uint64_t seed)
+{
+    if (!params) SMX_FAIL(SMX_EINVAL, "smx_batcher_add_sampled: null params");
+    return batcher_add(B, S, prompt, n_prompt, params, seed);
 }
 
 // Leaves the session where smx_session_generate would: its position is that of its last token.
@@ -1678,6 +1706,8 @@ SMX_API int smx_batcher_remove(smx_batcher *B, smx_session *S)
     B->slot.erase(B->slot.begin() + (std::ptrdiff_t)i);
     B->id.erase(B->id.begin() + (std::ptrdiff_t)i);
     B->pos.erase(B->pos.begin() + (std::ptrdiff_t)i);
+    B->samp.erase(B->samp.begin() + (std::ptrdiff_t)i);
+    B->on.erase(B->on.begin() + (std::ptrdiff_t)i);
     B->dirty = true;
     S->busy.store(0);
     return SMX_OK;
@@ -1717,16 +1747,23 @@ SMX_API int smx_batcher_step(smx_batcher *B, int n_steps, int32_t *out_tokens)
         SMX_HIP(hipMemcpyAsync(D.kc, kc.data(), (size_t)n * sizeof(float *), hipMemcpyHostToDevice, s));
         SMX_HIP(hipMemcpyAsync(D.vc, vc.data(), (size_t)n * sizeof(float *), hipMemcpyHostToDevice, s));
         SMX_HIP(hipMemcpyAsync(D.tok_arr, ta.data(), (size_t)n * sizeof(int32_t *), hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(B->d_samp, B->samp.data(), (size_t)n * sizeof(SampleState), hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(B->d_on, B->on.data(), (size_t)n * 4, hipMemcpyHostToDevice, s));
         SMX_HIP(hipStreamSynchronize(s));
         B->dirty = false;
     }
-    hipGraphExec_t &exec = B->graphs[n];
+    bool any = false;
+    for (int v : B->on) any = any || v;
+    hipGraphExec_t &exec = B->graphs[2 * n + (any ? 1 : 0)];
     if (!exec) {
         hipGraph_t graph = nullptr;
         SMX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
         int rc = run_tokens(m, D, n, B->slot[0]->ctx_stride, 0, s, nullptr);
         if (rc == SMX_OK) {
-            const hipError_t e = launch_argmax_rows(D.logits, m->cfg.vocab, m->cfg.vocab, n, D.ids, D.pos, D.tok_arr, s);
+            const int V = m->cfg.vocab;
+            hipError_t e = launch_argmax_rows(D.logits, V, V, n, D.ids, D.pos, D.tok_arr, s);
+            if (e == hipSuccess && any)
+                e = launch_sample_rows(D.logits, V, V, n, D.tok_arr, D.pos, D.ids, B->d_samp, B->d_on, B->d_probs, s);
             if (e != hipSuccess) { set_error(hipGetErrorString(e)); rc = SMX_EDEVICE; }
         }
         const hipError_t ce = hipStreamEndCapture(s, &graph);
@@ -1739,7 +1776,7 @@ SMX_API int smx_batcher_step(smx_batcher *B, int n_steps, int32_t *out_tokens)
         }
         if (graph) (void)hipGraphDestroy(graph);
         if (rc != SMX_OK) {
-            B->graphs.erase(n);
+            B->graphs.erase(2 * n + (any ? 1 : 0));
             return rc;
         }
     }
@@ -1751,6 +1788,7 @@ SMX_API int smx_batcher_step(smx_batcher *B, int n_steps, int32_t *out_tokens)
     for (int i = 0; i < n; i++) {
         B->pos[(size_t)i] += n_steps;
         B->id[(size_t)i] = out_tokens[(size_t)i * n_steps + n_steps - 1];
+        if (B->on[(size_t)i]) B->samp[(size_t)i].counter += (uint64_t)n_steps;
     }
     return SMX_OK;
 }
@@ -1767,6 +1805,7 @@ SMX_API int smx_batcher_destroy(smx_batcher *B)
         B->slot[i]->busy.store(0);
     }
     batch_free(B->D);
+    free_dev(B->d_samp); free_dev(B->d_on); free_dev(B->d_probs);
     B->m->sessions.fetch_sub(1);
     delete B;
     return SMX_OK;

@@ -248,6 +248,9 @@ __host__ __device__ inline double uniform_draw(uint64_t seed, uint64_t i)
     z = z ^ (z >> 31);
     return (double)(z >> 11) * (1.0 / 9007199254740992.0);
 }
+hipError_t launch_sample_rows(const float *logits, int n, int64_t stride, int M, int32_t *const *tok_arr,
+                              const int32_t *pos, int32_t *ids, SampleState *st, const int32_t *on, float *probs,
+                              hipStream_t s);
 hipError_t launch_sample_step(const float *logits, int n, int32_t *tokens, int32_t *pos, SampleState *st,
                               float *probs, hipStream_t s);
 hipError_t launch_silu_mul(const float *g, const float *u, float *y, int64_t n, hipStream_t s);

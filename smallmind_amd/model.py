@@ -270,9 +270,21 @@ class ContinuousBatcher:
             model._batchers = []
         model._batchers.append(self)
 
-    def add(self, session: "GpuInferenceSession", prompt):
+    def add(self, session: "GpuInferenceSession", prompt, sampling: dict | None = None, seed: int = 0):
+        """Prefills the prompt and makes the session a member; with sampling (keyword options of
+        generate_sampled) its tokens are drawn as generate_sampled draws them for this seed."""
         p = np.ascontiguousarray(prompt, dtype=np.int32).reshape(-1)
-        call("smx_batcher_add", self._h, session._h, p.ctypes.data_as(ctypes.c_void_p), p.size)
+        if sampling is None:
+            call("smx_batcher_add", self._h, session._h, p.ctypes.data_as(ctypes.c_void_p), p.size)
+        else:
+            from ._lib import SamplingC
+            o = dict(temperature=0.8, top_k=40, top_p=0.95, min_p=0.0, repetition_penalty=1.0,
+                     presence_penalty=0.0, frequency_penalty=0.0, repetition_window=0)
+            o.update(sampling)
+            sp = SamplingC(o["temperature"], o["top_k"], o["top_p"], o["min_p"], o["repetition_penalty"],
+                           o["presence_penalty"], o["frequency_penalty"], o["repetition_window"])
+            call("smx_batcher_add_sampled", self._h, session._h, p.ctypes.data_as(ctypes.c_void_p), p.size,
+                 ctypes.byref(sp), ctypes.c_uint64(seed))
         self.members.append(session)
 
     def remove(self, session: "GpuInferenceSession"):

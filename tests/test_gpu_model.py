@@ -331,6 +331,61 @@ def test_continuous_batching_matches_reference_per_request(pairs, key):
         assert outs[i].tolist() == _ref_greedy(om, p, budgets[i]), i
 
 
+def _check_sampled_chain(om, prompt, toks, opts, seed, min_checked):
+    """Each GPU token equals the oracle pipeline's draw on the reference logits for that step,
+    over the context so far, at the same u, except where u lies within 2e-3 of a step of the
+    oracle's CDF (there the GPU's logits may round the other way); options that keep only a
+    few tokens leave most draws checkable."""
+    from smallmind_amd.model import uniform_draw
+    opts = dict(opts)
+    opts["window"] = opts.pop("repetition_window", 0)
+    osess = om.session(96)
+    for q, t in enumerate(prompt[:-1]):
+        osess.step(int(t), q, want_logits=False)
+    tok, checked = int(prompt[-1]), 0
+    for i in range(len(toks)):
+        ref = osess.step(tok, len(prompt) - 1 + i)
+        u = uniform_draw(seed, i)
+        ctx = np.concatenate([prompt, toks[:i]]).astype(np.int32)
+        otok, op = O.sample(ref, u, context=ctx, **opts)
+        if np.min(np.abs(np.cumsum(op.astype(np.float64)) - u)) > 2e-3:
+            assert int(toks[i]) == otok, (i, int(toks[i]), otok)
+            checked += 1
+        tok = int(toks[i])
+    assert checked >= min_checked
+
+
+@pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0"])
+def test_batcher_sampled_members(pairs, key):
+    """Sampled and greedy members in one batcher: greedy members keep the reference's greedy
+    tokens, sampled ones draw the reference pipeline's token at every step; members leave and
+    the draw streams continue."""
+    from smallmind_amd.model import ContinuousBatcher
+    om, gm = _pair(pairs, key)
+    cfg = SMALL[key][0]
+    rng = np.random.default_rng(33)
+    pa, pb, pc = (rng.integers(0, cfg.vocab_size, n).astype(np.int32) for n in (6, 14, 3))
+    oa = dict(temperature=0.9, top_k=50, top_p=0.9, min_p=0.0)
+    oc = dict(temperature=0.7, top_k=20, top_p=1.0, min_p=0.05, repetition_penalty=1.3, presence_penalty=0.2,
+              frequency_penalty=0.1, repetition_window=8)
+    b = ContinuousBatcher(gm, 4, 96)
+    sa, sb, sc = (gm.create_session(96) for _ in range(3))
+    b.add(sa, pa, sampling=oa, seed=11)
+    b.add(sb, pb)
+    b.add(sc, pc, sampling=oc, seed=99)
+    t1 = b.step(5)
+    b.remove(sb)
+    t2 = b.step(5)
+    b.close()
+    assert t1[1].tolist() == _ref_greedy(om, pb, 5)
+    full = dict(temperature=0.8, top_k=40, top_p=0.95, min_p=0.0, repetition_penalty=1.0, presence_penalty=0.0,
+                frequency_penalty=0.0, repetition_window=0)
+    _check_sampled_chain(om, pa, np.concatenate([t1[0], t2[0]]), {**full, **oa}, 11, 6)
+    _check_sampled_chain(om, pc, np.concatenate([t1[2], t2[1]]), {**full, **oc}, 99, 6)
+    for s in (sa, sb, sc):
+        s.close()
+
+
 def test_batcher_membership_rules(pairs):
     from smallmind_amd.model import ContinuousBatcher
     from smallmind_amd.quantization import SmxError
