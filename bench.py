@@ -127,6 +127,25 @@ def other_configs():
         "decode_tok_s_aggregate": round(wl.sessions * wl.new_tokens / (st["decode_ms"] * 1e-3), 1),
         "decode_ms_per_step": round(st["decode_ms"] / wl.new_tokens, 4),
         "weight_bytes": int(model.weight_bytes())}
+    # the same 16 requests through the continuous batcher, one step per call as a serving loop
+    # runs it (each call returns its tokens to the host before the next step is queued)
+    import time
+
+    from smallmind_amd.model import ContinuousBatcher
+    log("other configs: smollm-1.7b-q5_k through the continuous batcher")
+    b = ContinuousBatcher(model, wl.sessions, wl.prompt_len + wl.new_tokens)
+    for x, p in zip(sess, prompts):
+        b.add(x, p)
+    for _ in range(4):
+        b.step(1)                                                     # warmup (graph capture)
+    n_steps = wl.new_tokens - 8
+    t0 = time.perf_counter()
+    for _ in range(n_steps):
+        b.step(1)
+    dt = time.perf_counter() - t0
+    b.close()
+    out["smollm-1.7b-q5_k"]["continuous_batcher_ms_per_step"] = round(dt * 1e3 / n_steps, 4)
+    out["smollm-1.7b-q5_k"]["continuous_batcher_tok_s_aggregate"] = round(wl.sessions * n_steps / dt, 1)
     for x in sess:
         x.close()
     model.close()

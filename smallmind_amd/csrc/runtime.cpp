@@ -1781,9 +1781,12 @@ SMX_API int smx_batcher_step(smx_batcher *B, int n_steps, int32_t *out_tokens)
         }
     }
     for (int k = 0; k < n_steps; k++) SMX_HIP(hipGraphLaunch(exec, s));
-    for (int i = 0; i < n; i++)
-        SMX_HIP(hipMemcpyAsync(out_tokens + (size_t)i * n_steps, B->slot[(size_t)i]->tokens + B->pos[(size_t)i] + 1,
-                               (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
+    if (n_steps == 1)   // the step's tokens are also each member's next input id: one copy
+        SMX_HIP(hipMemcpyAsync(out_tokens, D.ids, (size_t)n * 4, hipMemcpyDeviceToHost, s));
+    else
+        for (int i = 0; i < n; i++)
+            SMX_HIP(hipMemcpyAsync(out_tokens + (size_t)i * n_steps, B->slot[(size_t)i]->tokens + B->pos[(size_t)i] + 1,
+                                   (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
     SMX_HIP(hipStreamSynchronize(s));
     for (int i = 0; i < n; i++) {
         B->pos[(size_t)i] += n_steps;
