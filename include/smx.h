@@ -140,7 +140,9 @@ SMX_API int smx_argmax(const float *x_dev, int n, int32_t *out_dev, void *stream
 typedef struct smx_sampling {
     float temperature;          /* Temperature: logits * (1 / T); 1 = off */
     int32_t top_k;              /* TopK: keep logits >= the k-th largest; 0 = off */
-    float top_p;                /* TopP: nucleus; >= 1 = off */
+    double top_p;               /* TopP (a double, as ProductionInferenceOptions.cs:31 and the
+                                   float-sum >= double comparison of InferenceSession.cs:896 have it);
+                                   >= 1 = off */
     float min_p;                /* MinP: drop p < max p * min_p; 0 = off */
     float repetition_penalty;   /* RepetitionPenalty: l > 0 ? l / r : l * r; 1 = off */
     float presence_penalty;     /* PresencePenalty: l - presence */

@@ -72,6 +72,11 @@ def lib():
         L.smxo_session_create.restype = vp
         L.smxo_session_create.argtypes = [vp, ctypes.c_int]
         L.smxo_session_step.argtypes = [vp, ctypes.c_int32, ctypes.c_int, vp]
+        L.smxo_session_prefill.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp]
+        L.smxo_multi_step.argtypes = [vp, vp, vp, ctypes.c_int, vp]
+        L.smxo_step_tokens.argtypes = [vp, vp, vp, ctypes.c_int, vp, ctypes.c_int]
+        L.smxo_set_threads.argtypes = [ctypes.c_int]
+        L.smxo_get_threads.restype = ctypes.c_int
         L.smxo_session_destroy.argtypes = [vp]
         L.smxo_generate_greedy.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp, vp, vp]
         _ = c_f32p
@@ -215,6 +220,16 @@ def sample(logits: np.ndarray, u: float, context=(), temperature: float = 1.0, t
     return int(tok), probs
 
 
+def set_threads(n: int) -> None:
+    """Threads for the oracle's linears and attention (0 = all cores).  Results are
+    bit-identical for every thread count."""
+    lib().smxo_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(lib().smxo_get_threads())
+
+
 def fill_normal(seed: int, n: int, std: float) -> np.ndarray:
     out = np.empty(n, np.float32)
     lib().smxo_fill_normal(seed, n, std, _p(out))
@@ -254,6 +269,38 @@ class OracleModel:
     def session(self, max_ctx: int) -> "OracleSession":
         return OracleSession(self, max_ctx)
 
+    def multi_step(self, sessions, tokens, positions) -> np.ndarray:
+        """One token per session (distinct sessions of this model) in one batched pass;
+        logits [n][V], bit-identical to n OracleSession.step calls."""
+        n = len(sessions)
+        hs = (ctypes.c_void_p * n)(*[s._h for s in sessions])
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        p = np.ascontiguousarray(positions, dtype=np.int32)
+        out = np.empty((n, self.vocab), np.float32)
+        rc = lib().smxo_multi_step(hs, _p(t), _p(p), n, _p(out))
+        if rc:
+            raise ValueError(f"multi_step failed ({rc})")
+        return out
+
+    def prefill_many(self, sessions, prompts):
+        """Each session's prompt at positions 0.. in one batched pass (all prompts' tokens share
+        every weight load); bit-identical to prefilling each session token by token."""
+        ss, toks, pos = [], [], []
+        for s, p in zip(sessions, prompts):
+            p = np.asarray(p, np.int32).reshape(-1)
+            ss += [s._h] * p.size
+            toks.append(p)
+            pos.append(np.arange(p.size, dtype=np.int32))
+        n = len(ss)
+        if n == 0:
+            return
+        hs = (ctypes.c_void_p * n)(*ss)
+        t = np.ascontiguousarray(np.concatenate(toks), dtype=np.int32)
+        q = np.ascontiguousarray(np.concatenate(pos), dtype=np.int32)
+        rc = lib().smxo_step_tokens(hs, _p(t), _p(q), n, None, n)
+        if rc:
+            raise ValueError(f"step_tokens failed ({rc})")
+
     def generate_greedy(self, prompt, n_new):
         p = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.empty(n_new, np.int32)
@@ -284,6 +331,16 @@ class OracleSession:
         rc = lib().smxo_session_step(self._h, token, pos, _p(out) if want_logits else None)
         if rc:
             raise ValueError(f"session_step failed ({rc})")
+        return out
+
+    def prefill(self, tokens, pos0: int = 0, want_logits: bool = False):
+        """tokens at positions pos0.. in one batched pass (bit-identical to step() per token);
+        returns the last token's logits when want_logits."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty(self.model.vocab, np.float32) if want_logits else None
+        rc = lib().smxo_session_prefill(self._h, _p(t), t.size, pos0, _p(out) if want_logits else None)
+        if rc:
+            raise ValueError(f"session_prefill failed ({rc})")
         return out
 
     def __del__(self):

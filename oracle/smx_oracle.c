@@ -41,6 +41,11 @@
 #include <string.h>
 #include <time.h>
 
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+#include <immintrin.h>
+
 /* ------------------------------------------------------------------------------------ */
 /* fp16                                                                                 */
 /* ------------------------------------------------------------------------------------ */
@@ -831,6 +836,8 @@ void smxo_fill_normal(uint64_t seed, int64_t n, float std, float *out)
 /* model                                                                                */
 /* ------------------------------------------------------------------------------------ */
 
+static float *interleave8(float *W, int N, int K);
+
 typedef struct {
     float *attn_g, *attn_b;
     float *wq, *wk, *wv, *bq, *bk, *bv;   /* as uploaded */
@@ -852,7 +859,6 @@ struct smxo_session {
     smxo_model *m;
     int max_ctx;
     float *kc, *vc;     /* [L][Hkv][max_ctx][hd] */
-    float *x, *h, *qkv, *q, *att, *y, *t1, *t2, *t3, *scores;
 };
 
 smxo_model *smxo_model_create(int arch, int vocab, int ctx, int d, int n_layer, int n_head,
@@ -902,12 +908,23 @@ int smxo_model_set_tensor(smxo_model *m, const char *name, int type, const uint8
                           int64_t n_elems)
 {
     int64_t expect = 0;
+    if (m->finalized) return -5;
     float **slot = tensor_slot(m, name, &expect);
     if (!slot) return -1;
     if (expect != n_elems) return -2;
     float *buf = (float *)malloc(sizeof(float) * (size_t)n_elems);
     if (!buf) return -3;
-    if (smxo_dequant(type, bytes, n_elems, buf)) { free(buf); return -4; }
+    /* whole blocks per chunk, dequantized in parallel (each element depends on its block only) */
+    const int be = smxo_block_elems(type), bb = smxo_block_bytes(type);
+    if (!be || n_elems % be) { free(buf); return -4; }
+    const int64_t chunk = (int64_t)be * 4096, nchunk = (n_elems + chunk - 1) / chunk;
+    int bad = 0;
+#pragma omp parallel for schedule(static) num_threads(smxo_get_threads()) reduction(|:bad)
+    for (int64_t c = 0; c < nchunk; c++) {
+        const int64_t e0 = c * chunk, n = n_elems - e0 < chunk ? n_elems - e0 : chunk;
+        bad |= smxo_dequant(type, bytes + e0 / be * bb, n, buf + e0) != 0;
+    }
+    if (bad) { free(buf); return -4; }
     free(*slot);
     *slot = buf;
     return 0;
@@ -923,6 +940,7 @@ static float *concat3(const float *a, size_t na, const float *b, size_t nb, cons
 int smxo_model_finalize(smxo_model *m)
 {
     int d = m->d, kv = m->kvdim;
+    if (m->finalized) return 0;
     if (!m->tok || !m->out_g) return -1;
     if (m->arch == SMXO_ARCH_GPT2 && (!m->pos || !m->out_b)) return -1;
     if (!m->head) {   /* HandleWeightTying (GgufModelLoader.cs:1126-1147) */
@@ -946,6 +964,17 @@ int smxo_model_finalize(smxo_model *m)
         if (m->arch == SMXO_ARCH_LLAMA && !l->wg) return -3;
         if (m->arch == SMXO_ARCH_GPT2 && (!l->attn_b || !l->ffn_b)) return -3;
     }
+    /* the linears' weights in the 8-row interleaved layout linear() reads */
+    for (int i = 0; i < m->L; i++) {
+        olayer *l = &m->layers[i];
+        if (l->wq && l->wqkv != l->wq) { free(l->wq); free(l->wk); free(l->wv); l->wq = l->wk = l->wv = NULL; }
+        l->wqkv = interleave8(l->wqkv, m->nqkv, d);
+        l->wo = interleave8(l->wo, d, d);
+        l->wg = interleave8(l->wg, m->hidden, d);
+        l->wu = interleave8(l->wu, m->hidden, d);
+        l->wd = interleave8(l->wd, d, m->hidden);
+    }
+    m->head = interleave8(m->head, m->vocab, d);
     if (m->arch == SMXO_ARCH_LLAMA) {
         m->cos_t = (float *)malloc(sizeof(float) * (size_t)m->ctx * (m->hd / 2));
         m->sin_t = (float *)malloc(sizeof(float) * (size_t)m->ctx * (m->hd / 2));
@@ -969,32 +998,105 @@ void smxo_model_destroy(smxo_model *m)
     free(m->head); free(m->cos_t); free(m->sin_t); free(m);
 }
 
-/* Linear.ForwardFP32 (NeuralNet.cs:233-298): y = x * W^T, then + bias.  Each output
- * accumulates over k in order with fused multiply-add; eight outputs run side by side. */
-static void linear(const float *x, int T, int K, const float *W, const float *bias, int N, float *y)
+/* Linear.ForwardFP32 (NeuralNet.cs:233-298): y = x * W^T, then + bias.  Every output is one
+ * chain of fused multiply-adds over k = 0..K-1 in order, starting from 0, then the bias add:
+ * the same arithmetic whatever the tiling, thread count or vector width, so the threaded and
+ * vectorised form below gives bit-identical outputs to a single-threaded scalar loop
+ * (tests/test_oracle.py checks this).  Weights are kept as 8-row blocks interleaved by k,
+ * Wi[block][k][8] (rows past N zero), so one vector load serves 8 rows' chains; row blocks run
+ * over the threads, and with several tokens, 8 tokens share each weight load. */
+static int g_threads = 0;   /* 0: OpenMP default */
+
+void smxo_set_threads(int n) { g_threads = n > 0 ? n : 0; }
+
+int smxo_get_threads(void)
 {
-    for (int t = 0; t < T; t++) {
-        const float *xt = x + (size_t)t * K;
-        float *yt = y + (size_t)t * N;
-        int n = 0;
-        for (; n + 8 <= N; n += 8) {
-            float acc[8] = {0};
-            const float *w[8];
-            for (int r = 0; r < 8; r++) w[r] = W + (size_t)(n + r) * K;
-            for (int k = 0; k < K; k++) {
-                float xv = xt[k];
-                for (int r = 0; r < 8; r++) acc[r] = fmaf(xv, w[r][k], acc[r]);
+#ifdef _OPENMP
+    return g_threads > 0 ? g_threads : omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/* [N][K] row-major -> [ceil(N/8)][K][8]; frees W. */
+static float *interleave8(float *W, int N, int K)
+{
+    if (!W) return NULL;
+    const int nb = (N + 7) / 8;
+    float *Wi = (float *)aligned_alloc(32, sizeof(float) * (size_t)nb * K * 8);
+#pragma omp parallel for schedule(static) num_threads(smxo_get_threads())
+    for (int b = 0; b < nb; b++)
+        for (int k = 0; k < K; k++)
+            for (int r = 0; r < 8; r++) {
+                const int n = b * 8 + r;
+                Wi[((size_t)b * K + k) * 8 + r] = n < N ? W[(size_t)n * K + k] : 0.0f;
             }
-            for (int r = 0; r < 8; r++) yt[n + r] = acc[r];
+    free(W);
+    return Wi;
+}
+
+static void linear(const float *x, int T, int K, const float *Wi, const float *bias, int N, float *y)
+{
+    const int nb = (N + 7) / 8;
+    const int nth = smxo_get_threads();
+    if (T == 1) {
+        /* four row blocks per pass: four independent chains per lane */
+        const int ng = (nb + 3) / 4;
+#pragma omp parallel for schedule(static) num_threads(nth)
+        for (int g = 0; g < ng; g++) {
+            const int b0 = g * 4, nbg = nb - b0 < 4 ? nb - b0 : 4;
+            __m256 acc[4];
+            const float *w[4];
+            for (int j = 0; j < 4; j++) {
+                acc[j] = _mm256_setzero_ps();
+                w[j] = Wi + (size_t)(b0 + (j < nbg ? j : 0)) * K * 8;
+            }
+            for (int k = 0; k < K; k++) {
+                const __m256 xv = _mm256_broadcast_ss(x + k);
+                for (int j = 0; j < 4; j++) acc[j] = _mm256_fmadd_ps(xv, _mm256_load_ps(w[j] + (size_t)k * 8), acc[j]);
+            }
+            for (int j = 0; j < nbg; j++) {
+                float out[8];
+                _mm256_storeu_ps(out, acc[j]);
+                for (int r = 0; r < 8 && (b0 + j) * 8 + r < N; r++) y[(b0 + j) * 8 + r] = out[r];
+            }
         }
-        for (; n < N; n++) {
-            const float *w = W + (size_t)n * K;
-            float acc = 0.0f;
-            for (int k = 0; k < K; k++) acc = fmaf(xt[k], w[k], acc);
-            yt[n] = acc;
+    } else {
+        /* tokens transposed into tiles of 8: xt[tile][k][8], zero-padded */
+        const int nt = (T + 7) / 8;
+        float *xt = (float *)aligned_alloc(32, sizeof(float) * (size_t)nt * K * 8);
+        for (int tt = 0; tt < nt; tt++)
+            for (int k = 0; k < K; k++)
+                for (int l = 0; l < 8; l++) {
+                    int t = tt * 8 + l;
+                    xt[((size_t)tt * K + k) * 8 + l] = t < T ? x[(size_t)t * K + k] : 0.0f;
+                }
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nth)
+        for (int b = 0; b < nb; b++) {
+            const int n0 = b * 8, rows = N - n0 < 8 ? N - n0 : 8;
+            const float *w = Wi + (size_t)b * K * 8;
+            for (int tt = 0; tt < nt; tt++) {
+                const float *xp = xt + (size_t)tt * K * 8;
+                __m256 acc[8];
+                for (int r = 0; r < 8; r++) acc[r] = _mm256_setzero_ps();
+                for (int k = 0; k < K; k++) {
+                    const __m256 xv = _mm256_load_ps(xp + (size_t)k * 8);
+                    for (int r = 0; r < 8; r++)
+                        acc[r] = _mm256_fmadd_ps(_mm256_broadcast_ss(w + (size_t)k * 8 + r), xv, acc[r]);
+                }
+                float out[8][8];
+                for (int r = 0; r < 8; r++) _mm256_storeu_ps(out[r], acc[r]);
+                for (int l = 0; l < 8 && tt * 8 + l < T; l++)
+                    for (int r = 0; r < rows; r++) y[(size_t)(tt * 8 + l) * N + n0 + r] = out[r][l];
+            }
         }
-        if (bias) for (int i = 0; i < N; i++) yt[i] = yt[i] + bias[i];
+        free(xt);
     }
+    if (bias)
+        for (int t = 0; t < T; t++) {
+            float *yt = y + (size_t)t * N;
+            for (int i = 0; i < N; i++) yt[i] = yt[i] + bias[i];
+        }
 }
 
 static void norm_rows(const smxo_model *m, const float *x, const float *g, const float *b,
@@ -1047,7 +1149,6 @@ int smxo_forward_nocache(smxo_model *m, const int32_t *tokens, int T, float *log
     float *q = (float *)malloc(sizeof(float) * (size_t)H * T * hd);
     float *k = (float *)malloc(sizeof(float) * (size_t)Hkv * T * hd);
     float *v = (float *)malloc(sizeof(float) * (size_t)Hkv * T * hd);
-    float *att = (float *)malloc(sizeof(float) * (size_t)T * T);
     float *y = (float *)malloc(sizeof(float) * (size_t)T * d);
     float *o = (float *)malloc(sizeof(float) * (size_t)T * d);
     float *t1 = (float *)malloc(sizeof(float) * (size_t)T * hid);
@@ -1071,7 +1172,9 @@ int smxo_forward_nocache(smxo_model *m, const int32_t *tokens, int T, float *log
             smxo_rope_apply(q, 0, H, T, hd, m->cos_t, m->sin_t);
             smxo_rope_apply(k, 0, Hkv, T, hd, m->cos_t, m->sin_t);
         }
+#pragma omp parallel for schedule(dynamic, 1) num_threads(smxo_get_threads())
         for (int hh = 0; hh < H; hh++) {
+            float *att = (float *)malloc(sizeof(float) * (size_t)T * T);
             int kvh = hh / group;
             const float *qh = q + (size_t)hh * T * hd;
             const float *kh = k + (size_t)kvh * T * hd;
@@ -1093,6 +1196,7 @@ int smxo_forward_nocache(smxo_model *m, const int32_t *tokens, int T, float *log
                 /* ReshapeAttentionOutputInPlace (MultiHeadAttention.cs:643-667) */
                 memcpy(y + (size_t)i * d + hh * hd, acc, sizeof(float) * hd);
             }
+            free(att);
         }
         linear(y, T, d, l->wo, l->bo, d, o);
         for (size_t i = 0; i < (size_t)T * d; i++) x[i] = x[i] + o[i];   /* TransformerBlock.cs:170 */
@@ -1103,7 +1207,7 @@ int smxo_forward_nocache(smxo_model *m, const int32_t *tokens, int T, float *log
     int r0 = all_rows ? 0 : T - 1;
     norm_rows(m, x + (size_t)r0 * d, m->out_g, m->out_b, h, T - r0);
     linear(h, T - r0, d, m->head, NULL, m->vocab, logits);
-    free(x); free(h); free(qkv); free(q); free(k); free(v); free(att); free(y); free(o);
+    free(x); free(h); free(qkv); free(q); free(k); free(v); free(y); free(o);
     free(t1); free(t2);
     return 0;
 }
@@ -1115,10 +1219,6 @@ smxo_session *smxo_session_create(smxo_model *m, int max_ctx)
     size_t cache = (size_t)m->L * m->Hkv * max_ctx * m->hd;
     s->m = m; s->max_ctx = max_ctx;
     s->kc = (float *)calloc(cache, 4); s->vc = (float *)calloc(cache, 4);
-    s->x = (float *)malloc(4 * (size_t)m->d); s->h = (float *)malloc(4 * (size_t)m->d);
-    s->qkv = (float *)malloc(4 * (size_t)m->nqkv); s->y = (float *)malloc(4 * (size_t)m->d);
-    s->t1 = (float *)malloc(4 * (size_t)m->hidden); s->t2 = (float *)malloc(4 * (size_t)m->hidden);
-    s->t3 = (float *)malloc(4 * (size_t)m->d); s->scores = (float *)malloc(4 * (size_t)max_ctx);
     if (!s->kc || !s->vc) { smxo_session_destroy(s); return NULL; }
     return s;
 }
@@ -1126,62 +1226,125 @@ smxo_session *smxo_session_create(smxo_model *m, int max_ctx)
 void smxo_session_destroy(smxo_session *s)
 {
     if (!s) return;
-    free(s->kc); free(s->vc); free(s->x); free(s->h); free(s->qkv); free(s->y);
-    free(s->t1); free(s->t2); free(s->t3); free(s->scores); free(s);
+    free(s->kc); free(s->vc); free(s);
 }
 
-/* One token through the model with a KV cache that is written and read with the same
- * stride (the intent stated in GoldenValues.cs:71-83). */
-int smxo_session_step(smxo_session *s, int32_t token, int pos, float *logits)
+/* Tokens tok[i] of sessions ss[i] at positions pos[i], i < T, through the model with each
+ * session's KV cache (written and read with the same stride: the intent stated in
+ * GoldenValues.cs:71-83).  A session may appear several times at consecutive positions (a
+ * prefill run) or once per token (several sessions stepping together).  Per layer every token's
+ * K/V is written before any attention reads the cache, and token i attends to positions
+ * 0..pos[i] of its own session, so the outputs are bit-identical to T single-token steps in
+ * order.  logits: rows lg_from..T-1 ([T - lg_from][V]), or NULL. */
+static int step_batch(smxo_model *m, smxo_session *const *ss, const int32_t *tok, const int *pos, int T,
+                      float *logits, int lg_from)
 {
-    smxo_model *m = s->m;
-    if (pos < 0 || pos >= s->max_ctx || token < 0 || token >= m->vocab) return -1;
-    int d = m->d, H = m->H, Hkv = m->Hkv, hd = m->hd, kv = m->kvdim, N = m->nqkv;
+    int d = m->d, H = m->H, Hkv = m->Hkv, hd = m->hd, kv = m->kvdim, N = m->nqkv, hid = m->hidden;
     float scale = 1.0f / sqrtf((float)hd);
-    int group = H / Hkv, L = pos + 1;
-    embed(m, token, pos, s->x);
+    int group = H / Hkv, maxL = 1;
+    for (int i = 0; i < T; i++) {
+        if (pos[i] < 0 || pos[i] >= ss[i]->max_ctx || tok[i] < 0 || tok[i] >= m->vocab) return -1;
+        if (pos[i] + 1 > maxL) maxL = pos[i] + 1;
+    }
+    const int nth = smxo_get_threads();
+    float *x = (float *)malloc(sizeof(float) * (size_t)T * d);
+    float *h = (float *)malloc(sizeof(float) * (size_t)T * d);
+    float *qkv = (float *)malloc(sizeof(float) * (size_t)T * N);
+    float *y = (float *)malloc(sizeof(float) * (size_t)T * d);
+    float *t1 = (float *)malloc(sizeof(float) * (size_t)T * hid);
+    float *t2 = (float *)malloc(sizeof(float) * (size_t)T * hid);
+    float *t3 = (float *)malloc(sizeof(float) * (size_t)T * d);
+    float *sc = (float *)malloc(sizeof(float) * (size_t)nth * maxL);
+    for (int i = 0; i < T; i++) embed(m, tok[i], pos[i], x + (size_t)i * d);
     for (int li = 0; li < m->L; li++) {
         const olayer *l = &m->layers[li];
-        norm_rows(m, s->x, l->attn_g, l->attn_b, s->h, 1);
-        linear(s->h, 1, d, l->wqkv, l->bqkv, N, s->qkv);
-        float *q = s->qkv, *k = s->qkv + d, *v = s->qkv + d + kv;
-        if (m->arch == SMXO_ARCH_LLAMA) {
-            smxo_rope_apply(q, pos, H, 1, hd, m->cos_t, m->sin_t);
-            smxo_rope_apply(k, pos, Hkv, 1, hd, m->cos_t, m->sin_t);
+        norm_rows(m, x, l->attn_g, l->attn_b, h, T);
+        linear(h, T, d, l->wqkv, l->bqkv, N, qkv);
+        for (int i = 0; i < T; i++) {
+            float *q = qkv + (size_t)i * N, *k = q + d, *v = q + d + kv;
+            if (m->arch == SMXO_ARCH_LLAMA) {
+                smxo_rope_apply(q, pos[i], H, 1, hd, m->cos_t, m->sin_t);
+                smxo_rope_apply(k, pos[i], Hkv, 1, hd, m->cos_t, m->sin_t);
+            }
+            const smxo_session *s = ss[i];
+            for (int hh = 0; hh < Hkv; hh++) {
+                size_t base = (((size_t)li * Hkv + hh) * s->max_ctx + pos[i]) * hd;
+                memcpy(s->kc + base, k + hh * hd, 4 * (size_t)hd);
+                memcpy(s->vc + base, v + hh * hd, 4 * (size_t)hd);
+            }
         }
-        for (int hh = 0; hh < Hkv; hh++) {
-            size_t base = (((size_t)li * Hkv + hh) * s->max_ctx + pos) * hd;
-            memcpy(s->kc + base, k + hh * hd, 4 * (size_t)hd);
-            memcpy(s->vc + base, v + hh * hd, 4 * (size_t)hd);
-        }
-        for (int hh = 0; hh < H; hh++) {
-            int kvh = hh / group;
+        /* MultiHeadAttention.cs:676-844 per (token, head) */
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nth)
+        for (int ih = 0; ih < T * H; ih++) {
+            int i = ih / H, hh = ih % H;
+#ifdef _OPENMP
+            float *scores = sc + (size_t)omp_get_thread_num() * maxL;
+#else
+            float *scores = sc;
+#endif
+            const smxo_session *s = ss[i];
+            int kvh = hh / group, L = pos[i] + 1;
             const float *kh = s->kc + ((size_t)li * Hkv + kvh) * s->max_ctx * hd;
             const float *vh = s->vc + ((size_t)li * Hkv + kvh) * s->max_ctx * hd;
-            const float *qh = q + hh * hd;
+            const float *qh = qkv + (size_t)i * N + hh * hd;
             for (int j = 0; j < L; j++) {
                 float acc = 0.0f;
                 for (int e = 0; e < hd; e++) acc = fmaf(qh[e], kh[(size_t)j * hd + e], acc);
-                s->scores[j] = acc;
+                scores[j] = acc;
             }
-            smxo_scale_mask_softmax(s->scores, scale, 1, L, pos);
+            smxo_scale_mask_softmax(scores, scale, 1, L, pos[i]);
             float acc[512];
             for (int e = 0; e < hd; e++) acc[e] = 0.0f;
             for (int j = 0; j < L; j++)
-                for (int e = 0; e < hd; e++) acc[e] = fmaf(s->scores[j], vh[(size_t)j * hd + e], acc[e]);
-            memcpy(s->y + hh * hd, acc, 4 * (size_t)hd);
+                for (int e = 0; e < hd; e++) acc[e] = fmaf(scores[j], vh[(size_t)j * hd + e], acc[e]);
+            memcpy(y + (size_t)i * d + hh * hd, acc, 4 * (size_t)hd);
         }
-        linear(s->y, 1, d, l->wo, l->bo, d, s->t3);
-        for (int i = 0; i < d; i++) s->x[i] = s->x[i] + s->t3[i];
-        norm_rows(m, s->x, l->ffn_g, l->ffn_b, s->h, 1);
-        mlp(m, l, s->h, 1, s->t1, s->t2, s->t3);
-        for (int i = 0; i < d; i++) s->x[i] = s->x[i] + s->t3[i];
+        linear(y, T, d, l->wo, l->bo, d, t3);
+        for (size_t i = 0; i < (size_t)T * d; i++) x[i] = x[i] + t3[i];   /* TransformerBlock.cs:170 */
+        norm_rows(m, x, l->ffn_g, l->ffn_b, h, T);
+        mlp(m, l, h, T, t1, t2, t3);
+        for (size_t i = 0; i < (size_t)T * d; i++) x[i] = x[i] + t3[i];   /* TransformerBlock.cs:184 */
     }
-    if (logits) {
-        norm_rows(m, s->x, m->out_g, m->out_b, s->h, 1);
-        linear(s->h, 1, d, m->head, NULL, m->vocab, logits);
+    if (logits && lg_from < T) {
+        norm_rows(m, x + (size_t)lg_from * d, m->out_g, m->out_b, h, T - lg_from);
+        linear(h, T - lg_from, d, m->head, NULL, m->vocab, logits);
     }
+    free(x); free(h); free(qkv); free(y); free(t1); free(t2); free(t3); free(sc);
     return 0;
+}
+
+int smxo_session_step(smxo_session *s, int32_t token, int pos, float *logits)
+{
+    return step_batch(s->m, &s, &token, &pos, 1, logits, 0);
+}
+
+int smxo_session_prefill(smxo_session *s, const int32_t *tokens, int T, int pos0, float *logits_last)
+{
+    if (T <= 0 || pos0 < 0 || pos0 + T > s->max_ctx) return -1;
+    smxo_session **ss = (smxo_session **)malloc(sizeof(*ss) * (size_t)T);
+    int *pos = (int *)malloc(sizeof(int) * (size_t)T);
+    for (int i = 0; i < T; i++) { ss[i] = s; pos[i] = pos0 + i; }
+    int rc = step_batch(s->m, ss, tokens, pos, T, logits_last, T - 1);
+    free(ss); free(pos);
+    return rc;
+}
+
+int smxo_step_tokens(smxo_session *const *ss, const int32_t *tokens, const int *pos, int n, float *logits,
+                     int lg_from)
+{
+    if (n <= 0 || lg_from < 0) return -1;
+    for (int i = 0; i < n; i++) if (ss[i]->m != ss[0]->m) return -1;
+    return step_batch(ss[0]->m, ss, tokens, pos, n, logits, lg_from);
+}
+
+int smxo_multi_step(smxo_session *const *ss, const int32_t *tokens, const int *pos, int n, float *logits)
+{
+    if (n <= 0) return -1;
+    for (int i = 0; i < n; i++) {
+        if (ss[i]->m != ss[0]->m) return -1;
+        for (int j = 0; j < i; j++) if (ss[j] == ss[i]) return -1;
+    }
+    return step_batch(ss[0]->m, ss, tokens, pos, n, logits, 0);
 }
 
 static int64_t now_ns(void)
@@ -1199,7 +1362,7 @@ int smxo_generate_greedy(smxo_model *m, const int32_t *prompt, int n_prompt, int
     if (!s) return -2;
     float *logits = (float *)malloc(sizeof(float) * (size_t)m->vocab);
     int64_t t0 = now_ns();
-    for (int p = 0; p < n_prompt - 1; p++) smxo_session_step(s, prompt[p], p, NULL);
+    if (n_prompt > 1) smxo_session_prefill(s, prompt, n_prompt - 1, 0, NULL);
     int64_t t1 = now_ns();
     int32_t tok = prompt[n_prompt - 1];
     for (int i = 0; i < n_new; i++) {

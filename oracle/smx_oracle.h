@@ -84,7 +84,22 @@ int smxo_forward_nocache(smxo_model *m, const int32_t *tokens, int T, float *log
 /* KV-cached single-token step at position pos (cache written correctly). */
 smxo_session *smxo_session_create(smxo_model *m, int max_ctx);
 int  smxo_session_step(smxo_session *s, int32_t token, int pos, float *logits);
+/* T tokens at positions pos0..pos0+T-1 in one pass (batched linears); bit-identical to T
+ * smxo_session_step calls in order.  logits_last (may be NULL): the last token's logits. */
+int  smxo_session_prefill(smxo_session *s, const int32_t *tokens, int T, int pos0, float *logits_last);
+/* One token for each of n distinct sessions of one model (token i at pos[i] of ss[i]) in one
+ * pass; logits [n][V] (may be NULL).  Bit-identical to n smxo_session_step calls. */
+int  smxo_multi_step(smxo_session *const *ss, const int32_t *tokens, const int *pos, int n, float *logits);
+/* Tokens of any sessions of one model in one pass: token i at pos[i] of ss[i] attends to
+ * positions 0..pos[i] of its session, each of which this call or an earlier one writes (several
+ * prompts prefilled together).  logits: rows lg_from..n-1 ([n - lg_from][V]) or NULL. */
+int  smxo_step_tokens(smxo_session *const *ss, const int32_t *tokens, const int *pos, int n, float *logits,
+                      int lg_from);
 void smxo_session_destroy(smxo_session *s);
+
+/* Threads used by the linears and attention (0 = all; results do not depend on it). */
+void smxo_set_threads(int n);
+int  smxo_get_threads(void);
 
 /* Greedy decode with the cached step: prefill n_prompt tokens, then generate n_new tokens
  * (argmax, lowest index on ties).  Writes out_tokens[n_new]; returns elapsed ns of the

@@ -49,7 +49,7 @@ class ModelConfigC(ctypes.Structure):
 
 
 class SamplingC(ctypes.Structure):
-    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int32), ("top_p", ctypes.c_float),
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int32), ("top_p", ctypes.c_double),
                 ("min_p", ctypes.c_float), ("repetition_penalty", ctypes.c_float),
                 ("presence_penalty", ctypes.c_float), ("frequency_penalty", ctypes.c_float),
                 ("repetition_window", ctypes.c_int32)]

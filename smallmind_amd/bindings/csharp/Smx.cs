@@ -2,7 +2,7 @@
 // Not compiled in this repository (no .NET toolchain); tests/test_bindings.py checks every
 // declaration below against include/smx.h (names, parameter counts and type mapping).
 // The backend classes follow the reference's interfaces: IWeightTensor
-// (src/SmallMind.Quantization/Tensors/IWeightTensor.cs:7-42), TransformerModel.Forward with the
+// (src/SmallMind.Quantization/Abstractions/IWeightTensor.cs:7-42), TransformerModel.Forward with the
 // KV cache (TransformerModel.cs:272-344, ResetKVCache :476-506), InferenceSession's sampling
 // options (ProductionInferenceOptions.cs:19-87).
 using System;
@@ -32,7 +32,7 @@ namespace SmallMind.Backends.Rocm
         [StructLayout(LayoutKind.Sequential)]
         public struct Sampling               // smx_sampling; ProductionInferenceOptions.cs:19-87
         {
-            public float Temperature; public int TopK; public float TopP, MinP,
+            public float Temperature; public int TopK; public double TopP; public float MinP,
                 RepetitionPenalty, PresencePenalty, FrequencyPenalty; public int RepetitionWindow;
         }
 

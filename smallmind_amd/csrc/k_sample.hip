@@ -133,7 +133,7 @@ __device__ int sample_pipeline(const float *__restrict__ logits, int n, const in
         for (int i = tid; i < n; i += kT) probs[i] = probs[i] / sum;
     __syncthreads();
     // 5. top-p: threshold t = the largest probability with sum(p >= t) >= top_p
-    if (sp.top_p < 1.0f) {
+    if (sp.top_p < 1.0) {
         uint32_t key = 0;   // probabilities are >= 0: their bit patterns order like the values
         for (int b = 30; b >= 0; b--) {
             const uint32_t cand = key | (1u << b);
@@ -141,7 +141,7 @@ __device__ int sample_pipeline(const float *__restrict__ logits, int n, const in
             float c = 0.0f;
             for (int i = tid; i < n; i += kT) c += probs[i] >= t ? probs[i] : 0.0f;
             const float f = block_sum_t<float>(c, redf);
-            if (f >= sp.top_p && f > 0.0f) key = cand;
+            if ((double)f >= sp.top_p && f > 0.0f) key = cand;   // float sum against the double TopP
         }
         const float t = __uint_as_float(key);
         s = 0.0f;

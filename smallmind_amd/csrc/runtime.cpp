@@ -16,6 +16,7 @@
 
 #include <atomic>
 #include <map>
+#include <mutex>
 #include <memory>
 #include <string>
 #include <vector>
@@ -148,9 +149,12 @@ int mat_upload(Mat &m, const void *bytes, int64_t rows, int64_t cols, int on_dev
 
 }  // namespace
 
+// The context stream carries model uploads only (serialised by mu); every session and batcher
+// runs on a stream of its own, so a graph capture on one never records another thread's work.
 struct smx_context {
     int device = 0;
     hipStream_t stream = nullptr;
+    std::mutex mu;
 };
 
 struct smx_weight {
@@ -197,6 +201,7 @@ struct TokBatch {
 
 struct smx_session {
     smx_model *m = nullptr;
+    hipStream_t stream = nullptr;   // this session's work, its graph captures and replays
     int max_ctx = 0;
     // KV cache row length: max_ctx rounded up to 4 positions, so K rows are 16-byte aligned
     // (the one-launch decode attention reads them as float4)
@@ -385,7 +390,7 @@ constexpr int kDecodeBlock = 8;
 int capture_step(smx_session *S, bool with_head, bool with_embed, hipGraphExec_t *out, int steps = 1,
                  bool sample = false)
 {
-    hipStream_t s = S->m->ctx->stream;
+    hipStream_t s = S->stream;
     hipGraph_t graph = nullptr;
     SMX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     int rc = SMX_OK;
@@ -493,7 +498,7 @@ int setup_persistent(smx_session *S)
 // s >= head_from compute logits and the greedy token.
 int run_persistent(smx_session *S, int pos0, int n_steps, int head_from, float *logits_all)
 {
-    hipStream_t s = S->m->ctx->stream;
+    hipStream_t s = S->stream;
     SMX_HIP(hipMemsetAsync(S->bar, 0, 4, s));
     SMX_HIP(hipMemsetAsync(S->abort_flag, 0, 4, s));
     DecodeArgs a = S->dargs;
@@ -1091,6 +1096,7 @@ SMX_API int smx_model_upload_tensor(smx_model *m, const char *name, int type, co
 {
     if (!m || !name || !dims || !bytes) SMX_FAIL(SMX_EINVAL, "smx_model_upload_tensor: null argument");
     if (m->finalized) SMX_FAIL(SMX_ESTATE, "smx_model_upload_tensor: model already finalized");
+    std::lock_guard<std::mutex> lock(m->ctx->mu);
     SMX_HIP(hipSetDevice(m->ctx->device));
     const smx_model_config &c = m->cfg;
     const int64_t d = c.d_model, kv = m->kvdim, hid = m->hidden;
@@ -1173,6 +1179,7 @@ SMX_API int smx_model_upload_tensor(smx_model *m, const char *name, int type, co
 SMX_API int smx_model_finalize(smx_model *m)
 {
     if (!m) SMX_FAIL(SMX_EINVAL, "smx_model_finalize: null model");
+    std::lock_guard<std::mutex> lock(m->ctx->mu);
     if (m->finalized) return SMX_OK;
     SMX_HIP(hipSetDevice(m->ctx->device));
     const smx_model_config &c = m->cfg;
@@ -1277,9 +1284,10 @@ SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out)
     A((void **)&S->head_val, (size_t)(c.vocab / 2 + 1) * 4);
     A((void **)&S->head_idx, (size_t)(c.vocab / 2 + 1) * 4);
     for (int i = 0; i < 3 && e == hipSuccess; i++) e = hipEventCreate(&S->ev[i]);
-    if (e == hipSuccess) e = hipMemsetAsync(S->tokens, 0, (size_t)(max_ctx + 1) * 4, m->ctx->stream);
-    if (e == hipSuccess) e = hipMemsetAsync(S->pos, 0, 4, m->ctx->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(m->ctx->stream);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&S->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipMemsetAsync(S->tokens, 0, (size_t)(max_ctx + 1) * 4, S->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(S->pos, 0, 4, S->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(S->stream);
     if (e != hipSuccess) {
         smx_session_destroy(S);
         SMX_HIP(e);
@@ -1319,7 +1327,7 @@ SMX_API int smx_session_forward(smx_session *S, const int32_t *tokens, int n_tok
     int rc = check_tokens(S, tokens, n_tokens);
     if (rc != SMX_OK) return rc;
     SMX_HIP(hipSetDevice(S->m->ctx->device));
-    hipStream_t s = S->m->ctx->stream;
+    hipStream_t s = S->stream;
     const int32_t p0 = pos_offset;
     SMX_HIP(hipMemcpyAsync(S->tokens + pos_offset, tokens, (size_t)n_tokens * 4, hipMemcpyHostToDevice, s));
     SMX_HIP(hipMemcpyAsync(S->pos, &p0, 4, hipMemcpyHostToDevice, s));
@@ -1350,7 +1358,7 @@ SMX_API int smx_session_generate(smx_session *S, const int32_t *prompt, int n_pr
     int rc = check_tokens(S, prompt, n_prompt);
     if (rc != SMX_OK) return rc;
     SMX_HIP(hipSetDevice(S->m->ctx->device));
-    hipStream_t s = S->m->ctx->stream;
+    hipStream_t s = S->stream;
     const int V = S->m->cfg.vocab;
     const int32_t zero = 0;
     SMX_HIP(hipMemcpyAsync(S->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s));
@@ -1424,11 +1432,23 @@ SMX_API int smx_session_generate_sampled(smx_session *S, const int32_t *prompt, 
     int rc = check_tokens(S, prompt, n_prompt);
     if (rc != SMX_OK) return rc;
     SMX_HIP(hipSetDevice(S->m->ctx->device));
-    hipStream_t s = S->m->ctx->stream;
+    hipStream_t s = S->stream;
     const int V = S->m->cfg.vocab;
-    if (!S->samp) {
-        SMX_HIP(hipMalloc((void **)&S->samp, sizeof(SampleState)));
-        SMX_HIP(hipMalloc((void **)&S->probs, (size_t)V * 4));
+    if (!S->samp || !S->probs) {   // both or neither: the sampling graph reads both
+        free_dev(S->samp);
+        free_dev(S->probs);
+        S->samp = nullptr;
+        S->probs = nullptr;
+        SampleState *samp = nullptr;
+        float *probs = nullptr;
+        hipError_t e = hipMalloc((void **)&samp, sizeof(SampleState));
+        if (e == hipSuccess) e = hipMalloc((void **)&probs, (size_t)V * 4);
+        if (e != hipSuccess) {
+            free_dev(samp);
+            SMX_HIP(e);
+        }
+        S->samp = samp;
+        S->probs = probs;
     }
     if (!S->g_sample && (rc = capture_step(S, true, true, &S->g_sample, 1, true)) != SMX_OK) return rc;
     const SampleState st{*params, seed, 0};
@@ -1501,7 +1521,8 @@ SMX_API int smx_batch_generate(smx_session *const *sessions, int n_sessions, con
         if (rc != SMX_OK) return rc;
     }
     SMX_HIP(hipSetDevice(m->ctx->device));
-    hipStream_t s = m->ctx->stream;
+    // every listed session is held by this call: the first one's stream carries the batch
+    hipStream_t s = sessions[0]->stream;
     const int V = m->cfg.vocab, n = n_sessions;
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     TokBatch D;
@@ -1596,6 +1617,7 @@ SMX_API int smx_batch_generate(smx_session *const *sessions, int n_sessions, con
 // count, made on first use.
 struct smx_batcher {
     smx_model *m = nullptr;
+    hipStream_t stream = nullptr;   // member prefills, step captures and replays
     int cap = 0, max_ctx = 0;
     TokBatch D;
     std::vector<smx_session *> slot;
@@ -1623,12 +1645,14 @@ SMX_API int smx_batcher_create(smx_model *m, int max_members, int max_ctx, smx_b
     B->max_ctx = max_ctx;
     int rc = batch_alloc(m, B->D, max_members, max_members);
     hipError_t e = hipSuccess;
-    if (rc == SMX_OK) e = hipMalloc((void **)&B->d_samp, (size_t)max_members * sizeof(SampleState));
+    if (rc == SMX_OK) e = hipStreamCreateWithFlags(&B->stream, hipStreamNonBlocking);
+    if (rc == SMX_OK && e == hipSuccess) e = hipMalloc((void **)&B->d_samp, (size_t)max_members * sizeof(SampleState));
     if (rc == SMX_OK && e == hipSuccess) e = hipMalloc((void **)&B->d_on, (size_t)max_members * 4);
     if (rc == SMX_OK && e == hipSuccess) e = hipMalloc((void **)&B->d_probs, (size_t)max_members * m->cfg.vocab * 4);
     if (rc != SMX_OK || e != hipSuccess) {
         batch_free(B->D);
         free_dev(B->d_samp); free_dev(B->d_on); free_dev(B->d_probs);
+        if (B->stream) (void)hipStreamDestroy(B->stream);
         delete B;
         if (rc != SMX_OK) return rc;
         SMX_FAIL(SMX_ENOMEM, "smx_batcher_create: %s", hipGetErrorString(e));
@@ -1657,7 +1681,7 @@ static int batcher_add(smx_batcher *B, smx_session *S, const int32_t *prompt, in
     if (!S->busy.compare_exchange_strong(expected, 1))
         SMX_FAIL(SMX_EBUSY, "smx_batcher_add: session in use (on another thread or in a batcher)");
     auto release = [&]() { S->busy.store(0); };
-    hipStream_t s = B->m->ctx->stream;
+    hipStream_t s = B->stream;
     hipError_t e = hipSetDevice(B->m->ctx->device);
     if (e == hipSuccess) e = hipMemcpyAsync(S->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) {
@@ -1699,7 +1723,7 @@ SMX_API int smx_batcher_remove(smx_batcher *B, smx_session *S)
     while (i < B->slot.size() && B->slot[i] != S) i++;
     if (i == B->slot.size()) SMX_FAIL(SMX_EINVAL, "smx_batcher_remove: session is not a member");
     SMX_HIP(hipSetDevice(B->m->ctx->device));
-    hipStream_t s = B->m->ctx->stream;
+    hipStream_t s = B->stream;
     const int32_t p = B->pos[i];
     SMX_HIP(hipMemcpyAsync(S->pos, &p, 4, hipMemcpyHostToDevice, s));
     SMX_HIP(hipStreamSynchronize(s));
@@ -1732,7 +1756,7 @@ SMX_API int smx_batcher_step(smx_batcher *B, int n_steps, int32_t *out_tokens)
                      B->pos[(size_t)i], n_steps, B->max_ctx);
     smx_model *m = B->m;
     SMX_HIP(hipSetDevice(m->ctx->device));
-    hipStream_t s = m->ctx->stream;
+    hipStream_t s = B->stream;
     TokBatch &D = B->D;
     if (B->dirty) {
         std::vector<float *> kc((size_t)n), vc((size_t)n);
@@ -1800,7 +1824,7 @@ SMX_API int smx_batcher_destroy(smx_batcher *B)
 {
     if (!B) return SMX_OK;
     (void)hipSetDevice(B->m->ctx->device);
-    (void)hipStreamSynchronize(B->m->ctx->stream);
+    (void)hipStreamSynchronize(B->stream);
     for (auto &g : B->graphs) if (g.second) (void)hipGraphExecDestroy(g.second);
     for (size_t i = 0; i < B->slot.size(); i++) {
         const int32_t p = B->pos[i];
@@ -1809,6 +1833,7 @@ SMX_API int smx_batcher_destroy(smx_batcher *B)
     }
     batch_free(B->D);
     free_dev(B->d_samp); free_dev(B->d_on); free_dev(B->d_probs);
+    if (B->stream) (void)hipStreamDestroy(B->stream);
     B->m->sessions.fetch_sub(1);
     delete B;
     return SMX_OK;
@@ -1821,8 +1846,8 @@ SMX_API int smx_session_reset(smx_session *S)
     if (!guard.ok) SMX_FAIL(SMX_EBUSY, "smx_session_reset: session in use on another thread");
     SMX_HIP(hipSetDevice(S->m->ctx->device));
     const int32_t zero = 0;
-    SMX_HIP(hipMemcpyAsync(S->pos, &zero, 4, hipMemcpyHostToDevice, S->m->ctx->stream));
-    SMX_HIP(hipStreamSynchronize(S->m->ctx->stream));
+    SMX_HIP(hipMemcpyAsync(S->pos, &zero, 4, hipMemcpyHostToDevice, S->stream));
+    SMX_HIP(hipStreamSynchronize(S->stream));
     return SMX_OK;
 }
 
@@ -1838,6 +1863,10 @@ SMX_API int smx_session_destroy(smx_session *S)
     if (S->g_decode_block) (void)hipGraphExecDestroy(S->g_decode_block);
     if (S->g_sample) (void)hipGraphExecDestroy(S->g_sample);
     for (hipEvent_t e : S->ev) if (e) (void)hipEventDestroy(e);
+    if (S->stream) {
+        (void)hipStreamSynchronize(S->stream);
+        (void)hipStreamDestroy(S->stream);
+    }
     free_dev(S->kc); free_dev(S->vc); free_dev(S->x); free_dev(S->q); free_dev(S->att); free_dev(S->scores);
     free_dev(S->h); free_dev(S->logits); free_dev(S->tokens); free_dev(S->pos); free_dev(S->amax);
     free_dev(S->head_val); free_dev(S->head_idx);

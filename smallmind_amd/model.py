@@ -154,10 +154,10 @@ class GpuTransformerModel:
         return s
 
     def close(self):
-        for b in getattr(self, "_batchers", []):
+        for b in list(getattr(self, "_batchers", [])):
             b.close()
         self._batchers = []
-        for s in self._sessions:
+        for s in list(self._sessions):
             s.close()
         self._sessions = []
         if getattr(self, "_h", None) and self._h.value:
@@ -252,6 +252,9 @@ class GpuInferenceSession:
         if getattr(self, "_h", None) and self._h.value:
             call("smx_session_destroy", self._h)
             self._h = ctypes.c_void_p()
+        owned = getattr(self.model, "_sessions", None)
+        if owned is not None and self in owned:
+            owned.remove(self)
 
 
 class ContinuousBatcher:
@@ -308,6 +311,9 @@ class ContinuousBatcher:
             call("smx_batcher_destroy", self._h)
             self._h = ctypes.c_void_p()
             self.members = []
+        owned = getattr(self.model, "_batchers", None)
+        if owned is not None and self in owned:
+            owned.remove(self)
 
 
 def serve_continuous(model: "GpuTransformerModel", prompts, max_new_tokens, max_members: int, max_ctx: int,
@@ -319,10 +325,11 @@ def serve_continuous(model: "GpuTransformerModel", prompts, max_new_tokens, max_
     lim = [max_new_tokens] * len(prompts) if np.isscalar(max_new_tokens) else list(max_new_tokens)
     out = [[] for _ in prompts]
     b = ContinuousBatcher(model, max_members, max_ctx)
-    free = [model.create_session(max_ctx) for _ in range(min(max_members, len(prompts)))]
+    free = []
     active = {}    # session -> request index
     queue = list(range(len(prompts)))
     try:
+        free = [model.create_session(max_ctx) for _ in range(min(max_members, len(prompts)))]
         while queue or active:
             while queue and free:
                 r = queue.pop(0)
@@ -338,5 +345,9 @@ def serve_continuous(model: "GpuTransformerModel", prompts, max_new_tokens, max_
                     del active[s]
                     free.append(s)
     finally:
+        # the batcher releases its members first; then every session of this call is closed
+        # (each holds a KV cache of max_ctx positions)
         b.close()
+        for s in list(free) + list(active):
+            s.close()
     return [np.array(o, np.int32) for o in out]

@@ -77,3 +77,33 @@ def rel_err(a, b) -> float:
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def oracle_from_kept(cfg, kept):
+    """The oracle model of a GPU model built by load_synthetic_on_device(keep_blocks=True): the
+    same device-encoded bytes, copied to the host."""
+    arch = O.ARCH_GPT2 if cfg.architecture == "gpt2" else O.ARCH_LLAMA
+    om = O.OracleModel(arch, cfg.vocab_size, cfg.context_length, cfg.embedding_length,
+                       cfg.block_count, cfg.head_count, cfg.head_count_kv, cfg.feed_forward_length,
+                       cfg.rope_freq_base, cfg.norm_eps)
+    for name, (qt, dims, data) in kept.items():
+        om.set_tensor(name, qt, data.cpu().numpy(), int(np.prod(dims)))
+    om.finalize()
+    return om
+
+
+def check_greedy_against_oracle(osess, prompt, toks, logits, tol, prefilled=False):
+    """Walks the oracle session through the GPU run: every step's logits within tol
+    (max|d| / max|ref|) and every greedy token identical.  Returns the worst error."""
+    if not prefilled and len(prompt) > 1:
+        osess.prefill(prompt[:-1], 0)
+    tok, worst = int(prompt[-1]), 0.0
+    for i in range(len(toks)):
+        ref = osess.step(tok, len(prompt) - 1 + i)
+        err = rel_err(logits[i], ref)
+        worst = max(worst, err)
+        assert err <= tol, (i, err)
+        ref_tok = int(np.argmax(ref))
+        assert int(toks[i]) == ref_tok, (i, int(toks[i]), ref_tok)
+        tok = ref_tok
+    return worst

@@ -73,3 +73,58 @@ def test_status_codes_and_type_ids_match_the_header():
         assert re.search(rf"\b{name}\s*=\s*{val}\b", cs), name
     for name, val in re.findall(r"SMX_TYPE_(\w+)\s*=\s*(\d+)", h):
         assert re.search(rf"\b{name}\s*=\s*{val}\b", cs), name
+
+
+def _c_struct_fields(name):
+    """(type, field) pairs of `typedef struct name {...}` in include/smx.h, arrays expanded."""
+    h = open(os.path.join(ROOT, "include", "smx.h")).read()
+    body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), h, re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    out = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        m = re.match(r"(\w+)\s+(\w+)(?:\[(\d+)\])?$", decl)
+        assert m, decl
+        out += [(m.group(1), m.group(2))] * int(m.group(3) or 1)
+    return out
+
+
+def _cs_struct_types(name):
+    cs = open(os.path.join(ROOT, "smallmind_amd", "bindings", "csharp", "Smx.cs")).read()
+    one_line = re.search(r"public struct %s \{([^}\n]*)\}" % name, cs)
+    body = one_line.group(1) if one_line else re.search(r"public struct %s\b[^{]*\{(.*?)\n\s*\}" % name, cs,
+                                                         re.S).group(1)
+    body = re.sub(r"//[^\n]*", "", body)
+    types = []
+    for decl in body.split(";"):
+        m = re.match(r"\s*public\s+(?:fixed\s+)?(\w+)\s+(.*)", decl.strip(), re.S)
+        if not m:
+            continue
+        t, names = m.group(1), m.group(2)
+        for nm in names.split(","):
+            arr = re.search(r"\[(\d+)\]", nm)
+            types += [t] * (int(arr.group(1)) if arr else 1)
+    return types
+
+
+def test_struct_layouts_match_the_header():
+    """smx_sampling, smx_model_config and smx_gen_stats: the ctypes structures the Python host
+    passes and the C# structs declare the header's field types in the header's order."""
+    import ctypes
+
+    from smallmind_amd import _lib as L
+    c_to_ctypes = {"float": ctypes.c_float, "double": ctypes.c_double, "int32_t": ctypes.c_int32}
+    c_to_cs = {"float": "float", "double": "double", "int32_t": "int"}
+    for cname, py, csname in (("smx_sampling", L.SamplingC, "Sampling"), ("smx_model_config", L.ModelConfigC,
+                                                                          "ModelConfig"),
+                              ("smx_gen_stats", L.GenStatsC, "GenStats")):
+        fields = _c_struct_fields(cname)
+        flat = []
+        for fname, ftype in py._fields_:
+            n = getattr(ftype, "_length_", 1)
+            base = getattr(ftype, "_type_", ftype) if n > 1 else ftype
+            flat += [base] * n
+        assert [c_to_ctypes[t] for t, _ in fields] == flat, cname
+        assert [c_to_cs[t] for t, _ in fields] == _cs_struct_types(csname), cname

@@ -1,0 +1,162 @@
+"""Parity at the benchmark configurations' full sizes, on the workloads bench.py times.
+
+Each GPU model is built exactly as bench.py builds it (seeded weights drawn and encoded on the
+device, seed 42); the oracle model is built from the same device-encoded bytes copied to the
+host.  The oracle runs its linears over all host cores (bit-identical to one thread, see
+tests/test_oracle.py), with prompts prefilled in one batched pass.
+
+Bar (north star): logits within 1e-3 relative error (max|dl| / max|l_ref| per step) and greedy
+tokens identical, for the first 64 steps of the headline workload.
+"""
+import sys
+import time
+
+import numpy as np
+import pytest
+
+from tests.helpers import check_greedy_against_oracle, oracle_from_kept
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-3
+
+
+def _say(msg):
+    print(f"[fullsize] {msg}", file=sys.stderr, flush=True)
+
+
+def _build(key, keep=True):
+    from smallmind_amd.model import GpuTransformerModel
+    from smallmind_amd.synthetic import WORKLOADS, load_synthetic_on_device
+    wl = WORKLOADS[key]
+    t0 = time.time()
+    gm = GpuTransformerModel(wl.config)
+    kept = load_synthetic_on_device(gm, wl, seed=42, keep_blocks=keep)
+    om = oracle_from_kept(wl.config, kept) if keep else None
+    del kept
+    _say(f"{key}: GPU model and oracle built in {time.time() - t0:.1f} s")
+    return wl, gm, om
+
+
+@pytest.mark.timeout(900)
+def test_configs2_bench_workload_64_steps(gpu):
+    """configs[2] as bench.py runs it: LLaMA-1.1B, Q4_K layers + Q6_K embedding/head,
+    prompt_tokens(7, 512), the 511 prompt tokens through the chunked matrix-core prefill
+    (256 + 255), then 64 greedy decode steps.  Every step's logits and token against the
+    oracle; the block-graph decode bench.py times (no per-step logits, eight steps per graph)
+    gives the same tokens."""
+    from smallmind_amd.synthetic import prompt_tokens
+    wl, gm, om = _build("llama-1.1b-q4_k")
+    try:
+        cfg = wl.config
+        prompt = prompt_tokens(7, wl.prompt_len, cfg.vocab_size)
+        s = gm.create_session(wl.prompt_len + wl.new_tokens)
+        toks, st, logits = s.generate_greedy(prompt, 64, return_logits=True)
+        assert st["prefill_steps"] == 511 and st["decode_steps"] == 64
+        t0 = time.time()
+        worst = check_greedy_against_oracle(om.session(wl.prompt_len + 64), prompt, toks, logits, LOGIT_TOL)
+        _say(f"configs[2]: 64 steps match the oracle (worst logits error {worst:.2e}, oracle {time.time() - t0:.1f} s)")
+        # the benchmark's path: 256 tokens, no logits copied out (chained eight-step graphs)
+        bench_toks, _ = s.generate_greedy(prompt, wl.new_tokens)
+        assert np.array_equal(bench_toks[:64], toks)
+        _say(f"configs[2]: first tokens {bench_toks[:8].tolist()}")
+        s.close()
+    finally:
+        gm.close()
+
+
+@pytest.mark.timeout(900)
+def test_configs0_gpt2_small_full_size(gpu):
+    """GPT-2-small (12 layers, d768, V 50257 -- the head's last row group holds one
+    row), Q8_0 everywhere, tied head, learned positions; 32-token prompt, 64 greedy steps."""
+    from smallmind_amd.synthetic import prompt_tokens
+    wl, gm, om = _build("gpt2-small-q8_0")
+    try:
+        cfg = wl.config
+        prompt = prompt_tokens(7, wl.prompt_len, cfg.vocab_size)
+        s = gm.create_session(wl.prompt_len + wl.new_tokens)
+        toks, _, logits = s.generate_greedy(prompt, 64, return_logits=True)
+        worst = check_greedy_against_oracle(om.session(wl.prompt_len + 64), prompt, toks, logits, LOGIT_TOL)
+        _say(f"configs[0]: 64 steps match the oracle (worst logits error {worst:.2e})")
+        bench_toks, _ = s.generate_greedy(prompt, wl.new_tokens)
+        assert np.array_equal(bench_toks[:64], toks)
+        s.close()
+    finally:
+        gm.close()
+
+
+@pytest.mark.timeout(900)
+def test_configs4_sixteen_sessions_full_size(gpu):
+    """SmolLM-1.7B Q5_K, tied embeddings, 16 sessions with the bench's prompts
+    (prompt_tokens(100 + i, 256)).  Every session's first 8 steps (logits and tokens) against
+    the oracle; then all 128 tokens of every session are the same whether the session decodes
+    alone (GEMV graphs), in the lockstep batch (smx_batch_generate, 16-token GEMM with folded
+    RMSNorm) or through the continuous batcher one step per call."""
+    from smallmind_amd.model import ContinuousBatcher, GpuInferenceSession
+    from smallmind_amd.synthetic import prompt_tokens
+    wl, gm, om = _build("smollm-1.7b-q5_k")
+    try:
+        cfg = wl.config
+        n, ctx = wl.sessions, wl.prompt_len + wl.new_tokens
+        prompts = [prompt_tokens(100 + i, wl.prompt_len, cfg.vocab_size) for i in range(n)]
+        alone, first = [], []
+        for p in prompts:
+            s = gm.create_session(ctx)
+            t8, _, l8 = s.generate_greedy(p, 8, return_logits=True)
+            first.append((t8, l8))
+            t, _ = s.generate_greedy(p, wl.new_tokens)
+            assert np.array_equal(t[:8], t8)
+            alone.append(t)
+            s.close()
+        sess = [gm.create_session(ctx) for _ in range(n)]
+        lock, _ = GpuInferenceSession.generate_greedy_batch(sess, prompts, wl.new_tokens)
+        b = ContinuousBatcher(gm, n, ctx)
+        for x, p in zip(sess, prompts):
+            b.add(x, p)
+        cont = np.concatenate([b.step(1) for _ in range(wl.new_tokens)], axis=1)
+        b.close()
+        for x in sess:
+            x.close()
+        for i in range(n):
+            assert np.array_equal(lock[i], alone[i]), (i, int(np.argmax(lock[i] != alone[i])))
+            assert np.array_equal(cont[i], alone[i]), (i, int(np.argmax(cont[i] != alone[i])))
+        _say("configs[4]: lockstep, batcher and single-session tokens agree for 16 x 128 steps")
+        t0 = time.time()
+        osess = [om.session(ctx) for _ in range(n)]
+        om.prefill_many(osess, [p[:-1] for p in prompts])
+        _say(f"configs[4]: oracle prefill of 16 x 255 tokens in {time.time() - t0:.1f} s")
+        tok = [int(p[-1]) for p in prompts]
+        worst = 0.0
+        for k in range(8):
+            ref = om.multi_step(osess, tok, [wl.prompt_len - 1 + k] * n)
+            for i in range(n):
+                err = float(np.abs(first[i][1][k] - ref[i]).max() / np.abs(ref[i]).max())
+                worst = max(worst, err)
+                assert err <= LOGIT_TOL, (i, k, err)
+                assert int(first[i][0][k]) == int(np.argmax(ref[i])), (i, k)
+            tok = [int(first[i][0][k]) for i in range(n)]
+        _say(f"configs[4]: 16 sessions x 8 steps match the oracle (worst logits error {worst:.2e}, "
+             f"{time.time() - t0:.1f} s)")
+    finally:
+        gm.close()
+
+
+@pytest.mark.timeout(900)
+def test_configs3_long_prompt_full_size(gpu):
+    """LLaMA-1.1B with Q8_0 layers and a Q6_K head, the bench's 4096-token prompt
+    through 16 prefill chunks (matrix-core GEMM + prefill attention), then 8 greedy decode
+    steps at ~4.1K positions (two-workgroup P.V attention) against the oracle."""
+    from smallmind_amd.synthetic import prompt_tokens
+    wl, gm, om = _build("llama-1.1b-q8_0-4k")
+    try:
+        cfg = wl.config
+        prompt = prompt_tokens(7, wl.prompt_len, cfg.vocab_size)
+        s = gm.create_session(wl.prompt_len + wl.new_tokens)
+        toks, _, logits = s.generate_greedy(prompt, 8, return_logits=True)
+        t0 = time.time()
+        worst = check_greedy_against_oracle(om.session(wl.prompt_len + 8), prompt, toks, logits, LOGIT_TOL)
+        _say(f"configs[3]: 8 steps at 4096+ positions match the oracle (worst {worst:.2e}, "
+             f"oracle {time.time() - t0:.1f} s)")
+        s.close()
+    finally:
+        gm.close()

@@ -8,7 +8,7 @@ import pytest
 
 import oracle as O
 from smallmind_amd.model import ModelConfig
-from tests.helpers import build_pair, rel_err
+from tests.helpers import build_pair, check_greedy_against_oracle, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -155,6 +155,8 @@ def test_model_from_gguf_equals_direct_upload(key, tmp_path):
     t1, _, l1 = s1.generate_greedy(prompt, 16, return_logits=True)
     t2, _, l2 = s2.generate_greedy(prompt, 16, return_logits=True)
     assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
+    # and the GGUF-loaded model against the reference forward of the same tensors
+    check_greedy_against_oracle(om.session(64), prompt, t2, l2, LOGIT_TOL)
     s1.close()
     s2.close()
     gg.close()
@@ -514,3 +516,71 @@ def test_long_context_decode_two_chunk_attention(gpu):
         sess.close()
     finally:
         gm.close()
+
+
+def test_two_threads_generate_while_batcher_captures(pairs):
+    """One thread generates on a session while another drives a batcher of the same model
+    through three member counts (a graph capture for each); each session and batcher runs on
+    its own stream, so neither captures the other's work.  Both give the reference's tokens."""
+    import threading
+
+    from smallmind_amd.model import ContinuousBatcher
+    om, gm = _pair(pairs, "llama-q4k")
+    cfg = SMALL["llama-q4k"][0]
+    rng = np.random.default_rng(41)
+    pa = rng.integers(0, cfg.vocab_size, 10).astype(np.int32)
+    pb = [rng.integers(0, cfg.vocab_size, n).astype(np.int32) for n in (4, 9, 15)]
+    ref_a = _ref_greedy(om, pa, 24)
+    ref_b = [_ref_greedy(om, p, 12) for p in pb]
+    sa = gm.create_session(96)
+    sb = [gm.create_session(96) for _ in pb]
+    out, errors = {"a": []}, []
+
+    def run_a():
+        try:
+            for _ in range(6):
+                out["a"].append(sa.generate_greedy(pa, 24)[0].tolist())
+        except Exception as e:   # noqa: BLE001  (reported by the main thread)
+            errors.append(e)
+
+    def run_b():
+        try:
+            b = ContinuousBatcher(gm, 4, 96)
+            got = [[] for _ in pb]
+            for i, (s, p) in enumerate(zip(sb, pb)):
+                b.add(s, p)                      # member counts 1, 2, 3: a capture each
+                for _ in range(4):
+                    for j, t in enumerate(b.step(1)[:, 0]):
+                        got[j].append(int(t))
+            b.close()
+            out["b"] = got
+        except Exception as e:   # noqa: BLE001
+            errors.append(e)
+
+    ta, tb = threading.Thread(target=run_a), threading.Thread(target=run_b)
+    ta.start()
+    tb.start()
+    ta.join()
+    tb.join()
+    assert not errors, errors
+    assert all(t == ref_a for t in out["a"])
+    # member j joined before step 4*j: it has 12 - 4*j tokens
+    for j, p in enumerate(pb):
+        assert out["b"][j] == ref_b[j][:12 - 4 * j], j
+    for s in [sa] + sb:
+        s.close()
+
+
+def test_serve_continuous_releases_its_sessions(pairs):
+    """serve_continuous closes every session it made (each holds a KV cache) and its batcher,
+    call after call."""
+    from smallmind_amd.model import serve_continuous
+    om, gm = _pair(pairs, "smollm-q5k")
+    cfg = SMALL["smollm-q5k"][0]
+    rng = np.random.default_rng(3)
+    prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.int32) for n in (3, 8, 5)]
+    before = list(gm._sessions)
+    for _ in range(2):
+        outs = serve_continuous(gm, prompts, 4, max_members=2, max_ctx=64)
+        assert [o.tolist() for o in outs] == [_ref_greedy(om, p, 4) for p in prompts]
+        assert gm._sessions == before and not getattr(gm, "_batchers", [])

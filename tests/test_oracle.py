@@ -486,3 +486,62 @@ def test_single_token_attention_passes_v_through():
     # attention output of head h is the V row of its KV head.
     s = np.zeros((1, 1), np.float32)
     assert O.scale_mask_softmax(s, 0.125)[0, 0] == 1.0
+
+
+@pytest.mark.parametrize("arch", ["llama", "gpt2"])
+def test_threaded_batched_paths_are_bit_identical(arch):
+    """The oracle's linears run row blocks over threads and 8 tokens per vector; every output
+    keeps its own fma chain over k in order, so one thread, all threads, a batched prefill and a
+    multi-session step must agree bit for bit with single-token steps.  Ragged shapes: vocab
+    300 (a partial 8-row block and a partial group of four blocks), 13 tokens (a partial tile)."""
+    cfg, om, _ = _tiny(arch)
+    rng = np.random.default_rng(17)
+    toks = rng.integers(0, cfg.vocab_size, 13).astype(np.int32)
+    n0 = O.get_threads()
+    try:
+        O.set_threads(1)
+        full1 = om.forward_nocache(toks, all_rows=True)
+        s1 = om.session(32)
+        steps1 = [s1.step(int(t), p) for p, t in enumerate(toks)]
+        O.set_threads(3)
+        assert np.array_equal(om.forward_nocache(toks, all_rows=True), full1)
+    finally:
+        O.set_threads(0)
+    assert O.get_threads() == n0
+    assert np.array_equal(om.forward_nocache(toks, all_rows=True), full1)
+    s2 = om.session(32)
+    last = s2.prefill(toks[:9], 0, want_logits=True)
+    assert np.array_equal(last, steps1[8])
+    for p in range(9, 13):                       # steps continue on the prefilled cache
+        assert np.array_equal(s2.step(int(toks[p]), p), steps1[p])
+    # three sessions at different positions in one pass vs one step each
+    prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.int32) for n in (5, 1, 11)]
+    sa = [om.session(32) for _ in prompts]
+    sb = [om.session(32) for _ in prompts]
+    for a, b, p in zip(sa, sb, prompts):
+        if len(p) > 1:
+            a.prefill(p[:-1], 0)
+            b.prefill(p[:-1], 0)
+    tk = [int(p[-1]) for p in prompts]
+    for step in range(3):
+        pos = [len(p) - 1 + step for p in prompts]
+        multi = om.multi_step(sa, tk, pos)
+        single = [b.step(t, q) for b, t, q in zip(sb, tk, pos)]
+        assert np.array_equal(multi, np.stack(single))
+        tk = [int(np.argmax(r)) for r in single]
+
+
+def test_prefill_many_equals_prefill_each():
+    """Several prompts prefilled in one pass leave every session's cache as its own prefill
+    does: the next step's logits are bit-identical."""
+    cfg, om, _ = _tiny("llama")
+    rng = np.random.default_rng(23)
+    prompts = [rng.integers(0, cfg.vocab_size, n).astype(np.int32) for n in (7, 2, 12)]
+    sa = [om.session(32) for _ in prompts]
+    sb = [om.session(32) for _ in prompts]
+    om.prefill_many(sa, [p[:-1] for p in prompts])
+    for b, p in zip(sb, prompts):
+        for q, t in enumerate(p[:-1]):
+            b.step(int(t), q, want_logits=False)
+    for a, b, p in zip(sa, sb, prompts):
+        assert np.array_equal(a.step(int(p[-1]), len(p) - 1), b.step(int(p[-1]), len(p) - 1))
