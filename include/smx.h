@@ -86,6 +86,14 @@ SMX_API int smx_weight_info(const smx_weight *w, int *type, int64_t *rows, int64
  * (Q8WeightTensor.cs:43-48). */
 SMX_API int smx_weight_matmul(const smx_weight *w, const float *act_dev, float *out_dev, int m,
                               int k, int n, void *stream);
+/* smx_weight_matmul without any device allocation: no counterpart in the reference.  For callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same results as smx_weight_matmul.  From m >= 4 rows the activation parts go to a
+ * fixed 16 MiB scratch array per GPU: calls needing more (ceil(m/16) * k/32 * 3072 bytes) return
+ * SMX_EINVAL.  Every call on one GPU shares that array, so calls that overlap on one GPU (other
+ * streams, other threads) race: the caller serialises them. */
+SMX_API int smx_weight_matmul_noalloc(const smx_weight *w, const float *act_dev, float *out_dev, int m,
+                                      int k, int n, void *stream);
 /* IWeightTensor.ToFloat32 (IWeightTensor.cs:41): [rows][cols] fp32, bit-identical to the
  * reference dequantization of the original blocks. */
 SMX_API int smx_weight_to_float32(const smx_weight *w, float *out_dev, void *stream);

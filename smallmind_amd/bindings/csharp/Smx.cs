@@ -52,6 +52,8 @@ namespace SmallMind.Backends.Rocm
         [DllImport(Lib)] public static extern int smx_weight_info(IntPtr w, out int type, out long rows, out long cols);
         [DllImport(Lib)] public static extern int smx_weight_matmul(IntPtr w, float* actDev, float* outDev, int m,
             int k, int n, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_weight_matmul_noalloc(IntPtr w, float* actDev, float* outDev,
+            int m, int k, int n, IntPtr stream);
         [DllImport(Lib)] public static extern int smx_weight_to_float32(IntPtr w, float* outDev, IntPtr stream);
         [DllImport(Lib)] public static extern int smx_weight_destroy(IntPtr w);
 

@@ -876,6 +876,80 @@ SMX_API int smx_weight_matmul(const smx_weight *w, const float *act_dev, float *
     return SMX_OK;
 }
 
+}  // extern "C"
+
+// Scratch of smx_weight_matmul_noalloc: the matrix-core GEMM's activation parts live in this
+// file-scope device array instead of an allocation.  Each GPU holds its own copy for the life
+// of the process.  Host code never passes the array's name to a kernel or a copy (in host code
+// it names a host-side stand-in): it uses the per-device address from hipGetSymbolAddress.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per device.
+int noalloc_scratch(uint8_t **out)
+{
+    int dev = -1;
+    SMX_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) SMX_FAIL(SMX_EUNSUPPORTED, "smx_weight_matmul_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        SMX_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (!ptr) SMX_FAIL(SMX_EDEVICE, "smx_weight_matmul_noalloc: no device address for the scratch array");
+        g_scratch_ptr[dev] = (uint8_t *)ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return SMX_OK;
+}
+}  // namespace
+
+extern "C" {
+
+SMX_API int smx_weight_matmul_noalloc(const smx_weight *w, const float *act_dev, float *out_dev, int m, int k,
+                                      int n, void *stream)
+{
+    if (!w || !act_dev || !out_dev) SMX_FAIL(SMX_EINVAL, "smx_weight_matmul_noalloc: null argument");
+    if (k != w->mat.cols || n != w->mat.rows)
+        SMX_FAIL(SMX_EINVAL, "smx_weight_matmul_noalloc: k=%d must equal cols=%lld and n=%d rows=%lld", k,
+                 (long long)w->mat.cols, n, (long long)w->mat.rows);
+    if (m <= 0 || m > 65535) SMX_FAIL(SMX_EINVAL, "smx_weight_matmul_noalloc: m=%d out of range", m);
+    hipStream_t st = (hipStream_t)stream;
+    if (m < kQgemmMinRows) {   // the GEMV path uses no scratch
+        GemvArgs a{};
+        a.w = w->mat.view();
+        a.x = act_dev;
+        a.x_stride = k;
+        a.out = out_dev;
+        a.out_stride = n;
+        a.pro = PRO_NONE;
+        a.epi = EPI_STORE;
+        SMX_HIP(launch_gemv(a, m, st));
+        return SMX_OK;
+    }
+    const size_t need = qgemm_xp_bytes(m, k);
+    if (need > kNoAllocScratchBytes)
+        SMX_FAIL(SMX_EINVAL, "smx_weight_matmul_noalloc: m=%d, k=%d needs %zu bytes of scratch; the limit is %zu "
+                             "(ceil(m/16) * k/32 * 3072 bytes)", m, k, need, kNoAllocScratchBytes);
+    uint8_t *xp = nullptr;
+    int rc = noalloc_scratch(&xp);
+    if (rc != SMX_OK) return rc;
+    // k_qprep writes every byte of the parts it uses (padding rows as zeros): nothing to clear
+    QgemmArgs q{};
+    q.w = w->mat.view();
+    q.xp = xp;
+    q.M = m;
+    q.y = out_dev;
+    q.y_stride = n;
+    q.epi = EPI_STORE;
+    SMX_HIP(launch_qgemm(q, act_dev, k, PRO_NONE, nullptr, nullptr, 0.0f, st));
+    return SMX_OK;
+}
+
 SMX_API int smx_weight_to_float32(const smx_weight *w, float *out_dev, void *stream)
 {
     if (!w || !out_dev) SMX_FAIL(SMX_EINVAL, "smx_weight_to_float32: null argument");
