@@ -2,12 +2,12 @@
 
 One step = one request of the configs[2] workload: a 512-token seeded prompt (prefilled
 through the KV cache) and 256 greedy tokens, all on the device.  `value` is decode tokens/s
-(GPU-event time of the token-producing steps).  The dominant kernel -- the fused Q4_K GEMV at
-the gate/up shape (11264 x 2048) -- is then timed on its own with HIP events around replays of
-a captured graph of launches over rotating weight copies larger than the 256 MB MALL, giving
-the roofline figure; the configs[1] Q4_0 GEMV shapes are timed the same way.  The CPU
-baseline is the oracle's reference-faithful path (fp32 weights dequantized at load, one
-thread) timed on a bounded sample of the same model.
+(GPU-event time of the token-producing steps).  The metric's kernel -- the fused Q4_K GEMV at
+the gate/up shape (11264 x 2048), the largest weight stream of the decode step -- is then timed
+on its own with HIP events around replays of a captured graph of launches over rotating weight
+copies larger than the 256 MB MALL, giving the roofline figure; the configs[1] Q4_0 GEMV shapes
+are timed the same way.  The CPU baseline is the oracle on the same model at the same
+positions: reference-faithful (fp32 weights dequantized at load, one thread) and on all cores.
 """
 from __future__ import annotations
 
@@ -71,7 +71,7 @@ def gemv_timing(qt: int, N: int, K: int, seed: int, min_bytes: int = 600 << 20, 
 
 
 def gemv_roofline():
-    """The dominant decode kernel: the fused Q4_K GEMV at the gate/up shape (11264 x 2048)."""
+    """The metric's kernel: the fused Q4_K GEMV at the gate/up shape (11264 x 2048)."""
     g = gemv_timing(12, 2 * 5632, 2048, seed=3)
     g["kernel"] = "k_gemv<Q4_K,R=4,S=1> (fused dequant-GEMV, gate/up shape 11264x2048)"
     return g
@@ -88,10 +88,39 @@ def c2_gemv_lines():
     return out
 
 
+def decode_step_bytes(wl, mean_pos: float) -> int:
+    """Algorithmic HBM bytes of one decode step (one token for each of wl.sessions sessions): every
+    layer matrix and the head once per step, one embedding row (and one learned-position row)
+    per token -- the tables themselves are not streamed unless the head is tied to them -- all
+    norm weights and biases, and each session's K/V of mean_pos positions (fp32)."""
+    from smallmind_amd.quantization import row_bytes
+    from smallmind_amd.synthetic import tensor_specs
+    cfg = wl.config
+    total = 0
+    for s in tensor_specs(cfg, wl.layer_type, wl.embd_type, wl.head_type):
+        if len(s.dims) == 1:
+            total += 4 * s.n
+        elif s.name in ("token_embd.weight", "position_embd.weight"):
+            total += wl.sessions * row_bytes(s.qtype, s.dims[0])
+            if s.name == "token_embd.weight" and wl.head_type is None:   # tied: the head reads it all
+                total += s.dims[1] * row_bytes(s.qtype, s.dims[0])
+        else:
+            total += s.dims[1] * row_bytes(s.qtype, s.dims[0])
+    kv_per_pos = 2 * cfg.block_count * cfg.head_count_kv * cfg.head_dim * 4
+    return int(total + wl.sessions * kv_per_pos * mean_pos)
+
+
+def mean_attended(wl) -> float:
+    """Decode token i (0-based) sits at position prompt_len - 1 + i and attends to prompt_len + i
+    positions; the mean over the new tokens."""
+    return wl.prompt_len + (wl.new_tokens - 1) / 2
+
+
 def other_configs():
     """configs[0], [3] and [4] measured on the same build: GPT-2-small Q8_0 decode; LLaMA-1.1B
     Q8_0 with a 4096-token prefill (matrix-core GEMM chunks) then decode at ~4.1K context; and
     SmolLM-1.7B Q5_K with 16 sessions (256-token prompts, 128 tokens each) in lockstep."""
+    import numpy as np
     import torch
 
     from smallmind_amd.model import GpuInferenceSession, GpuTransformerModel
@@ -106,10 +135,16 @@ def other_configs():
         prompt = prompt_tokens(7, wl.prompt_len, wl.config.vocab_size)
         sess.generate_greedy(prompt, 8)                      # warmup
         toks, st = sess.generate_greedy(prompt, wl.new_tokens)
+        tok_s = wl.new_tokens / (st["decode_ms"] * 1e-3)
+        step_bytes = decode_step_bytes(wl, mean_attended(wl))
         out[key] = {"prompt_len": wl.prompt_len, "new_tokens": wl.new_tokens,
                     "prefill_tok_s": round((wl.prompt_len - 1) / (st["prefill_ms"] * 1e-3), 1),
-                    "decode_tok_s": round(wl.new_tokens / (st["decode_ms"] * 1e-3), 1),
-                    "weight_bytes": int(model.weight_bytes())}
+                    "decode_tok_s": round(tok_s, 1),
+                    "weight_bytes": int(model.weight_bytes()),
+                    "bytes_per_token": step_bytes,
+                    "decode_effective_gbs": round(step_bytes * tok_s / 1e9, 1),
+                    "hbm_frac": round(step_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+                    "first_tokens": [int(t) for t in toks[:8]]}
         sess.close()
         model.close()
         torch.cuda.synchronize()
@@ -121,12 +156,17 @@ def other_configs():
     prompts = [prompt_tokens(100 + i, wl.prompt_len, wl.config.vocab_size) for i in range(wl.sessions)]
     GpuInferenceSession.generate_greedy_batch(sess, prompts, 8)        # warmup
     toks, st = GpuInferenceSession.generate_greedy_batch(sess, prompts, wl.new_tokens)
+    step_bytes = decode_step_bytes(wl, mean_attended(wl))
+    step_s = st["decode_ms"] * 1e-3 / wl.new_tokens
     out["smollm-1.7b-q5_k"] = {
         "sessions": wl.sessions, "prompt_len": wl.prompt_len, "new_tokens": wl.new_tokens,
         "prefill_tok_s": round(st["prefill_steps"] / (st["prefill_ms"] * 1e-3), 1),
         "decode_tok_s_aggregate": round(wl.sessions * wl.new_tokens / (st["decode_ms"] * 1e-3), 1),
         "decode_ms_per_step": round(st["decode_ms"] / wl.new_tokens, 4),
-        "weight_bytes": int(model.weight_bytes())}
+        "weight_bytes": int(model.weight_bytes()),
+        "bytes_per_step": step_bytes,
+        "decode_effective_gbs": round(step_bytes / step_s / 1e9, 1),
+        "hbm_frac": round(step_bytes / step_s / 1e9 / HBM_PEAK_GBS, 4)}
     # the same 16 requests through the continuous batcher, one step per call as a serving loop
     # runs it (each call returns its tokens to the host before the next step is queued)
     import time
@@ -136,14 +176,17 @@ def other_configs():
     b = ContinuousBatcher(model, wl.sessions, wl.prompt_len + wl.new_tokens)
     for x, p in zip(sess, prompts):
         b.add(x, p)
-    for _ in range(4):
-        b.step(1)                                                     # warmup (graph capture)
+    got = [b.step(1) for _ in range(4)]                               # warmup (graph capture)
     n_steps = wl.new_tokens - 8
     t0 = time.perf_counter()
     for _ in range(n_steps):
-        b.step(1)
+        got.append(b.step(1))
     dt = time.perf_counter() - t0
     b.close()
+    # the batcher's tokens are the lockstep run's (same prompts, same model)
+    got = np.concatenate(got, axis=1)
+    out["smollm-1.7b-q5_k"]["continuous_batcher_tokens_match_lockstep"] = bool(
+        np.array_equal(got, toks[:, :got.shape[1]]))
     out["smollm-1.7b-q5_k"]["continuous_batcher_ms_per_step"] = round(dt * 1e3 / n_steps, 4)
     out["smollm-1.7b-q5_k"]["continuous_batcher_tok_s_aggregate"] = round(wl.sessions * n_steps / dt, 1)
     for x in sess:
@@ -181,10 +224,16 @@ def copy_calibration(n_bytes: int = 1 << 30, reps: int = 5):
           flush=True)
 
 
-def cpu_baseline(kept, wl, budget_s: float = 15.0):
+def cpu_baseline(kept, wl, budget_s: float = 12.0):
+    """The oracle on the host's cores, on the headline workload's positions: the 511 prompt
+    tokens are prefilled (all cores, untimed), then decode steps from position 511 on are timed
+    -- first the reference-faithful way (fp32 weights dequantized at load, GEMV on one thread,
+    BASELINE.md mode R), then on every core (mode A: the same fp32 arithmetic over all threads).
+    Each mode runs about budget_s seconds."""
     import numpy as np
 
     import oracle as O
+    from smallmind_amd.synthetic import prompt_tokens
     cfg = wl.config
     t0 = time.time()
     om = O.OracleModel(O.ARCH_LLAMA, cfg.vocab_size, cfg.context_length, cfg.embedding_length,
@@ -194,14 +243,35 @@ def cpu_baseline(kept, wl, budget_s: float = 15.0):
         om.set_tensor(name, qt, data.cpu().numpy(), int(np.prod(dims)))
     om.finalize()
     load_s = time.time() - t0
-    prompt = np.arange(4, dtype=np.int32) * 97 % cfg.vocab_size
-    _, _, dec1 = om.generate_greedy(prompt, 1)
-    n = max(2, min(64, int(budget_s / max(dec1, 1e-3))))
-    toks, pre, dec = om.generate_greedy(prompt, n)
-    return {"value": n / dec, "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"same seeded configs[2] weights, fp32 dequantized at load ({load_s:.1f} s), "
-                      f"4-token prompt then {n} greedy decode steps, single thread, "
-                      f"{platform.processor() or platform.machine()} x{os.cpu_count()} host"}
+    prompt = prompt_tokens(7, wl.prompt_len, cfg.vocab_size)
+    n_all = O.get_threads()
+    out = {}
+    for mode, threads in (("reference", 1), ("all_cores", n_all)):
+        O.set_threads(n_all)
+        s = om.session(wl.prompt_len + 256)
+        s.prefill(prompt[:-1], 0)
+        O.set_threads(threads)
+        tok, pos, n, t_dec = int(prompt[-1]), wl.prompt_len - 1, 0, 0.0
+        while t_dec < budget_s and n < 256:
+            t1 = time.perf_counter()
+            tok = int(np.argmax(s.step(tok, pos)))
+            t_dec += time.perf_counter() - t1
+            pos += 1
+            n += 1
+        out[mode] = (n / t_dec, n, threads)
+        del s
+    O.set_threads(0)
+    v, n, _ = out["reference"]
+    va, na, ta = out["all_cores"]
+    cpu = f"{platform.processor() or platform.machine()} x{os.cpu_count()} host"
+    return {"value": round(v, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"oracle on the same seeded configs[2] weights (fp32, dequantized at load in {load_s:.1f} s), "
+                      f"the {wl.prompt_len - 1}-token prompt prefilled untimed, then {n} greedy decode steps "
+                      f"at positions {wl.prompt_len - 1}..{wl.prompt_len - 2 + n} timed on one thread "
+                      f"(the reference's single-threaded M=1 GEMV); {cpu}",
+            "all_cores": {"value": round(va, 3), "unit": "tok/s", "cores": ta,
+                          "sample": f"{na} decode steps from position {wl.prompt_len - 1}, linears and attention "
+                                    f"over {ta} threads (same fp32 arithmetic; not the reference's threading)"}}
 
 
 def main():
@@ -244,7 +314,6 @@ def main():
     log(f"building {args.workload} on device")
     model = GpuTransformerModel(cfg)
     kept = load_synthetic_on_device(model, wl, seed=42, keep_blocks=not args.no_cpu_baseline)
-    wbytes = model.weight_bytes()
     max_ctx = wl.prompt_len + wl.new_tokens
     sess = model.create_session(max_ctx)
     prompt = prompt_tokens(7, wl.prompt_len, cfg.vocab_size)
@@ -264,10 +333,7 @@ def main():
     wall = time.perf_counter() - t0
     dec_tok_s = args.steps * wl.new_tokens / (dec_ms * 1e-3)
     pre_tok_s = args.steps * (wl.prompt_len - 1) / (pre_ms * 1e-3)
-    hd = cfg.head_dim
-    mean_pos = wl.prompt_len + wl.new_tokens / 2
-    kv_bytes = 2 * cfg.block_count * cfg.head_count_kv * hd * 4 * mean_pos
-    token_bytes = wbytes + kv_bytes
+    token_bytes = decode_step_bytes(wl, mean_attended(wl))
     out = {
         "metric": METRIC, "value": round(dec_tok_s, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3 / args.steps, 3),
@@ -281,11 +347,15 @@ def main():
         "decode_ms_per_token": round(dec_ms / (args.steps * wl.new_tokens), 4),
         "decode_effective_gbs": round(token_bytes / (dec_ms * 1e-3 / (args.steps * wl.new_tokens)) / 1e9, 1),
         "bytes_per_token": int(token_bytes),
+        "bytes_per_token_note": f"layers + head + one embedding row + norms + K/V at the mean attended "
+                                f"position {mean_attended(wl):.1f}",
+        "hbm_frac": round(token_bytes / (dec_ms * 1e-3 / (args.steps * wl.new_tokens)) / 1e9 / HBM_PEAK_GBS, 4),
         "first_tokens": [int(t) for t in tokens[:8]],
     }
     if not args.no_roofline:
         log("timing the dominant GEMV kernel")
         g = gemv_roofline()
+        # the metric's kernel: the quantized GEMV (the decode step's largest byte stream)
         out["roofline"] = {"bound": "hbm", "achieved": round(g["gbs"], 1), "peak": HBM_PEAK_GBS,
                            "unit": "GB/s", "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
                            "traffic": traffic_from_profiles(),
@@ -298,7 +368,7 @@ def main():
     if not args.no_other_configs:
         out["other_configs"] = other_configs()
     if not args.no_cpu_baseline:
-        log("timing the CPU baseline (oracle, one thread)")
+        log("timing the CPU baseline (oracle: one thread, then all cores)")
         out["cpu_baseline"] = cpu_baseline(kept, wl)
     del kept
     print(json.dumps(out), flush=True)

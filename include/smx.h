@@ -80,12 +80,23 @@ typedef struct smx_weight smx_weight;
 SMX_API int smx_weight_create(int type, int64_t rows, int64_t cols, const void *blocks,
                               int blocks_on_device, smx_weight **out);
 SMX_API int smx_weight_info(const smx_weight *w, int *type, int64_t *rows, int64_t *cols);
-/* IWeightTensor.MatMul (IWeightTensor.cs:33): out[m][n] = act[m][k] . W^T with k == cols and
- * n == rows (the GGUF-loader semantics y = x W^T).  Output fully overwritten.
- * SMX_EINVAL on dimension mismatch, as the reference throws ArgumentException
- * (Q8WeightTensor.cs:43-48). */
+/* IWeightTensor.MatMul (IWeightTensor.cs:33) on device pointers, queued on `stream`:
+ * out[m][n] = act[m][k] . W^T with k == cols and n == rows (the GGUF-loader semantics
+ * y = x W^T).  Output fully overwritten.  SMX_EINVAL on dimension mismatch, as the reference
+ * throws ArgumentException (Q8WeightTensor.cs:43-48).  From m >= 4 rows the matrix-core GEMM's
+ * activation parts use device memory kept per weight (grown to the largest m seen; uses on
+ * different streams are ordered), or a stream-ordered allocation under graph capture. */
 SMX_API int smx_weight_matmul(const smx_weight *w, const float *act_dev, float *out_dev, int m,
                               int k, int n, void *stream);
+/* IWeightTensor.MatMul with the reference's operands in host memory (IWeightTensor.cs:33,
+ * ReadOnlySpan<float> activations, Span<float> output): act is m*k floats, out m*n floats, both
+ * owned by the caller and borrowed for the call, which is synchronous.  Checks and results as
+ * smx_weight_matmul.  The device staging is kept per weight and grows to the largest m seen, so
+ * repeated calls allocate nothing; concurrent calls on one weight are serialised. */
+SMX_API int smx_weight_matmul_host(const smx_weight *w, const float *act, float *out, int m, int k, int n);
+/* IWeightTensor.ToFloat32 (IWeightTensor.cs:41) into caller-owned host memory of rows*cols floats
+ * ([rows][cols], bit-identical to the reference dequantization); synchronous. */
+SMX_API int smx_weight_to_float32_host(const smx_weight *w, float *out);
 /* smx_weight_matmul without any device allocation: no counterpart in the reference.  For callers
  * that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  Same results as smx_weight_matmul.  From m >= 4 rows the activation parts go to a
@@ -120,7 +131,8 @@ SMX_API int smx_scale_mask_softmax(float *scores_dev, float scale, int seq, int 
                                    int cache_offset, void *stream);
 /* One decode position of MultiHeadAttention (MultiHeadAttention.cs:676-844): q [n_head][hd],
  * k_cache [n_kv_head][hd][ctx_stride] (dimension-major), v_cache [n_kv_head][ctx_stride][hd],
- * each holding n_pos positions, out [n_head][hd]. */
+ * each holding n_pos positions, out [n_head][hd].  The scores use device memory kept per device
+ * (grown to the largest request seen; uses on different streams are ordered). */
 SMX_API int smx_attention_decode(const float *q_dev, const float *k_cache_dev,
                                  const float *v_cache_dev, float *out_dev, int n_head,
                                  int n_kv_head, int head_dim, int ctx_stride, int n_pos,

@@ -23,7 +23,7 @@ EXPORTS = [
     "smx_version", "smx_last_error", "smx_type_block_elems", "smx_type_block_bytes",
     "smx_type_row_bytes", "smx_dequant", "smx_quantize", "smx_fill_normal",
     "smx_weight_create", "smx_weight_info", "smx_weight_matmul", "smx_weight_matmul_noalloc",
-    "smx_weight_to_float32",
+    "smx_weight_matmul_host", "smx_weight_to_float32", "smx_weight_to_float32_host",
     "smx_weight_destroy", "smx_rmsnorm", "smx_layernorm", "smx_rope_tables", "smx_rope",
     "smx_scale_mask_softmax", "smx_attention_decode", "smx_attention_prefill", "smx_silu_mul", "smx_gelu", "smx_argmax",
     "smx_context_create", "smx_context_destroy", "smx_model_create", "smx_model_upload_tensor",
@@ -96,6 +96,8 @@ def load() -> ctypes.CDLL:
         "smx_weight_info": (i32, [vp, ctypes.POINTER(i32), ctypes.POINTER(i64), ctypes.POINTER(i64)]),
         "smx_weight_matmul": (i32, [vp, vp, vp, i32, i32, i32, vp]),
         "smx_weight_matmul_noalloc": (i32, [vp, vp, vp, i32, i32, i32, vp]),
+        "smx_weight_matmul_host": (i32, [vp, vp, vp, i32, i32, i32]),
+        "smx_weight_to_float32_host": (i32, [vp, vp]),
         "smx_weight_to_float32": (i32, [vp, vp, vp]),
         "smx_weight_destroy": (i32, [vp]),
         "smx_rmsnorm": (i32, [vp, vp, vp, i32, i32, f32, vp]),

@@ -7,6 +7,8 @@
 // options (ProductionInferenceOptions.cs:19-87).
 using System;
 using System.Runtime.InteropServices;
+using SmallMind.Quantization.Abstractions;
+using SmallMind.Runtime.Execution;
 
 namespace SmallMind.Backends.Rocm
 {
@@ -52,6 +54,9 @@ namespace SmallMind.Backends.Rocm
         [DllImport(Lib)] public static extern int smx_weight_info(IntPtr w, out int type, out long rows, out long cols);
         [DllImport(Lib)] public static extern int smx_weight_matmul(IntPtr w, float* actDev, float* outDev, int m,
             int k, int n, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_weight_matmul_host(IntPtr w, float* act, float* output, int m,
+            int k, int n);
+        [DllImport(Lib)] public static extern int smx_weight_to_float32_host(IntPtr w, float* output);
         [DllImport(Lib)] public static extern int smx_weight_matmul_noalloc(IntPtr w, float* actDev, float* outDev,
             int m, int k, int n, IntPtr stream);
         [DllImport(Lib)] public static extern int smx_weight_to_float32(IntPtr w, float* outDev, IntPtr stream);
@@ -127,6 +132,94 @@ namespace SmallMind.Backends.Rocm
                 _ => new InvalidOperationException(msg),
             };
         }
+    }
+
+    // IWeightTensor (IWeightTensor.cs:7-42) on the device, injected through
+    // Linear.SetQuantizedWeight (NeuralNet.cs:84-107).  The reference checks k == Rows and
+    // n == Cols (Q8WeightTensor.cs:43-48): Rows = input features, Cols = output features.  The
+    // device matrix holds the GGUF [out][in] rows, and the library computes
+    // output[m][n] = activations[m][k] . W[n][k]^T, the product the reference defines for its
+    // [k][n] weight.  Operands stay in host memory; libsmx.so stages them on the device itself
+    // (kept per weight, so repeated calls allocate nothing).
+    internal sealed unsafe class GpuWeightTensor : IWeightTensor, IDisposable
+    {
+        readonly IntPtr _w;
+        readonly int _in, _out;
+
+        public GpuWeightTensor(int ggmlType, int outFeatures, int inFeatures, ReadOnlySpan<byte> ggufBlocks,
+                               QuantScheme scheme)
+        {
+            _in = inFeatures;
+            _out = outFeatures;
+            Scheme = scheme;
+            fixed (byte* p = ggufBlocks)
+                Smx.Check(Smx.smx_weight_create(ggmlType, outFeatures, inFeatures, p, 0, out _w));
+        }
+
+        public int Rows => _in;
+        public int Cols => _out;
+        public QuantScheme Scheme { get; }
+
+        public void MatMul(ReadOnlySpan<float> activations, Span<float> output, int m, int k, int n)
+        {
+            if (k != Rows) throw new ArgumentException($"k={k} must equal Rows={Rows}");   // Q8WeightTensor.cs:43-48
+            if (n != Cols) throw new ArgumentException($"n={n} must equal Cols={Cols}");
+            if (activations.Length < m * k || output.Length < m * n) throw new ArgumentException("span too short");
+            fixed (float* a = activations)
+            fixed (float* o = output)
+                Smx.Check(Smx.smx_weight_matmul_host(_w, a, o, m, k, n));   // output fully overwritten
+        }
+
+        public float[] ToFloat32()
+        {
+            var r = new float[_in * _out];   // [out][in] rows, bit-identical to GgufModelLoader's dequantization
+            fixed (float* o = r)
+                Smx.Check(Smx.smx_weight_to_float32_host(_w, o));
+            return r;
+        }
+
+        public void Dispose() => Smx.smx_weight_destroy(_w);
+    }
+
+    // IRuntimeExecutor (Execution/IRuntimeExecutor.cs) on the device: RuntimeExecutor's Prefill
+    // and Decode (RuntimeExecutor.cs:40-178) are TransformerModel.Forward calls at position 0 and
+    // at context.CurrentPosition with the KV cache on; here each is one smx_session_forward on the
+    // session that stands for the context's cache (smx_session_reset = ResetKVCache).
+    internal sealed unsafe class GpuRuntimeExecutor : IDisposable
+    {
+        readonly GpuSession _session;
+        readonly int _blockSize, _vocab;
+
+        public GpuRuntimeExecutor(GpuTransformerBackend backend, int blockSize, int vocabSize)
+        {
+            _session = backend.CreateSession(blockSize);
+            _blockSize = blockSize;
+            _vocab = vocabSize;
+        }
+
+        // The prompt, cropped to its last blockSize tokens (RuntimeExecutor.cs:55-57), at
+        // position 0; returns the last position's logits and the number of tokens processed.
+        public (float[] logits, int processed) Prefill(ReadOnlySpan<int> promptTokens)
+        {
+            if (promptTokens.Length == 0) throw new ArgumentException("Prompt tokens cannot be empty");
+            int start = Math.Max(0, promptTokens.Length - _blockSize);
+            var slice = promptTokens.Slice(start);
+            var logits = new float[_vocab];
+            _session.ResetKVCache();
+            _session.ForwardLastRow(slice, 0, logits);
+            return (logits, slice.Length);
+        }
+
+        // One token at the context's current position (RuntimeExecutor.cs:125-145).
+        public float[] Decode(int nextToken, int currentPosition)
+        {
+            var logits = new float[_vocab];
+            Span<int> t = stackalloc int[1] { nextToken };
+            _session.ForwardLastRow(t, currentPosition, logits);
+            return logits;
+        }
+
+        public void Dispose() => _session.Dispose();
     }
 
     // The model on the device: loaded from a GGUF file in one call, or tensor by tensor.

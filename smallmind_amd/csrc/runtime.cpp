@@ -147,6 +147,58 @@ int mat_upload(Mat &m, const void *bytes, int64_t rows, int64_t cols, int on_dev
     return SMX_OK;
 }
 
+// Device memory reused across calls instead of allocated per call: grown on demand (to the
+// largest request seen), with its uses on different streams ordered by an event -- each use
+// waits for the previous one.  The caller holds the mutex that guards it.
+struct Scratch {
+    void *p = nullptr;
+    size_t cap = 0;
+    hipEvent_t last = nullptr;
+    bool used = false;
+};
+
+// Returns S.p with at least `need` bytes, ready for a use queued on stream s.
+int scratch_acquire(Scratch &S, size_t need, hipStream_t s, void **out)
+{
+    if (!S.last) SMX_HIP(hipEventCreateWithFlags(&S.last, hipEventDisableTiming));
+    if (need > S.cap) {
+        if (S.used) SMX_HIP(hipEventSynchronize(S.last));   // every earlier use has finished
+        if (S.p) (void)hipFree(S.p);
+        S.p = nullptr;
+        S.cap = 0;
+        SMX_HIP(hipMalloc(&S.p, need));
+        S.cap = need;
+    } else if (S.used) {
+        SMX_HIP(hipStreamWaitEvent(s, S.last, 0));
+    }
+    *out = S.p;
+    return SMX_OK;
+}
+
+// Marks the end of a use queued on stream s.
+int scratch_release(Scratch &S, hipStream_t s)
+{
+    SMX_HIP(hipEventRecord(S.last, s));
+    S.used = true;
+    return SMX_OK;
+}
+
+void scratch_free(Scratch &S)
+{
+    if (S.used && S.last) (void)hipEventSynchronize(S.last);
+    if (S.p) (void)hipFree(S.p);
+    if (S.last) (void)hipEventDestroy(S.last);
+    S = Scratch{};
+}
+
+// Whether work queued on s is being captured into a graph (stream-ordered allocations are then
+// recorded as graph nodes, made once when the graph is instantiated).
+bool capturing(hipStream_t s)
+{
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(s, &st) == hipSuccess && st == hipStreamCaptureStatusActive;
+}
+
 }  // namespace
 
 // The context stream carries model uploads only (serialised by mu); every session and batcher
@@ -159,7 +211,14 @@ struct smx_context {
 
 struct smx_weight {
     int type = 0;
+    int device = 0;
     Mat mat;
+    // reused device memory, guarded by mu: the GEMM's activation parts, and the staging of the
+    // host-memory entry points (activations in, products or dequantized rows out) with the
+    // stream they run on
+    std::mutex mu;
+    Scratch xp, act, out;
+    hipStream_t host_stream = nullptr;
 };
 
 struct Layer {
@@ -810,8 +869,11 @@ SMX_API int smx_weight_create(int type, int64_t rows, int64_t cols, const void *
         SMX_FAIL(SMX_EINVAL, "smx_weight_create: cols=%lld must be a positive multiple of %d",
                  (long long)cols, fmt_block_elems(fmt));
     if (cols > 16384) SMX_FAIL(SMX_EUNSUPPORTED, "smx_weight_create: cols=%lld exceeds 16384", (long long)cols);
+    int dev = 0;
+    SMX_HIP(hipGetDevice(&dev));
     smx_weight *w = new smx_weight();
     w->type = type;
+    w->device = dev;
     int rc = mat_alloc(w->mat, fmt, rows, cols);
     if (rc == SMX_OK) rc = mat_upload(w->mat, blocks, rows, cols, blocks_on_device, 0, 1, nullptr);
     if (rc != SMX_OK) {
@@ -836,44 +898,129 @@ SMX_API int smx_weight_info(const smx_weight *w, int *type, int64_t *rows, int64
 // GEMV pass per row.
 constexpr int kQgemmMinRows = 4;
 
-SMX_API int smx_weight_matmul(const smx_weight *w, const float *act_dev, float *out_dev, int m,
-                              int k, int n, void *stream)
+}  // extern "C"
+
+namespace {
+int weight_check(const smx_weight *w, int m, int k, int n, const char *fn)
 {
-    if (!w || !act_dev || !out_dev) SMX_FAIL(SMX_EINVAL, "smx_weight_matmul: null argument");
     if (k != w->mat.cols || n != w->mat.rows)
-        SMX_FAIL(SMX_EINVAL, "smx_weight_matmul: k=%d must equal cols=%lld and n=%d rows=%lld", k,
-                 (long long)w->mat.cols, n, (long long)w->mat.rows);
-    if (m <= 0 || m > 65535) SMX_FAIL(SMX_EINVAL, "smx_weight_matmul: m=%d out of range", m);
-    if (m >= kQgemmMinRows) {
-        // several activation rows: one pass over the weights on the matrix cores; the
-        // activation-part scratch is stream-ordered, so concurrent calls on other streams
-        // cannot share it
-        hipStream_t st = (hipStream_t)stream;
+        SMX_FAIL(SMX_EINVAL, "%s: k=%d must equal cols=%lld and n=%d rows=%lld", fn, k, (long long)w->mat.cols, n,
+                 (long long)w->mat.rows);
+    if (m <= 0 || m > 65535) SMX_FAIL(SMX_EINVAL, "%s: m=%d out of range", fn, m);
+    return SMX_OK;
+}
+
+// out[m][n] = act[m][k] W^T on device pointers, queued on st.  The caller holds w->mu.
+int weight_matmul_dev(smx_weight *w, const float *act_dev, float *out_dev, int m, int k, int n, hipStream_t st)
+{
+    if (m < kQgemmMinRows) {
+        GemvArgs a{};
+        a.w = w->mat.view();
+        a.x = act_dev;
+        a.x_stride = k;
+        a.out = out_dev;
+        a.out_stride = n;
+        a.pro = PRO_NONE;
+        a.epi = EPI_STORE;
+        SMX_HIP(launch_gemv(a, m, st));
+        return SMX_OK;
+    }
+    // several activation rows: one pass over the weights on the matrix cores
+    QgemmArgs q{};
+    q.w = w->mat.view();
+    q.M = m;
+    q.y = out_dev;
+    q.y_stride = n;
+    q.epi = EPI_STORE;
+    const size_t need = qgemm_xp_bytes(m, k);
+    if (capturing(st)) {
+        // under graph capture the parts are a stream-ordered allocation recorded in the graph
         uint8_t *xp = nullptr;
-        SMX_HIP(hipMallocAsync((void **)&xp, qgemm_xp_bytes(m, k), st));
-        QgemmArgs q{};
-        q.w = w->mat.view();
+        SMX_HIP(hipMallocAsync((void **)&xp, need, st));
         q.xp = xp;
-        q.M = m;
-        q.y = out_dev;
-        q.y_stride = n;
-        q.epi = EPI_STORE;
         const hipError_t e = launch_qgemm(q, act_dev, k, PRO_NONE, nullptr, nullptr, 0.0f, st);
         const hipError_t f = hipFreeAsync(xp, st);
         SMX_HIP(e);
         SMX_HIP(f);
         return SMX_OK;
     }
-    GemvArgs a{};
-    a.w = w->mat.view();
-    a.x = act_dev;
-    a.x_stride = k;
-    a.out = out_dev;
-    a.out_stride = n;
-    a.pro = PRO_NONE;
-    a.epi = EPI_STORE;
-    SMX_HIP(launch_gemv(a, m, (hipStream_t)stream));
-    return SMX_OK;
+    void *xp = nullptr;
+    int rc = scratch_acquire(w->xp, need, st, &xp);
+    if (rc != SMX_OK) return rc;
+    q.xp = (const uint8_t *)xp;
+    const hipError_t e = launch_qgemm(q, act_dev, k, PRO_NONE, nullptr, nullptr, 0.0f, st);
+    rc = scratch_release(w->xp, st);
+    SMX_HIP(e);
+    return rc;
+}
+
+// Host staging of the host-memory entry points: the weight's own stream and reused device
+// buffers.  The caller holds w->mu.
+int host_stage(smx_weight *w, size_t in_bytes, size_t out_bytes, void **in_dev, void **out_dev)
+{
+    SMX_HIP(hipSetDevice(w->device));
+    if (!w->host_stream) SMX_HIP(hipStreamCreateWithFlags(&w->host_stream, hipStreamNonBlocking));
+    int rc = SMX_OK;
+    if (in_bytes && (rc = scratch_acquire(w->act, in_bytes, w->host_stream, in_dev)) != SMX_OK) return rc;
+    return scratch_acquire(w->out, out_bytes, w->host_stream, out_dev);
+}
+}  // namespace
+
+extern "C" {
+
+SMX_API int smx_weight_matmul(const smx_weight *w, const float *act_dev, float *out_dev, int m,
+                              int k, int n, void *stream)
+{
+    if (!w || !act_dev || !out_dev) SMX_FAIL(SMX_EINVAL, "smx_weight_matmul: null argument");
+    int rc = weight_check(w, m, k, n, "smx_weight_matmul");
+    if (rc != SMX_OK) return rc;
+    smx_weight *W = const_cast<smx_weight *>(w);   // the weight is read-only; its scratch is not
+    std::lock_guard<std::mutex> lock(W->mu);
+    return weight_matmul_dev(W, act_dev, out_dev, m, k, n, (hipStream_t)stream);
+}
+
+SMX_API int smx_weight_matmul_host(const smx_weight *w, const float *act, float *out, int m, int k, int n)
+{
+    if (!w || !act || !out) SMX_FAIL(SMX_EINVAL, "smx_weight_matmul_host: null argument");
+    int rc = weight_check(w, m, k, n, "smx_weight_matmul_host");
+    if (rc != SMX_OK) return rc;
+    smx_weight *W = const_cast<smx_weight *>(w);
+    std::lock_guard<std::mutex> lock(W->mu);
+    const size_t in_bytes = (size_t)m * k * 4, out_bytes = (size_t)m * n * 4;
+    void *a = nullptr, *o = nullptr;
+    if ((rc = host_stage(W, in_bytes, out_bytes, &a, &o)) != SMX_OK) return rc;
+    hipStream_t st = W->host_stream;
+    SMX_HIP(hipMemcpyAsync(a, act, in_bytes, hipMemcpyHostToDevice, st));
+    rc = weight_matmul_dev(W, (const float *)a, (float *)o, m, k, n, st);
+    if (rc == SMX_OK) {
+        const hipError_t e = hipMemcpyAsync(out, o, out_bytes, hipMemcpyDeviceToHost, st);
+        if (e != hipSuccess) {
+            set_error(hipGetErrorString(e));
+            rc = SMX_EDEVICE;
+        }
+    }
+    const int r1 = scratch_release(W->act, st), r2 = scratch_release(W->out, st);
+    SMX_HIP(hipStreamSynchronize(st));
+    return rc != SMX_OK ? rc : r1 != SMX_OK ? r1 : r2;
+}
+
+SMX_API int smx_weight_to_float32_host(const smx_weight *w, float *out)
+{
+    if (!w || !out) SMX_FAIL(SMX_EINVAL, "smx_weight_to_float32_host: null argument");
+    smx_weight *W = const_cast<smx_weight *>(w);
+    std::lock_guard<std::mutex> lock(W->mu);
+    const size_t out_bytes = (size_t)w->mat.rows * w->mat.cols * 4;
+    void *o = nullptr;
+    int rc = host_stage(W, 0, out_bytes, nullptr, &o);
+    if (rc != SMX_OK) return rc;
+    hipStream_t st = W->host_stream;
+    hipError_t e = launch_dequant_smx(w->mat.view(), 0, w->mat.rows, (float *)o, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, o, out_bytes, hipMemcpyDeviceToHost, st);
+    rc = scratch_release(W->out, st);
+    const hipError_t f = hipStreamSynchronize(st);
+    SMX_HIP(e);
+    SMX_HIP(f);
+    return rc;
 }
 
 }  // extern "C"
@@ -889,6 +1036,9 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 uint8_t *g_scratch_ptr[kMaxDevices] = {};
+// smx_attention_decode's scores, per device, reused across calls (kept until the process ends)
+std::mutex g_attn_mu;
+Scratch g_attn_scratch[kMaxDevices];
 
 // The device address of `scratch` on the current device, looked up once per device.
 int noalloc_scratch(uint8_t **out)
@@ -914,10 +1064,8 @@ SMX_API int smx_weight_matmul_noalloc(const smx_weight *w, const float *act_dev,
                                       int n, void *stream)
 {
     if (!w || !act_dev || !out_dev) SMX_FAIL(SMX_EINVAL, "smx_weight_matmul_noalloc: null argument");
-    if (k != w->mat.cols || n != w->mat.rows)
-        SMX_FAIL(SMX_EINVAL, "smx_weight_matmul_noalloc: k=%d must equal cols=%lld and n=%d rows=%lld", k,
-                 (long long)w->mat.cols, n, (long long)w->mat.rows);
-    if (m <= 0 || m > 65535) SMX_FAIL(SMX_EINVAL, "smx_weight_matmul_noalloc: m=%d out of range", m);
+    int rc = weight_check(w, m, k, n, "smx_weight_matmul_noalloc");
+    if (rc != SMX_OK) return rc;
     hipStream_t st = (hipStream_t)stream;
     if (m < kQgemmMinRows) {   // the GEMV path uses no scratch
         GemvArgs a{};
@@ -936,8 +1084,7 @@ SMX_API int smx_weight_matmul_noalloc(const smx_weight *w, const float *act_dev,
         SMX_FAIL(SMX_EINVAL, "smx_weight_matmul_noalloc: m=%d, k=%d needs %zu bytes of scratch; the limit is %zu "
                              "(ceil(m/16) * k/32 * 3072 bytes)", m, k, need, kNoAllocScratchBytes);
     uint8_t *xp = nullptr;
-    int rc = noalloc_scratch(&xp);
-    if (rc != SMX_OK) return rc;
+    if ((rc = noalloc_scratch(&xp)) != SMX_OK) return rc;
     // k_qprep writes every byte of the parts it uses (padding rows as zeros): nothing to clear
     QgemmArgs q{};
     q.w = w->mat.view();
@@ -960,6 +1107,11 @@ SMX_API int smx_weight_to_float32(const smx_weight *w, float *out_dev, void *str
 SMX_API int smx_weight_destroy(smx_weight *w)
 {
     if (!w) return SMX_OK;
+    (void)hipSetDevice(w->device);
+    scratch_free(w->xp);
+    scratch_free(w->act);
+    scratch_free(w->out);
+    if (w->host_stream) (void)hipStreamDestroy(w->host_stream);
     w->mat.release();
     delete w;
     return SMX_OK;
@@ -1026,16 +1178,31 @@ SMX_API int smx_attention_decode(const float *q, const float *kc, const float *v
         SMX_FAIL(SMX_EUNSUPPORTED, "smx_attention_decode: head_dim must be 16, 32, 64 or 128");
     if (n_pos <= 0 || n_pos > ctx_stride || ctx_stride > 40000)
         SMX_FAIL(SMX_EINVAL, "smx_attention_decode: need 1 <= n_pos <= ctx_stride <= 40000");
-    // scores scratch, stream-ordered like the caller's work
     hipStream_t st = (hipStream_t)stream;
-    float *scores = nullptr;
-    SMX_HIP(hipMallocAsync((void **)&scores, attention_scores_floats(n_head, n_pos) * 4, st));
-    const hipError_t e = launch_attention_split(q, kc, vc, out, scores, n_head, n_kv_head, head_dim,
+    const size_t need = attention_scores_floats(n_head, n_pos) * 4;
+    if (capturing(st)) {   // a stream-ordered allocation recorded in the caller's graph
+        float *scores = nullptr;
+        SMX_HIP(hipMallocAsync((void **)&scores, need, st));
+        const hipError_t e = launch_attention_split(q, kc, vc, out, scores, n_head, n_kv_head, head_dim,
+                                                    ctx_stride, nullptr, n_pos, n_pos, st);
+        const hipError_t f = hipFreeAsync(scores, st);
+        SMX_HIP(e);
+        SMX_HIP(f);
+        return SMX_OK;
+    }
+    // the scores scratch of this device, reused call after call
+    int dev = -1;
+    SMX_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) SMX_FAIL(SMX_EUNSUPPORTED, "smx_attention_decode: device %d", dev);
+    std::lock_guard<std::mutex> lock(g_attn_mu);
+    void *scores = nullptr;
+    int rc = scratch_acquire(g_attn_scratch[dev], need, st, &scores);
+    if (rc != SMX_OK) return rc;
+    const hipError_t e = launch_attention_split(q, kc, vc, out, (float *)scores, n_head, n_kv_head, head_dim,
                                                 ctx_stride, nullptr, n_pos, n_pos, st);
-    const hipError_t f = hipFreeAsync(scores, st);
+    rc = scratch_release(g_attn_scratch[dev], st);
     SMX_HIP(e);
-    SMX_HIP(f);
-    return SMX_OK;
+    return rc;
 }
 
 SMX_API int smx_attention_prefill(const float *q, const float *kc, const float *vc, float *out,

@@ -131,6 +131,25 @@ class GpuWeightTensor:
         call("smx_weight_matmul", self._h, _ptr(activations), _ptr(output), m, k, n, _stream())
         return output
 
+    def mat_mul_host(self, activations: np.ndarray, m: int, k: int, n: int, output: np.ndarray | None = None):
+        """IWeightTensor.MatMul with host operands, as the reference takes them
+        (ReadOnlySpan<float> activations, Span<float> output): numpy float32 arrays of at least
+        m*k and m*n elements; synchronous (smx_weight_matmul_host)."""
+        a = np.ascontiguousarray(activations, dtype=np.float32).reshape(-1)
+        if output is None:
+            output = np.empty((m, n), np.float32)
+        if a.size < m * k or output.size < m * n or not output.flags.c_contiguous or output.dtype != np.float32:
+            raise ValueError("activation/output buffers are too small or not contiguous float32")
+        call("smx_weight_matmul_host", self._h, a.ctypes.data_as(ctypes.c_void_p),
+             output.ctypes.data_as(ctypes.c_void_p), m, k, n)
+        return output
+
+    def to_float32_host(self) -> np.ndarray:
+        """IWeightTensor.ToFloat32 into host memory: [Rows][Cols] float32 (smx_weight_to_float32_host)."""
+        out = np.empty((self.rows, self.cols), np.float32)
+        call("smx_weight_to_float32_host", self._h, out.ctypes.data_as(ctypes.c_void_p))
+        return out
+
     def to_float32(self):
         """IWeightTensor.ToFloat32: [Rows][Cols] fp32 on the device."""
         torch = _torch()

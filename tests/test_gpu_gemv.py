@@ -151,3 +151,75 @@ def test_matmul_dimension_mismatch_raises(gpu):
     with pytest.raises(ValueError):
         w.mat_mul(x, y, 1, 256, 32)
     w.close()
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q8_0", "Q6_K"])
+def test_host_memory_matmul_matches_oracle_and_device_api(gpu, name):
+    """IWeightTensor.MatMul with the reference's host operands (smx_weight_matmul_host): numpy
+    arrays in and out, m = 1 (GEMV) and m = 16 (matrix-core GEMM) against the oracle's float64
+    GEMV; a run of calls with growing and shrinking m (the staging and the GEMM scratch are kept
+    per weight and grow) gives the device entry point's bits; ToFloat32 into host memory is the
+    oracle's dequantization bit for bit."""
+    import torch
+
+    from smallmind_amd.quantization import GpuWeightTensor
+    qt = TYPES[name]
+    N, K = 384, 2048
+    W = quantized(qt, (N, K), seed=91)
+    w = GpuWeightTensor(qt, N, K, W)
+    rng = np.random.default_rng(5)
+    for m in (1, 16, 40, 4, 16, 2):
+        x = rng.normal(0, 1, (m, K)).astype(np.float32)
+        y = w.mat_mul_host(x, m, K, N)
+        yd = torch.empty((m, N), dtype=torch.float32, device="cuda")
+        w.mat_mul(_dev(x), yd, m, K, N)
+        torch.cuda.synchronize()
+        assert np.array_equal(y, yd.cpu().numpy()), m
+        if m in (1, 16):
+            for r in range(m):
+                assert rel_err(y[r], O.gemv_f64(qt, W, N, K, x[r])) <= TIGHT, (m, r)
+    assert np.array_equal(w.to_float32_host().reshape(-1), O.dequant(qt, W, N * K))
+    with pytest.raises(Exception):
+        w.mat_mul_host(np.zeros((2, K + 32), np.float32), 2, K + 32, N)   # k != Cols
+    w.close()
+
+
+def test_weight_scratch_reuse_across_streams_and_threads(gpu):
+    """The GEMM scratch of one weight serves calls on two streams from two threads: each call
+    waits for the previous use, so every product is right."""
+    import threading
+
+    import torch
+
+    from smallmind_amd.quantization import GpuWeightTensor
+    qt, N, K, m = O.Q4_K, 256, 4096, 24
+    W = quantized(qt, (N, K), seed=17)
+    w = GpuWeightTensor(qt, N, K, W)
+    xs = [np.random.default_rng(i).normal(0, 1, (m, K)).astype(np.float32) for i in range(2)]
+    refs = [np.stack([O.gemv_f64(qt, W, N, K, x[r]) for r in range(m)]) for x in xs]
+    errors = []
+
+    def run(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                xd = _dev(xs[i])
+                out = torch.empty((m, N), dtype=torch.float32, device="cuda")
+                for _ in range(20):
+                    w.mat_mul(xd, out, m, K, N)
+                s.synchronize()
+                if rel_err(out.cpu().numpy(), refs[i]) > TIGHT:
+                    errors.append(i)
+            for _ in range(5):
+                if rel_err(w.mat_mul_host(xs[i], m, K, N), refs[i]) > TIGHT:
+                    errors.append(10 + i)
+        except Exception as e:   # noqa: BLE001
+            errors.append(e)
+
+    ts = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors, errors
+    w.close()
