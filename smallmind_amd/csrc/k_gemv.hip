@@ -414,6 +414,8 @@ template <int R, int S, int C, int PRO, int EC, int STG>
 hipError_t launch_v(const GemvArgs &a, int m, hipStream_t s)
 {
     constexpr int F = SMX_GEMV_FMT;
+    // a staged launch runs one round of 64*S*C chunks: it must cover the row
+    if (STG && a.w.cols > (int64_t)64 * S * C * 32) return hipErrorInvalidValue;
     const int64_t groups = (a.w.rows + R - 1) / R;
     const dim3 grid((unsigned)((groups + (4 / S) - 1) / (4 / S)), (unsigned)m);
     const size_t lds = STG ? (size_t)a.w.cols * 4 : 0;
@@ -431,8 +433,8 @@ hipError_t launch_v(const GemvArgs &a, int m, hipStream_t s)
     return hipGetLastError();
 }
 
-// Shape selection: S waves split K so that one round covers it (up to 4 waves x 64 lanes x C
-// chunks); R = 4 rows per wave for tall matrices with short rows, else 2.  The activation
+// Shape selection (gemv_shape): S waves split K so that one round covers it (up to 4 waves x 64
+// lanes x C chunks); R = 2 or 4 rows per wave.  The activation
 // vector is staged in LDS (up to 8192 floats with a fused norm, 16384 without).
 template <int PRO, int EC>
 hipError_t launch_pe(const GemvArgs &a, int m, hipStream_t s)
@@ -446,21 +448,33 @@ hipError_t launch_pe(const GemvArgs &a, int m, hipStream_t s)
             case GS_R4S1: return launch_v<4, 1, 1, PRO, EC, 3>(a, m, s);
             case GS_R2S1: return launch_v<2, 1, 1, PRO, EC, 3>(a, m, s);
             case GS_R2S2: return launch_v<2, 2, 1, PRO, EC, 3>(a, m, s);
+            case GS_R4S2: return launch_v<4, 2, 1, PRO, EC, 3>(a, m, s);
+            case GS_R2S1C3: return launch_v<2, 1, 3, PRO, EC, 3>(a, m, s);
+            case GS_R4S4: return launch_v<4, 4, 1, PRO, EC, 3>(a, m, s);
             default: return launch_v<2, 4, 1, PRO, EC, 3>(a, m, s);
             }
         }
     }
     switch (gemv_shape(a.w.rows, K)) {
     case GS_WIDE:
-        if constexpr (PRO == PRO_NONE && EC == EC_SIMPLE) {
-            if (K <= 16384) return launch_v<2, 4, 2, PRO, EC, 2>(a, m, s);
-            return launch_v<2, 4, 2, PRO, EC, 0>(a, m, s);
+    case GS_R4S2C3:
+    case GS_R4S2C4:
+        if constexpr (PRO == PRO_NONE && EC == EC_SIMPLE) {   // K > 8192: no fused norm
+            if (K > 16384) return launch_v<2, 4, 2, PRO, EC, 0>(a, m, s);
+            switch (gemv_shape(a.w.rows, K)) {
+            case GS_R4S2C3: return launch_v<4, 2, 3, PRO, EC, 2>(a, m, s);
+            case GS_R4S2C4: return launch_v<4, 2, 4, PRO, EC, 2>(a, m, s);
+            default: return launch_v<2, 4, 2, PRO, EC, 2>(a, m, s);
+            }
         }
         return hipErrorInvalidValue;
     case GS_R4S1: return launch_v<4, 1, 1, PRO, EC, 1>(a, m, s);
     case GS_R2S1: return launch_v<2, 1, 1, PRO, EC, 1>(a, m, s);
     case GS_R2S2: return launch_v<2, 2, 1, PRO, EC, 1>(a, m, s);
-    default: return launch_v<2, 4, 1, PRO, EC, 1>(a, m, s);   // nch <= 256
+    case GS_R4S2: return launch_v<4, 2, 1, PRO, EC, 1>(a, m, s);
+    case GS_R2S1C3: return launch_v<2, 1, 3, PRO, EC, 1>(a, m, s);
+    case GS_R4S4: return launch_v<4, 4, 1, PRO, EC, 1>(a, m, s);
+    default: return launch_v<2, 4, 1, PRO, EC, 1>(a, m, s);   // GS_R2S4: nch <= 256
     }
 }
 

@@ -522,6 +522,46 @@ __global__ void k_gelu(const float *__restrict__ x, float *__restrict__ y, int64
     if (i < n) y[i] = gelu_pade(x[i]);
 }
 
+// Thread-local argmax scan of x[tid], x[tid + T], ... in batches of U loads issued before any
+// compare (one memory round trip per batch instead of one per element).  Indices ascend within
+// a thread, so `>` keeps the lowest index of equal values.
+template <int U>
+__device__ __forceinline__ void argmax_scan(const float *__restrict__ x, int n, int tid, int T, float &best, int &idx)
+{
+    for (int base = tid; base < n; base += U * T) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = base + u * T;
+            v[u] = i < n ? x[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (v[u] > best) { best = v[u]; idx = base + u * T; }
+    }
+}
+
+// The same over (value, index) pairs: (v, i) wins over (best, idx) when larger, or equal with a
+// lower index.
+template <int U>
+__device__ __forceinline__ void argmax_scan_pairs(const float *__restrict__ val, const int32_t *__restrict__ ix,
+                                                  int n, int tid, int T, float &best, int &idx)
+{
+    for (int base = tid; base < n; base += U * T) {
+        float v[U];
+        int k[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = base + u * T;
+            v[u] = i < n ? val[i] : -INFINITY;
+            k[u] = i < n ? ix[i] : 0x7FFFFFFF;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (v[u] > best || (v[u] == best && k[u] < idx)) { best = v[u]; idx = k[u]; }
+    }
+}
+
 // Argmax with the lowest index on ties.  With `tokens`/`pos` set it also appends the token to
 // the device token array and advances the device position (end of a decode step).
 __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ x, int n,
@@ -533,10 +573,7 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ x, in
     __shared__ int bi[16];
     float best = -INFINITY;
     int idx = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = x[i];
-        if (v > best) { best = v; idx = i; }   // strided ascending scan: keeps the lowest index
-    }
+    argmax_scan<16>(x, n, threadIdx.x, blockDim.x, best, idx);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(best, o, 64);
@@ -574,11 +611,7 @@ __global__ __launch_bounds__(256) void k_argmax_pairs(const float *__restrict__ 
     __shared__ int bi[4];
     float best = -INFINITY;
     int bidx = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < n; i += 256) {
-        const float v = val[i];
-        const int ix = idx[i];
-        if (v > best || (v == best && ix < bidx)) { best = v; bidx = ix; }
-    }
+    argmax_scan_pairs<16>(val, idx, n, threadIdx.x, 256, best, bidx);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(best, o, 64);
@@ -672,11 +705,7 @@ __global__ __launch_bounds__(kThreads) void k_argmax_embed(const float *__restri
     if (threadIdx.x == 0) p = *pos;
     float best = -INFINITY;
     int bidx = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < n; i += kThreads) {
-        const float v = val[i];
-        const int ix = idx[i];
-        if (v > best || (v == best && ix < bidx)) { best = v; bidx = ix; }
-    }
+    argmax_scan_pairs<16>(val, idx, n, threadIdx.x, kThreads, best, bidx);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(best, o, 64);
@@ -770,10 +799,7 @@ __global__ __launch_bounds__(1024) void k_argmax_rows(const float *__restrict__ 
     const float *xr = x + (int64_t)blockIdx.x * stride;
     float best = -INFINITY;
     int idx = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = xr[i];
-        if (v > best) { best = v; idx = i; }
-    }
+    argmax_scan<16>(xr, n, threadIdx.x, blockDim.x, best, idx);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(best, o, 64);

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <stdlib.h>
+
 #include <string>
 
 #include "../../include/smx.h"
@@ -110,17 +112,32 @@ struct GemvArgs {
 hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s);
 
 // Launch shape of the fused GEMV for a [rows][cols] matrix: R rows per wave, S waves per row
-// group, 4/S row groups per 4-wave workgroup (workgroup b owns rows [b*n, (b+1)*n), n = R*4/S).
-enum GemvShape { GS_R4S1, GS_R2S1, GS_R2S2, GS_R2S4, GS_WIDE };
+// group splitting K, C chunks of 32 elements per lane, 4/S row groups per 4-wave workgroup
+// (workgroup b owns rows [b*n, (b+1)*n), n = R*4/S).  One round of 64*S*C chunks covers the
+// whole row for the staged launches.
+enum GemvShape {
+    GS_R4S1, GS_R2S1, GS_R2S2, GS_R4S2, GS_R2S4,   // C = 1
+    GS_R2S1C3,                                     // K <= 6144: whole rows per wave
+    GS_R4S4,                                       // K <= 8192
+    GS_R4S2C3, GS_R4S2C4,                          // K <= 12288 / 16384 (plain GEMVs)
+    GS_WIDE                                        // R=2, S=4, C=2 (plain GEMVs, few rows)
+};
+// Every workgroup stages the whole activation vector (K floats), so the longer the rows, the
+// more rows one staged copy should serve; short matrices keep more, smaller workgroups in
+// flight.  Measured on MI355X (graph-timed, weights from HBM): 2048 x 5632 Q8_0 5.20 us with two
+// rows per workgroup (R2S4), 4.75 us with eight (R2S1C3); 2048 x 8192 Q5_K 6.05 us (R2S4), 5.53
+// (R4S4), 6.50 (R2S1C4); 4096 x 11008 Q4_0 12.1 us (R2S4C2), 9.2 us (R4S2C3).
 inline GemvShape gemv_shape(int64_t rows, int64_t cols)
 {
     const int64_t nch = cols / 32;
-    if (cols > 8192) return GS_WIDE;                     // R=2, S=4 (plain GEMVs only)
     if (nch <= 64) return rows >= 8192 ? GS_R4S1 : GS_R2S1;
-    if (nch <= 128) return GS_R2S2;
-    return GS_R2S4;                                      // nch <= 256
+    if (nch <= 128) return rows >= 4096 ? GS_R4S2 : GS_R2S2;
+    if (rows < 1024) return nch <= 256 ? GS_R2S4 : GS_WIDE;
+    if (nch <= 192) return GS_R2S1C3;
+    if (nch <= 256) return GS_R4S4;
+    if (nch <= 384) return GS_R4S2C3;
+    return nch <= 512 ? GS_R4S2C4 : GS_WIDE;
 }
-
 
 // ---- quantized GEMM on the matrix cores for M activation rows (tokens) ------------------------
 // y[M][rows] = norm(x)[M][cols] W^T with the GEMV's prologues and epilogues applied per token.

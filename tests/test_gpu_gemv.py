@@ -32,7 +32,8 @@ def _gemv(qt, blocks, N, K, x, m=1):
     return y
 
 
-SHAPES = [(2, 256), (48, 512), (2560, 2048), (2048, 5632), (1000, 768), (3, 3072)]
+SHAPES = [(2, 256), (48, 512), (2560, 2048), (2048, 5632), (1000, 768), (3, 3072), (1030, 8192), (1024, 11008),
+          (700, 8192), (1100, 6144), (1024, 16384)]
 
 
 @pytest.mark.parametrize("name", list(TYPES))
