@@ -47,7 +47,14 @@ enum smx_type {
     SMX_TYPE_Q8_0 = 8,
     SMX_TYPE_Q4_K = 12,
     SMX_TYPE_Q5_K = 13,
-    SMX_TYPE_Q6_K = 14
+    SMX_TYPE_Q6_K = 14,
+    /* SmallMind's own SMQ blocks (Q8Tensor / Q4Tensor, src/SmallMind.Quantization/Tensors/Q8Tensor.cs,
+     * Q4Tensor.cs): 1000 + the SMQ QuantScheme id (QuantScheme.cs: Q8_0 = 10, Q4_0 = 11).  As
+     * upload bytes they are laid out in 32-element blocks, each the fp32 scale of the SMQ block
+     * holding those elements followed by the codes (32 int8 / 16 bytes of two's-complement nibbles,
+     * element 2i in the low nibble) -- see smx_smq_pack. */
+    SMX_TYPE_SMQ_Q8 = 1010,
+    SMX_TYPE_SMQ_Q4 = 1011
 };
 
 /* ---- library ----------------------------------------------------------------------------- */
@@ -234,6 +241,31 @@ SMX_API int smx_model_load_gguf(smx_context *ctx, const char *path, smx_model **
 /* Parses a GGUF file's header, metadata and tensor table and returns the derived
  * configuration and the tensor count; no device work. */
 SMX_API int smx_gguf_read_config(const char *path, smx_model_config *cfg, int64_t *n_tensors);
+/* Loads a SmallMind .smq file (SmqModelLoader.LoadFromSmq, src/SmallMind.Runtime/SmqModelLoader.cs:
+ * 29-100, reading through SmqReader, src/SmallMind.Quantization/IO/Smq/SmqReader.cs:33-293) into
+ * SmallMind's GPT-2 style TransformerModel.  cfg (arch must be SMX_ARCH_GPT2) plays the role of the
+ * reference's ModelConfig argument; NULL takes the configuration from the file's metadata
+ * (vocab_size, block_size, embed_dim, num_layers, num_heads; d_ff = 4 * embed_dim).  Tensors are
+ * matched by TransformerModel.GetNamedParameters names (TransformerModel.cs:545-728); a file
+ * none of whose tensor names is a parameter name (the param_NNNN / tensor_NNN files of the
+ * quantize command, QuantizeCommand.cs:63-97) is matched by parameter order.  Q8_0 / Q4_0 weight
+ * matrices stay quantized on the device (SMX_TYPE_SMQ_Q8 / _Q4, the file's fp32 scales
+ * unchanged); norm weights and biases are dequantized as SmqModelLoader.DequantizeTensor does
+ * (SmqModelLoader.cs:320-360).  SMX_EINVAL for a malformed file, SMX_EUNSUPPORTED for F16
+ * entries, other data types, or matrices whose columns or block size are not multiples of 32. */
+SMX_API int smx_model_load_smq(smx_context *ctx, const char *path, const smx_model_config *cfg,
+                               smx_model **out);
+/* Parses an .smq file's header, metadata and tensor directory and returns the configuration its
+ * metadata describes and the tensor count; no device work. */
+SMX_API int smx_smq_read_config(const char *path, smx_model_config *cfg, int64_t *n_tensors);
+/* Re-lays one rank-2 Q8Tensor / Q4Tensor (codes `data` as stored in the .smq file: rows * cols
+ * int8, or (rows * cols + 1) / 2 nibble bytes; `scales`: one fp32 per block_size consecutive
+ * elements of the flattened tensor; Q8Tensor.cs:17-60, Q4Tensor.cs:17-62) into the upload layout
+ * of SMX_TYPE_SMQ_Q8 / _Q4: per 32 elements, the scale of their block then their codes.  No
+ * value changes.  cols and block_size must be multiples of 32; out_bytes must equal
+ * rows * cols / 32 * (36 for Q8, 20 for Q4).  Host memory only. */
+SMX_API int smx_smq_pack(int type, const void *data, const float *scales, int64_t rows, int64_t cols,
+                         int block_size, void *out, size_t out_bytes);
 SMX_API int smx_model_weight_bytes(const smx_model *m, int64_t *bytes);
 SMX_API int smx_model_destroy(smx_model *m);
 

@@ -16,10 +16,11 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 8, 12, 13, 14
+SMQ_Q8, SMQ_Q4 = 1010, 1011   # SMQ Q8Tensor / Q4Tensor blocks re-laid per 32 (fp32 scale + codes)
 ARCH_LLAMA, ARCH_GPT2 = 0, 1
 
-BLOCK_ELEMS = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
-BLOCK_BYTES = {F32: 4, F16: 2, Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+BLOCK_ELEMS = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, SMQ_Q8: 32, SMQ_Q4: 32}
+BLOCK_BYTES = {F32: 4, F16: 2, Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, SMQ_Q8: 36, SMQ_Q4: 20}
 
 
 def build(force: bool = False) -> str:
@@ -48,6 +49,7 @@ def lib():
         L.smxo_quantize.argtypes = [ctypes.c_int, vp, ctypes.c_int64, vp]
         L.smxo_quantize_ref_q8.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
         L.smxo_quantize_ref_q4.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
+        L.smxo_dequant_smq.argtypes = [ctypes.c_int, vp, vp, ctypes.c_int64, ctypes.c_int, vp]
         L.smxo_gemv_f64.argtypes = [ctypes.c_int, vp, ctypes.c_int, ctypes.c_int, vp, vp]
         L.smxo_rmsnorm.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_float]
         L.smxo_layernorm.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_float]
@@ -135,6 +137,16 @@ def quantize_ref_q4(x: np.ndarray, block: int = 64):
     s = np.zeros((x.size + block - 1) // block, np.float32)
     lib().smxo_quantize_ref_q4(_p(x), x.size, block, _p(d), _p(s))
     return d, s
+
+
+def dequant_smq(scheme: int, data: np.ndarray, scales: np.ndarray, n: int, block: int) -> np.ndarray:
+    """Q8Tensor.Dequantize (scheme 10) / Q4Tensor.Dequantize (scheme 11) of n flattened elements."""
+    d = np.ascontiguousarray(data).view(np.uint8)
+    sc = np.ascontiguousarray(scales, dtype=np.float32)
+    out = np.empty(n, np.float32)
+    if lib().smxo_dequant_smq(scheme, _p(d), _p(sc), n, block, _p(out)):
+        raise ValueError("dequant_smq failed")
+    return out
 
 
 def gemv_f64(qtype: int, W: np.ndarray, N: int, K: int, x: np.ndarray) -> np.ndarray:

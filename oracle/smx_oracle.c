@@ -17,6 +17,12 @@
  *                           :145-155); random bytes vs committed golden vectors
  *   smxo_quantize           round-trip error bounds, half-even ties, known small cases
  *   smxo_quantize_ref_q8/q4 hand-computed cases from the Quantize formulas
+ *   smxo_dequant_smq        hand cases (nibble order, two's complement, short last block);
+ *                           the reference's benchmark-model.smq: every Q8 block's max |code|
+ *                           is 127 (or all zero with scale 1), LayerNorm gammas decode to 1.0
+ *                           and biases to 0.0 (tests/test_smq.py)
+ *   SMQ upload blocks       smx_smq_pack's layout decoded equals smxo_dequant_smq of the
+ *   (types 1010 / 1011)     original flattened tensor
  *   smxo_gemv_f64           numpy float64 matmul on the dequantized matrix
  *   smxo_rmsnorm/layernorm  the reference's closed-form tests (RMSNormOpsTests.cs:145-163,
  *                           LayerNormOpsTests.cs:206-229) and numpy float64
@@ -114,7 +120,7 @@ int smxo_block_elems(int type)
 {
     switch (type) {
     case SMXO_F32: case SMXO_F16: return 1;
-    case SMXO_Q4_0: case SMXO_Q8_0: return 32;
+    case SMXO_Q4_0: case SMXO_Q8_0: case SMXO_SMQ_Q8: case SMXO_SMQ_Q4: return 32;
     case SMXO_Q4_K: case SMXO_Q5_K: case SMXO_Q6_K: return 256;
     default: return 0;
     }
@@ -130,6 +136,8 @@ int smxo_block_bytes(int type)
     case SMXO_Q4_K: return 144;  /* d, dmin, 12 B scales, 128 B qs (Q4KTensor / KQuantTensorTests.cs:27) */
     case SMXO_Q5_K: return 176;  /* d, dmin, 12 B scales, 32 B qh, 128 B ql (GgufModelLoader.cs:836) */
     case SMXO_Q6_K: return 210;  /* 128 B ql, 64 B qh, 16 B int8 scales, fp16 d (KQuantTensorTests.cs:153) */
+    case SMXO_SMQ_Q8: return 36; /* fp32 scale of the SMQ block + 32 int8 (upload layout) */
+    case SMXO_SMQ_Q4: return 20; /* fp32 scale of the SMQ block + 16 B nibbles */
     default: return 0;
     }
 }
@@ -262,6 +270,29 @@ static void dq_q6_k(const uint8_t *b, float *y, int n)
     }
 }
 
+/* Q8Tensor.Dequantize / Q4Tensor.Dequantize (Q8Tensor.cs:131-157, Q4Tensor.cs:150-176): element
+ * i of the flattened tensor is code(i) * scales[i / block], one fp32 multiply; Q4 element i is
+ * the low (i even) or high (i odd) nibble of byte i / 2, two's complement. */
+int smxo_dequant_smq(int scheme, const uint8_t *data, const float *scales, int64_t n, int block, float *dst)
+{
+    if ((scheme != 10 && scheme != 11) || block <= 0 || n < 0) return -1;
+    for (int64_t i = 0; i < n; i++) {
+        int q;
+        if (scheme == 10) q = (int8_t)data[i];
+        else q = smxo_decode_nibble((i % 2 == 0) ? (data[i / 2] & 0xF) : ((data[i / 2] >> 4) & 0xF));
+        dst[i] = (float)q * scales[i / block];
+    }
+    return 0;
+}
+
+/* The 32-element upload layout of SMQ blocks: fp32 scale, then the codes as in the file. */
+static void dq_smq32(int type, const uint8_t *b, float *y, int n)
+{
+    float scale;
+    memcpy(&scale, b, 4);
+    smxo_dequant_smq(type == SMXO_SMQ_Q8 ? 10 : 11, b + 4, &scale, n, 32, y);
+}
+
 int smxo_dequant(int type, const uint8_t *src, int64_t n, float *dst)
 {
     int be = smxo_block_elems(type), bb = smxo_block_bytes(type);
@@ -282,6 +313,7 @@ int smxo_dequant(int type, const uint8_t *src, int64_t n, float *dst)
         case SMXO_Q4_K: dq_q4_k(b, y, cnt); break;
         case SMXO_Q5_K: dq_q5_k(b, y, cnt); break;
         case SMXO_Q6_K: dq_q6_k(b, y, cnt); break;
+        case SMXO_SMQ_Q8: case SMXO_SMQ_Q4: dq_smq32(type, b, y, cnt); break;
         default: return -1;
         }
     }
@@ -492,6 +524,13 @@ int smxo_quantize(int type, const float *src, int64_t n, uint8_t *dst)
         case SMXO_Q4_K: q_q4_k(x, b); break;
         case SMXO_Q5_K: q_q5_k(x, b); break;
         case SMXO_Q6_K: q_q6_k(x, b); break;
+        case SMXO_SMQ_Q8: case SMXO_SMQ_Q4: {   /* the reference quantizer at block 32 */
+            float scale;
+            if (type == SMXO_SMQ_Q8) smxo_quantize_ref_q8(x, 32, 32, (int8_t *)(b + 4), &scale);
+            else smxo_quantize_ref_q4(x, 32, 32, b + 4, &scale);
+            memcpy(b, &scale, 4);
+            break;
+        }
         default: return -1;
         }
     }

@@ -24,7 +24,9 @@ extern "C" {
 /* GGUF tensor type ids (GgufTensorType.cs:6-52). */
 enum {
     SMXO_F32 = 0, SMXO_F16 = 1, SMXO_Q4_0 = 2, SMXO_Q8_0 = 8,
-    SMXO_Q4_K = 12, SMXO_Q5_K = 13, SMXO_Q6_K = 14
+    SMXO_Q4_K = 12, SMXO_Q5_K = 13, SMXO_Q6_K = 14,
+    /* SMQ Q8Tensor / Q4Tensor blocks re-laid per 32 elements: fp32 scale + codes */
+    SMXO_SMQ_Q8 = 1010, SMXO_SMQ_Q4 = 1011
 };
 
 /* ---- block formats ------------------------------------------------------------------ */
@@ -46,6 +48,10 @@ int smxo_quantize(int type, const float *src, int64_t n, uint8_t *dst);
 void smxo_quantize_ref_q8(const float *src, int n, int block, int8_t *q, float *scales);
 void smxo_quantize_ref_q4(const float *src, int n, int block, uint8_t *data, float *scales);
 int  smxo_decode_nibble(int nibble);        /* Q4Tensor.cs:140-143 */
+/* Q8Tensor.Dequantize (scheme 10) / Q4Tensor.Dequantize (scheme 11) of a flattened SMQ tensor:
+ * n elements, one fp32 scale per `block` consecutive elements.  0 = ok. */
+int  smxo_dequant_smq(int scheme, const uint8_t *data, const float *scales, int64_t n, int block,
+                      float *dst);
 
 /* y[n] = sum_k dequant(W)[n][k] * x[k], accumulated in double. W is [N][K] GGUF rows. */
 int smxo_gemv_f64(int type, const uint8_t *W, int N, int K, const float *x, double *y);

@@ -29,7 +29,8 @@ EXPORTS = [
     "smx_context_create", "smx_context_destroy", "smx_model_create", "smx_model_upload_tensor",
     "smx_model_finalize", "smx_model_weight_bytes", "smx_model_destroy", "smx_session_create",
     "smx_session_forward", "smx_session_generate", "smx_batch_generate", "smx_session_reset",
-    "smx_session_destroy", "smx_model_load_gguf", "smx_gguf_read_config", "smx_sample",
+    "smx_session_destroy", "smx_model_load_gguf", "smx_gguf_read_config", "smx_model_load_smq",
+    "smx_smq_read_config", "smx_smq_pack", "smx_sample",
     "smx_session_generate_sampled", "smx_batcher_create", "smx_batcher_add", "smx_batcher_add_sampled", "smx_batcher_remove",
     "smx_batcher_count", "smx_batcher_step", "smx_batcher_destroy",
 ]
@@ -119,6 +120,9 @@ def load() -> ctypes.CDLL:
         "smx_model_finalize": (i32, [vp]),
         "smx_model_load_gguf": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(vp)]),
         "smx_gguf_read_config": (i32, [ctypes.c_char_p, ctypes.POINTER(ModelConfigC), ctypes.POINTER(ctypes.c_int64)]),
+        "smx_model_load_smq": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(ModelConfigC), ctypes.POINTER(vp)]),
+        "smx_smq_read_config": (i32, [ctypes.c_char_p, ctypes.POINTER(ModelConfigC), ctypes.POINTER(ctypes.c_int64)]),
+        "smx_smq_pack": (i32, [i32, vp, vp, i64, i64, i32, vp, ctypes.c_size_t]),
         "smx_model_weight_bytes": (i32, [vp, ctypes.POINTER(i64)]),
         "smx_model_destroy": (i32, [vp]),
         "smx_session_create": (i32, [vp, i32, pp]),

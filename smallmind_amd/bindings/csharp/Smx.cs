@@ -19,6 +19,8 @@ namespace SmallMind.Backends.Rocm
         public const int OK = 0, EINVAL = -1, ENOMEM = -2, EDEVICE = -3, EBUSY = -4,
                          EUNSUPPORTED = -5, ESTATE = -6, ERANGE = -7;
         public const int F32 = 0, F16 = 1, Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14;
+        // SMQ Q8Tensor / Q4Tensor blocks in their upload layout (smx_smq_pack)
+        public const int SMQ_Q8 = 1010, SMQ_Q4 = 1011;
 
         [StructLayout(LayoutKind.Sequential)]
         public struct ModelConfig            // smx_model_config; ModelConfig.cs:142-258
@@ -95,6 +97,13 @@ namespace SmallMind.Backends.Rocm
             [MarshalAs(UnmanagedType.LPUTF8Str)] string path, out IntPtr model);
         [DllImport(Lib)] public static extern int smx_gguf_read_config([MarshalAs(UnmanagedType.LPUTF8Str)] string path,
             out ModelConfig cfg, out long nTensors);
+        // cfg: the ModelConfig argument of SmqModelLoader.LoadFromSmq, or null for the file's metadata
+        [DllImport(Lib)] public static extern int smx_model_load_smq(IntPtr ctx,
+            [MarshalAs(UnmanagedType.LPUTF8Str)] string path, ModelConfig* cfg, out IntPtr model);
+        [DllImport(Lib)] public static extern int smx_smq_read_config([MarshalAs(UnmanagedType.LPUTF8Str)] string path,
+            out ModelConfig cfg, out long nTensors);
+        [DllImport(Lib)] public static extern int smx_smq_pack(int type, void* data, float* scales, long rows, long cols,
+            int blockSize, void* output, nuint outBytes);
         [DllImport(Lib)] public static extern int smx_model_weight_bytes(IntPtr model, out long bytes);
         [DllImport(Lib)] public static extern int smx_model_destroy(IntPtr model);
         [DllImport(Lib)] public static extern int smx_session_create(IntPtr model, int maxCtx, out IntPtr session);
@@ -222,7 +231,7 @@ namespace SmallMind.Backends.Rocm
         public void Dispose() => _session.Dispose();
     }
 
-    // The model on the device: loaded from a GGUF file in one call, or tensor by tensor.
+    // The model on the device: loaded from a GGUF or .smq file in one call, or tensor by tensor.
     internal sealed unsafe class GpuTransformerBackend : IDisposable
     {
         readonly IntPtr _ctx, _model;
@@ -230,7 +239,23 @@ namespace SmallMind.Backends.Rocm
         public GpuTransformerBackend(string ggufPath, int device = 0)
         {
             Smx.Check(Smx.smx_context_create(device, out _ctx));
-            Smx.Check(Smx.smx_model_load_gguf(_ctx, ggufPath, out _model));
+            int rc = Smx.smx_model_load_gguf(_ctx, ggufPath, out _model);
+            if (rc != 0) { Smx.smx_context_destroy(_ctx); Smx.Check(rc); }
+        }
+
+        GpuTransformerBackend(IntPtr ctx, IntPtr model) { _ctx = ctx; _model = model; }
+
+        // SmqModelLoader.LoadFromSmq(smqPath, config) (SmqModelLoader.cs:29-100): config null
+        // takes the GPT-2 configuration from the file's metadata.
+        public static GpuTransformerBackend FromSmq(string smqPath, Smx.ModelConfig? config = null, int device = 0)
+        {
+            Smx.Check(Smx.smx_context_create(device, out IntPtr ctx));
+            IntPtr model;
+            int rc;
+            if (config is Smx.ModelConfig c) rc = Smx.smx_model_load_smq(ctx, smqPath, &c, out model);
+            else rc = Smx.smx_model_load_smq(ctx, smqPath, null, out model);
+            if (rc != 0) { Smx.smx_context_destroy(ctx); Smx.Check(rc); }
+            return new GpuTransformerBackend(ctx, model);
         }
 
         public GpuSession CreateSession(int maxCtx) => new GpuSession(_model, maxCtx);

@@ -9,6 +9,10 @@ hipError_t launch_gemv_fmt1(const GemvArgs &a, int m, hipStream_t s);
 hipError_t launch_gemv_fmt2(const GemvArgs &a, int m, hipStream_t s);
 hipError_t launch_gemv_fmt3(const GemvArgs &a, int m, hipStream_t s);
 hipError_t launch_gemv_fmt4(const GemvArgs &a, int m, hipStream_t s);
+hipError_t launch_gemv_fmt5(const GemvArgs &a, int m, hipStream_t s);
+hipError_t launch_gemv_fmt6(const GemvArgs &a, int m, hipStream_t s);
+hipError_t launch_gemv_fmt7(const GemvArgs &a, int m, hipStream_t s);
+hipError_t launch_gemv_fmt8(const GemvArgs &a, int m, hipStream_t s);
 
 hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s)
 {
@@ -27,6 +31,10 @@ hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s)
     case FMT_Q4_K: return launch_gemv_fmt2(a, m, s);
     case FMT_Q5_K: return launch_gemv_fmt3(a, m, s);
     case FMT_Q6_K: return launch_gemv_fmt4(a, m, s);
+    case FMT_F16: return launch_gemv_fmt5(a, m, s);
+    case FMT_F32: return launch_gemv_fmt6(a, m, s);
+    case FMT_SQ8: return launch_gemv_fmt7(a, m, s);
+    case FMT_SQ4: return launch_gemv_fmt8(a, m, s);
     default: return hipErrorInvalidValue;
     }
 }

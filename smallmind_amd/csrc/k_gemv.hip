@@ -1,4 +1,5 @@
-// k_gemv.hip -- fused dequantize-GEMV for Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K weights.
+// k_gemv.hip -- fused dequantize-GEMV for Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K weights, SmallMind's
+// SMQ Q8 / Q4 blocks (fp32 scales) and unquantized F16 / F32 matrices.
 //
 // y[r] = sum_k W[r][k] * x[k] for a row-major [rows][cols] weight in the backend layout
 // (smx_internal.h).  Replaces Linear.ForwardFP32 / IWeightTensor.MatMul for batch-1 decode
@@ -461,10 +462,16 @@ hipError_t launch_pe(const GemvArgs &a, int m, hipStream_t s)
     case GS_R4S2C4:
         if constexpr (PRO == PRO_NONE && EC == EC_SIMPLE) {   // K > 8192: no fused norm
             if (K > 16384) return launch_v<2, 4, 2, PRO, EC, 0>(a, m, s);
-            switch (gemv_shape(a.w.rows, K)) {
-            case GS_R4S2C3: return launch_v<4, 2, 3, PRO, EC, 2>(a, m, s);
-            case GS_R4S2C4: return launch_v<4, 2, 4, PRO, EC, 2>(a, m, s);
-            default: return launch_v<2, 4, 2, PRO, EC, 2>(a, m, s);
+            // F32 chunks are 128 bytes: 4 rows x 3-4 chunks in flight would not fit the
+            // registers (the C = 4 instance spills 436 bytes per lane and returned wrong sums)
+            if constexpr (SMX_GEMV_FMT == FMT_F32) {
+                return launch_v<2, 4, 2, PRO, EC, 2>(a, m, s);
+            } else {
+                switch (gemv_shape(a.w.rows, K)) {
+                case GS_R4S2C3: return launch_v<4, 2, 3, PRO, EC, 2>(a, m, s);
+                case GS_R4S2C4: return launch_v<4, 2, 4, PRO, EC, 2>(a, m, s);
+                default: return launch_v<2, 4, 2, PRO, EC, 2>(a, m, s);
+                }
             }
         }
         return hipErrorInvalidValue;

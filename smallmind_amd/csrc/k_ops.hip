@@ -641,24 +641,33 @@ __global__ void k_advance(int32_t *pos)
     if (threadIdx.x == 0) *pos = *pos + 1;
 }
 
+// Chunk c of a row of any weight layout, dequantised exactly (decode_chunk_exact).
+__device__ __forceinline__ void decode_chunk_any(const WView &w, int64_t row, int c, float *y)
+{
+    switch (w.fmt) {
+    case FMT_Q4_0: decode_chunk_exact<FMT_Q4_0>(w, row, c, y); break;
+    case FMT_Q8_0: decode_chunk_exact<FMT_Q8_0>(w, row, c, y); break;
+    case FMT_Q4_K: decode_chunk_exact<FMT_Q4_K>(w, row, c, y); break;
+    case FMT_Q5_K: decode_chunk_exact<FMT_Q5_K>(w, row, c, y); break;
+    case FMT_Q6_K: decode_chunk_exact<FMT_Q6_K>(w, row, c, y); break;
+    case FMT_F16: decode_chunk_exact<FMT_F16>(w, row, c, y); break;
+    case FMT_F32: decode_chunk_exact<FMT_F32>(w, row, c, y); break;
+    case FMT_SQ8: decode_chunk_exact<FMT_SQ8>(w, row, c, y); break;
+    default: decode_chunk_exact<FMT_SQ4>(w, row, c, y); break;
+    }
+}
+
 // Embedding gather (NeuralNet.cs:376-391, row copies :576-592) with the row dequantised
 // exactly, plus the learned position row for GPT-2 (TransformerModel.cs:299-326).
-template <int F>
 __device__ void embed_row(const WView &w, int64_t row, float *y, const WView *pw, int64_t prow)
 {
     const int nch = (int)(w.cols / 32);
     for (int c = threadIdx.x; c < nch; c += blockDim.x) {
         float v[32];
-        decode_chunk_exact<F>(w, row, c, v);
+        decode_chunk_any(w, row, c, v);
         if (pw) {
             float p[32];
-            switch (pw->fmt) {
-            case FMT_Q4_0: decode_chunk_exact<FMT_Q4_0>(*pw, prow, c, p); break;
-            case FMT_Q8_0: decode_chunk_exact<FMT_Q8_0>(*pw, prow, c, p); break;
-            case FMT_Q4_K: decode_chunk_exact<FMT_Q4_K>(*pw, prow, c, p); break;
-            case FMT_Q5_K: decode_chunk_exact<FMT_Q5_K>(*pw, prow, c, p); break;
-            default: decode_chunk_exact<FMT_Q6_K>(*pw, prow, c, p); break;
-            }
+            decode_chunk_any(*pw, prow, c, p);
 #pragma unroll
             for (int i = 0; i < 32; i++) v[i] = v[i] + p[i];
         }
@@ -676,13 +685,7 @@ __global__ __launch_bounds__(kThreads) void k_embed(WView w, WView pw, int has_p
     int64_t tok = tokens[p];
     if (tok < 0 || tok >= w.rows) tok = 0;   // the host validates tokens; never read out of bounds
     const WView *pp = has_pos ? &pw : nullptr;
-    switch (w.fmt) {
-    case FMT_Q4_0: embed_row<FMT_Q4_0>(w, tok, x, pp, p); break;
-    case FMT_Q8_0: embed_row<FMT_Q8_0>(w, tok, x, pp, p); break;
-    case FMT_Q4_K: embed_row<FMT_Q4_K>(w, tok, x, pp, p); break;
-    case FMT_Q5_K: embed_row<FMT_Q5_K>(w, tok, x, pp, p); break;
-    default: embed_row<FMT_Q6_K>(w, tok, x, pp, p); break;
-    }
+    embed_row(w, tok, x, pp, p);
 }
 
 // End of a decode step with the next step's embedding folded in: argmax over the head's
@@ -734,13 +737,7 @@ __global__ __launch_bounds__(kThreads) void k_argmax_embed(const float *__restri
     // context it is never used)
     const int64_t prow = has_pos ? (p + 1 < pw.rows ? p + 1 : pw.rows - 1) : 0;
     const WView *pp = has_pos ? &pw : nullptr;
-    switch (w.fmt) {
-    case FMT_Q4_0: embed_row<FMT_Q4_0>(w, tok, x_next, pp, prow); break;
-    case FMT_Q8_0: embed_row<FMT_Q8_0>(w, tok, x_next, pp, prow); break;
-    case FMT_Q4_K: embed_row<FMT_Q4_K>(w, tok, x_next, pp, prow); break;
-    case FMT_Q5_K: embed_row<FMT_Q5_K>(w, tok, x_next, pp, prow); break;
-    default: embed_row<FMT_Q6_K>(w, tok, x_next, pp, prow); break;
-    }
+    embed_row(w, tok, x_next, pp, prow);
 }
 
 // Embedding rows of a token batch: x[t] = emb[tok[t]] (+ pos_emb[pos[t]]), one workgroup per
@@ -756,13 +753,7 @@ __global__ __launch_bounds__(kThreads) void k_embed_tokens(WView w, WView pw, in
     const int p = pos[t];
     float *xr = x + (int64_t)t * x_stride;
     const WView *pp = has_pos ? &pw : nullptr;
-    switch (w.fmt) {
-    case FMT_Q4_0: embed_row<FMT_Q4_0>(w, id, xr, pp, p); break;
-    case FMT_Q8_0: embed_row<FMT_Q8_0>(w, id, xr, pp, p); break;
-    case FMT_Q4_K: embed_row<FMT_Q4_K>(w, id, xr, pp, p); break;
-    case FMT_Q5_K: embed_row<FMT_Q5_K>(w, id, xr, pp, p); break;
-    default: embed_row<FMT_Q6_K>(w, id, xr, pp, p); break;
-    }
+    embed_row(w, id, xr, pp, p);
 }
 
 // Decode attention for a token batch: token t (its own position and KV cache) x head h.

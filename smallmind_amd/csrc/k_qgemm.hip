@@ -135,6 +135,39 @@ template <> struct QW<FMT_Q8_0> {
     __device__ __forceinline__ static Scl scale(const RawQ &r, int) { return {h2f(r.d), 0.0f, 0.0f}; }
 };
 
+// SMQ blocks (Q8Tensor / Q4Tensor): the Q8_0 / Q4_0 codes with an fp32 scale per 32 elements.
+template <> struct QW<FMT_SQ8> {
+    static constexpr float kOff = 128.0f;
+    static constexpr bool kHalves = false;
+    __device__ __forceinline__ static RawQ load(const WView &w, uint32_t row, int s, int g)
+    {
+        RawQ r{};
+        const uint32_t blk = row * (uint32_t)w.nb + (uint32_t)s;
+        const uint2 v = *(const uint2 *)(w.q + blk * 32u + 8u * g);
+        r.v = v.x;
+        r.v2 = v.y;
+        r.d = ((const uint32_t *)w.d)[blk];
+        return r;
+    }
+    __device__ __forceinline__ static uint4 codes(const RawQ &r, int g) { return QW<FMT_Q8_0>::codes(r, g); }
+    __device__ __forceinline__ static Scl scale(const RawQ &r, int) { return {__uint_as_float(r.d), 0.0f, 0.0f}; }
+};
+
+template <> struct QW<FMT_SQ4> {
+    static constexpr float kOff = 136.0f;
+    static constexpr bool kHalves = false;
+    __device__ __forceinline__ static RawQ load(const WView &w, uint32_t row, int s, int g)
+    {
+        RawQ r{};
+        const uint32_t blk = row * (uint32_t)w.nb + (uint32_t)s;
+        r.v = *(const uint32_t *)(w.q + blk * 16u + 4u * g);
+        r.d = ((const uint32_t *)w.d)[blk];
+        return r;
+    }
+    __device__ __forceinline__ static uint4 codes(const RawQ &r, int g) { return QW<FMT_Q4_0>::codes(r, g); }
+    __device__ __forceinline__ static Scl scale(const RawQ &r, int) { return {__uint_as_float(r.d), 0.0f, 0.0f}; }
+};
+
 // Q4_K: sub-block s = qs bytes 16 + 16*(s % 8) of super-block s / 8.
 template <> struct QW<FMT_Q4_K> {
     static constexpr float kOff = 128.0f;
@@ -453,6 +486,141 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm(QgemmArgs a)
         }
 }
 
+// ---- unquantized weights (F16 / F32) --------------------------------------------------------
+// The FP32 Linear on F16 / F32 matrices (NeuralNet.cs:233-298, F32WeightTensor.cs:9-60).  The
+// weights have no block scale to factor out, so they enter as bf16 parts of their own, exactly:
+// an fp16 value (11 significant bits) is hi + lo, an fp32 value hi + mid + lo (8 + 8 + 8), each
+// part a round-to-nearest-even bf16 of the remainder.  Every product of a weight part and an
+// activation part is exact in fp32; the MFMA sums them (6 products per element for F16, 9 for
+// F32).  Same operand layout, work split and epilogue as k_qgemm; no sum(x) term.
+template <int F> struct DW {
+    static constexpr int kParts = F == FMT_F16 ? 2 : 3;
+    // the 8 weights of (row, sub-block s, k-group g) as fp32, element order 0..7
+    __device__ __forceinline__ static void load(const WView &w, uint32_t row, int s, int g, float *v)
+    {
+        const uint8_t *p = w.q + ((size_t)row * (uint32_t)w.nb + (uint32_t)s) * fmt_main_bytes(F);
+        if constexpr (F == FMT_F16) {
+            const uint4 h = *(const uint4 *)(p + 16 * g);
+            const uint32_t u[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[2 * i] = h2f(u[i] & 0xFFFFu);
+                v[2 * i + 1] = h2f(u[i] >> 16);
+            }
+        } else {
+            const float4 a = *(const float4 *)(p + 32 * g), b = *(const float4 *)(p + 32 * g + 16);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        }
+    }
+    // bf16 parts in the operand order (pair q = element q, element q + 4)
+    __device__ __forceinline__ static void parts(const float *v, uint4 *o)
+    {
+        uint32_t pt[3][8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t h = bf16_rne(v[k]);
+            const float r1 = v[k] - __uint_as_float(h << 16);
+            const uint32_t m = bf16_rne(r1);
+            pt[0][k] = h;
+            pt[1][k] = m;
+            if constexpr (kParts == 3) pt[2][k] = bf16_rne(r1 - __uint_as_float(m << 16));
+        }
+#pragma unroll
+        for (int p = 0; p < kParts; p++)
+            o[p] = make_uint4(pt[p][0] | (pt[p][4] << 16), pt[p][1] | (pt[p][5] << 16), pt[p][2] | (pt[p][6] << 16),
+                              pt[p][3] | (pt[p][7] << 16));
+    }
+};
+
+template <int F, int RT, int TT, int NW, int SB>
+__global__ __launch_bounds__(64 * NW) void k_dgemm(QgemmArgs a)
+{
+    using D = DW<F>;
+    constexpr int NP = D::kParts;
+    const WView &w = a.w;
+    const uint8_t *__restrict__ xp = a.xp;
+    const int M = a.M;
+    __shared__ f32x4 s_part[NW - 1][RT * TT][64];
+    const int wv = wave_id();
+    const int lane = lane_id();
+    const int g = lane >> 4, li = lane & 15;
+    const uint32_t lane16 = (uint32_t)lane * 16u;
+    const uint32_t N = (uint32_t)w.rows;
+    const int nsb = (int)(w.cols >> 5);
+    const uint32_t row_base = blockIdx.x * (16 * RT);
+    const int tt0 = blockIdx.y * TT;
+    const int ntt = (M + 15) >> 4;
+
+    f32x4 acc[RT][TT];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int t = 0; t < TT; t++) acc[r][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t wrow[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        const uint32_t rr = row_base + 16 * r + li;
+        wrow[r] = rr < N ? rr : N - 1;
+    }
+
+    for (int s0 = wv; s0 < nsb; s0 += NW * SB) {
+        float wf[SB][RT][8];
+        uint4 xa[SB][TT][3];
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            const int s = s0 + u * NW < nsb ? s0 + u * NW : nsb - 1;
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                const int tt = tt0 + t < ntt ? tt0 + t : ntt - 1;
+#pragma unroll
+                for (int p = 0; p < 3; p++) xa[u][t][p] = ld_part(xp, tt, nsb, s, p, lane16);
+            }
+#pragma unroll
+            for (int r = 0; r < RT; r++) D::load(w, wrow[r], s, g, wf[u][r]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            if (s0 + u * NW >= nsb) break;   // wave-uniform: past the end of K
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                uint4 wp[NP];
+                D::parts(wf[u][r], wp);
+#pragma unroll
+                for (int t = 0; t < TT; t++)
+#pragma unroll
+                    for (int q = 0; q < NP; q++)
+#pragma unroll
+                        for (int p = 0; p < 3; p++) acc[r][t] = mfma(xa[u][t][p], wp[q], acc[r][t]);
+            }
+        }
+    }
+
+    if (wv > 0) {
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int t = 0; t < TT; t++) s_part[wv - 1][r * TT + t][lane] = acc[r][t];
+    }
+    __syncthreads();
+    if (wv != 0) return;
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            f32x4 v = acc[r][t];
+#pragma unroll
+            for (int k = 0; k < NW - 1; k++) {
+                const f32x4 o = s_part[k][r * TT + t][lane];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] += o[i];
+            }
+            const uint32_t row = row_base + 16 * r + li;
+#pragma unroll
+            for (int i = 0; i < 4; i++) qgemm_epilogue(a, v[i], row, (tt0 + t) * 16 + 4 * g + i, true);
+        }
+}
+
 // ---- LDS-staged variant --------------------------------------------------------------------
 // The lane-per-(row, k-group) operand layout makes direct weight loads touch 16 rows (16 cache
 // lines) per instruction for 4 useful bytes each.  Here every wave copies its weight tile --
@@ -460,12 +628,16 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm(QgemmArgs a)
 // loads (the next super-block's copy in flight while the current one is multiplied), and reads
 // the operand dwords from LDS.  RT row tiles per wave share each activation-part load.
 // Waves of a workgroup take contiguous super-block ranges of K.
+// kBytes: main-stream bytes per row and super-block; kDW: dwords of the d stream per row and
+// super-block (8 fp16 scales, one fp16 scale, or 8 fp32 scales).
 template <int F> struct Stage;
-template <> struct Stage<FMT_Q4_0> { static constexpr int kBytes = 128, kD = 8; };
-template <> struct Stage<FMT_Q8_0> { static constexpr int kBytes = 256, kD = 8; };
-template <> struct Stage<FMT_Q4_K> { static constexpr int kBytes = 144, kD = 0; };
-template <> struct Stage<FMT_Q5_K> { static constexpr int kBytes = 176, kD = 0; };
-template <> struct Stage<FMT_Q6_K> { static constexpr int kBytes = 208, kD = 1; };
+template <> struct Stage<FMT_Q4_0> { static constexpr int kBytes = 128, kDW = 4; };
+template <> struct Stage<FMT_Q8_0> { static constexpr int kBytes = 256, kDW = 4; };
+template <> struct Stage<FMT_Q4_K> { static constexpr int kBytes = 144, kDW = 0; };
+template <> struct Stage<FMT_Q5_K> { static constexpr int kBytes = 176, kDW = 0; };
+template <> struct Stage<FMT_Q6_K> { static constexpr int kBytes = 208, kDW = 1; };
+template <> struct Stage<FMT_SQ4> { static constexpr int kBytes = 128, kDW = 8; };
+template <> struct Stage<FMT_SQ8> { static constexpr int kBytes = 256, kDW = 8; };
 
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { return *(const uint32_t *)p; }
 
@@ -480,6 +652,13 @@ __device__ __forceinline__ RawQ stage_raw(const uint8_t *row, const uint32_t *dr
     if constexpr (F == FMT_Q4_0) {
         r.v = lds_u32(row + 16 * j + 4 * g);
         r.d = (dr[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+    } else if constexpr (F == FMT_SQ4) {
+        r.v = lds_u32(row + 16 * j + 4 * g);
+        r.d = dr[j];
+    } else if constexpr (F == FMT_SQ8) {
+        r.v = lds_u32(row + 32 * j + 8 * g);
+        r.v2 = lds_u32(row + 32 * j + 8 * g + 4);
+        r.d = dr[j];
     } else if constexpr (F == FMT_Q8_0) {
         r.v = lds_u32(row + 32 * j + 8 * g);
         r.v2 = lds_u32(row + 32 * j + 8 * g + 4);
@@ -511,7 +690,7 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
     constexpr int NPC = (R16 * G::kBytes / 16 + 63) / 64;   // 16-byte pieces per lane
     // dword accesses below: the byte array must be dword (here 16-byte) aligned
     __shared__ __align__(16) uint8_t s_w[NW][R16 * RS];
-    __shared__ __align__(16) uint32_t s_d[NW][R16][G::kD > 1 ? G::kD / 2 : 1];
+    __shared__ __align__(16) uint32_t s_d[NW][R16][G::kDW > 0 ? G::kDW : 1];
     __shared__ f32x4 s_part[NW - 1][RT * TT][64];
     const WView &w = a.w;
     const uint8_t *__restrict__ xp = a.xp;
@@ -571,7 +750,7 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
 
     // staging loads of one super-block: piece p -> (row p / (kBytes/16), 16-byte column)
     uint4 wp[NPC];
-    uint4 dp = kZero4;
+    uint4 dp = kZero4, dp2 = kZero4;
     auto issue = [&](int sup) {
 #pragma unroll
         for (int k = 0; k < NPC; k++) {
@@ -583,13 +762,21 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
                         ? *(const uint4 *)(w.q + gr * row_bytes + (uint32_t)sup * G::kBytes + 16u * col)
                         : kZero4;
         }
-        if constexpr (G::kD == 8) {
+        if constexpr (G::kDW == 4) {
             if (lane < R16) {
                 uint32_t gr = row_base + (uint32_t)lane;
                 gr = gr < N ? gr : N - 1;
                 dp = *(const uint4 *)(w.d + (gr * (uint32_t)nsb + (uint32_t)sup * 8));
             }
-        } else if constexpr (G::kD == 1) {
+        } else if constexpr (G::kDW == 8) {
+            if (lane < R16) {
+                uint32_t gr = row_base + (uint32_t)lane;
+                gr = gr < N ? gr : N - 1;
+                const uint4 *dq = (const uint4 *)((const uint32_t *)w.d + (gr * (uint32_t)nsb + (uint32_t)sup * 8));
+                dp = dq[0];
+                dp2 = dq[1];
+            }
+        } else if constexpr (G::kDW == 1) {
             if (lane < R16) {
                 uint32_t gr = row_base + (uint32_t)lane;
                 gr = gr < N ? gr : N - 1;
@@ -613,12 +800,13 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
                 o[3] = wp[k].w;
             }
         }
-        if constexpr (G::kD == 8) {
+        if constexpr (G::kDW == 4 || G::kDW == 8) {
             if (lane < R16) {
                 uint32_t *o = s_d[wv][lane];
                 o[0] = dp.x; o[1] = dp.y; o[2] = dp.z; o[3] = dp.w;
+                if constexpr (G::kDW == 8) { o[4] = dp2.x; o[5] = dp2.y; o[6] = dp2.z; o[7] = dp2.w; }
             }
-        } else if constexpr (G::kD == 1) {
+        } else if constexpr (G::kDW == 1) {
             if (lane < R16) s_d[wv][lane][0] = dp.x;
         }
         // keep every read of the staged tile below these stores
@@ -994,6 +1182,25 @@ hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
     return launch_frt<F, 1, 1, 16, 4>(a, s);
 }
 
+template <int F, int RT, int TT, int NW, int SB>
+hipError_t launch_drt(const QgemmArgs &a, hipStream_t s)
+{
+    const dim3 grid((unsigned)((a.w.rows + 16 * RT - 1) / (16 * RT)), (unsigned)(((a.M + 15) / 16 + TT - 1) / TT));
+    hipLaunchKernelGGL((k_dgemm<F, RT, TT, NW, SB>), grid, dim3(64 * NW), 0, s, a);
+    return hipGetLastError();
+}
+
+// F16 / F32 weights: the decomposition of the unstaged quantized kernel (4 token tiles per
+// workgroup above 16 tokens, else one tile and 16 waves splitting K).
+template <int F>
+hipError_t launch_d(const QgemmArgs &a, hipStream_t s)
+{
+    constexpr int SB = F == FMT_F32 ? 2 : 4;   // F32 with 4 in flight would spill at 128 registers
+    if (a.M > 16) return launch_drt<F, 1, 4, 4, 2>(a, s);
+    if (a.w.rows >= 16 * 2 * 512) return launch_drt<F, 2, 1, 16, SB>(a, s);
+    return launch_drt<F, 1, 1, 16, SB>(a, s);
+}
+
 }  // namespace
 
 size_t qgemm_xp_bytes(int M, int K) { return (size_t)((M + 15) / 16) * (K / 32) * 3 * 1024; }
@@ -1010,8 +1217,8 @@ hipError_t launch_qgemm(const QgemmArgs &a, const float *x, int64_t x_stride, in
     if ((!x && pro != PRO_NONE) || (a.yp && (a.epi == EPI_SILU ? a.w.rows % 64 : a.w.rows % 32)) ||
         (a.yp && a.epi != EPI_SILU && a.epi != EPI_GELU))
         return hipErrorInvalidValue;
-    // folded RMSNorm: one token tile on the staged path
-    if ((a.rss || a.np) && (a.M > 16 || K % 256 != 0)) return hipErrorInvalidValue;
+    // folded RMSNorm: one token tile on the staged path (block formats only)
+    if ((a.rss || a.np) && (a.M > 16 || K % 256 != 0 || fmt_dense(a.w.fmt))) return hipErrorInvalidValue;
     if (a.rss && (x || pro != PRO_NONE || a.rss_n < 1 || a.rss_n > 256)) return hipErrorInvalidValue;
     if (a.np && (a.epi != EPI_RESID || a.w.rows % 32 != 0 || !a.ngamma || !a.nss)) return hipErrorInvalidValue;
     const unsigned mp = (unsigned)((a.M + 15) / 16 * 16);
@@ -1032,9 +1239,13 @@ hipError_t launch_qgemm(const QgemmArgs &a, const float *x, int64_t x_stride, in
     switch (a.w.fmt) {
     case FMT_Q4_0: return launch_f<FMT_Q4_0>(a, s);
     case FMT_Q8_0: return launch_f<FMT_Q8_0>(a, s);
+    case FMT_SQ4: return launch_f<FMT_SQ4>(a, s);
+    case FMT_SQ8: return launch_f<FMT_SQ8>(a, s);
     case FMT_Q4_K: return launch_f<FMT_Q4_K>(a, s);
     case FMT_Q5_K: return launch_f<FMT_Q5_K>(a, s);
     case FMT_Q6_K: return launch_f<FMT_Q6_K>(a, s);
+    case FMT_F16: return launch_d<FMT_F16>(a, s);
+    case FMT_F32: return launch_d<FMT_F32>(a, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -48,6 +48,23 @@ __global__ void k_dequant_gguf(int type, const uint8_t *__restrict__ src, int64_
         for (int i = 0; i < cnt; i++) y[i] = f[i];
     } else if (type == SMX_TYPE_F16) {
         for (int i = 0; i < cnt; i++) y[i] = rd_half_exact(src + 2 * (e0 + i));
+    } else if (type == SMX_TYPE_SMQ_Q8 || type == SMX_TYPE_SMQ_Q4) {
+        // Q8Tensor.Dequantize / Q4Tensor.Dequantize (Q8Tensor.cs:131-157, Q4Tensor.cs:150-178):
+        // code * scale, one fp32 multiply; 32-element blocks of [fp32 scale | codes]
+        const bool q8 = type == SMX_TYPE_SMQ_Q8;
+        const uint8_t *b = src + chunk * (q8 ? 36 : 20);
+        const float d = __uint_as_float((uint32_t)b[0] | ((uint32_t)b[1] << 8) | ((uint32_t)b[2] << 16) |
+                                        ((uint32_t)b[3] << 24));
+        for (int i = 0; i < cnt; i++) {
+            int q;
+            if (q8) {
+                q = (int8_t)b[4 + i];
+            } else {
+                const uint32_t n = (b[4 + i / 2] >> (4 * (i & 1))) & 15u;
+                q = n < 8 ? (int)n : (int)n - 16;   // Q4Tensor.DecodeNibble (Q4Tensor.cs:140-143)
+            }
+            y[i] = (float)q * d;
+        }
     } else if (type == SMX_TYPE_Q8_0) {   // GgufModelLoader.cs:464-492
         const uint8_t *b = src + chunk * 34;
         const float d = rd_half_exact(b);
@@ -157,6 +174,36 @@ __device__ void enc_q4_0(const float *x, uint8_t *b)
     }
 }
 
+// Q8Tensor.Quantize / Q4Tensor.Quantize (Q8Tensor.cs:72-128, Q4Tensor.cs:75-134) as written, fp32
+// scale kept, at 32-element blocks: the SMQ upload layout (fp32 scale, then the codes).
+__device__ void enc_smq_q8(const float *x, uint8_t *b)
+{
+    float maxAbs = block_maxabs(x, 32);
+    float scale = maxAbs > 0.0f ? maxAbs / 127.0f : 1.0f;
+    float inv = 1.0f / scale;
+    const uint32_t u = __float_as_uint(scale);
+    for (int i = 0; i < 4; i++) b[i] = (uint8_t)(u >> (8 * i));
+    for (int i = 0; i < 32; i++) {
+        float t = x[i] * inv;
+        b[4 + i] = (uint8_t)(int8_t)(int)rintf(clampf(t, -127.0f, 127.0f));
+    }
+}
+
+__device__ void enc_smq_q4(const float *x, uint8_t *b)
+{
+    float maxAbs = block_maxabs(x, 32);
+    float scale = maxAbs > 0.0f ? maxAbs / 7.0f : 1.0f;
+    float inv = 1.0f / scale;
+    const uint32_t u = __float_as_uint(scale);
+    for (int i = 0; i < 4; i++) b[i] = (uint8_t)(u >> (8 * i));
+    for (int i = 0; i < 16; i++) {
+        float t0 = x[2 * i] * inv, t1 = x[2 * i + 1] * inv;
+        int c0 = (int)rintf(clampf(t0, -8.0f, 7.0f));
+        int c1 = (int)rintf(clampf(t1, -8.0f, 7.0f));
+        b[4 + i] = (uint8_t)((c0 & 0xF) | ((c1 & 0xF) << 4));
+    }
+}
+
 __device__ void enc_q4_k(const float *x, uint8_t *b)
 {
     float scl[8], mnv[8], maxs = 0.0f, maxm = 0.0f;
@@ -260,6 +307,8 @@ __global__ void k_quantize(int type, const float *__restrict__ x, int64_t nblock
     case SMX_TYPE_Q4_K: enc_q4_k(x + blk * 256, out + blk * 144); break;
     case SMX_TYPE_Q5_K: enc_q5_k(x + blk * 256, out + blk * 176); break;
     case SMX_TYPE_Q6_K: enc_q6_k(x + blk * 256, out + blk * 210); break;
+    case SMX_TYPE_SMQ_Q8: enc_smq_q8(x + blk * 32, out + blk * 36); break;
+    case SMX_TYPE_SMQ_Q4: enc_smq_q4(x + blk * 32, out + blk * 20); break;
     case SMX_TYPE_F16: {
         uint32_t h = f2h_rne(x[blk]);
         out[2 * blk] = (uint8_t)h;
@@ -304,7 +353,13 @@ __global__ void k_repack(int fmt, const uint8_t *__restrict__ src, int64_t rows,
     const int gb = fmt_gguf_bytes(fmt), mb = fmt_main_bytes(fmt);
     const uint8_t *s = src + idx * gb;
     uint8_t *o = dq + (dr * nb + b) * mb;
-    if (fmt == FMT_Q4_0 || fmt == FMT_Q8_0) {
+    if (fmt == FMT_F16 || fmt == FMT_F32) {
+        for (int i = 0; i < mb; i++) o[i] = s[i];
+    } else if (fmt == FMT_SQ8 || fmt == FMT_SQ4) {
+        ((uint32_t *)dd)[dr * nb + b] = (uint32_t)s[0] | ((uint32_t)s[1] << 8) | ((uint32_t)s[2] << 16) |
+                                        ((uint32_t)s[3] << 24);
+        for (int i = 0; i < mb; i++) o[i] = s[4 + i];
+    } else if (fmt == FMT_Q4_0 || fmt == FMT_Q8_0) {
         dd[dr * nb + b] = (uint16_t)ld_u16(s);
         for (int i = 0; i < mb; i++) o[i] = s[2 + i];
     } else if (fmt == FMT_Q4_K) {
@@ -368,6 +423,10 @@ int fmt_from_type(int type)
     case SMX_TYPE_Q4_K: return FMT_Q4_K;
     case SMX_TYPE_Q5_K: return FMT_Q5_K;
     case SMX_TYPE_Q6_K: return FMT_Q6_K;
+    case SMX_TYPE_F16: return FMT_F16;
+    case SMX_TYPE_F32: return FMT_F32;
+    case SMX_TYPE_SMQ_Q8: return FMT_SQ8;
+    case SMX_TYPE_SMQ_Q4: return FMT_SQ4;
     default: return -1;
     }
 }
@@ -383,7 +442,9 @@ hipError_t launch_dequant_gguf(int type, const void *blocks, int64_t n, float *o
 
 hipError_t launch_quantize_gguf(int type, const float *x, int64_t n, void *blocks, hipStream_t s)
 {
-    const int be = type == SMX_TYPE_F16 ? 1 : (type == SMX_TYPE_Q8_0 || type == SMX_TYPE_Q4_0 ? 32 : 256);
+    const int be = type == SMX_TYPE_F16 ? 1
+                 : (type == SMX_TYPE_Q8_0 || type == SMX_TYPE_Q4_0 || type == SMX_TYPE_SMQ_Q8 || type == SMX_TYPE_SMQ_Q4)
+                     ? 32 : 256;
     const int64_t nblocks = n / be;
     if (nblocks == 0) return hipSuccess;
     hipLaunchKernelGGL(k_quantize, dim3(grid_for(nblocks)), dim3(kThreads), 0, s, type, x, nblocks,
@@ -424,6 +485,10 @@ hipError_t launch_dequant_smx(const WView &w, int64_t row0, int64_t nrows, float
     case FMT_Q4_K: hipLaunchKernelGGL(k_dequant_smx<FMT_Q4_K>, g, b, 0, s, w, row0, nrows, out); break;
     case FMT_Q5_K: hipLaunchKernelGGL(k_dequant_smx<FMT_Q5_K>, g, b, 0, s, w, row0, nrows, out); break;
     case FMT_Q6_K: hipLaunchKernelGGL(k_dequant_smx<FMT_Q6_K>, g, b, 0, s, w, row0, nrows, out); break;
+    case FMT_F16: hipLaunchKernelGGL(k_dequant_smx<FMT_F16>, g, b, 0, s, w, row0, nrows, out); break;
+    case FMT_F32: hipLaunchKernelGGL(k_dequant_smx<FMT_F32>, g, b, 0, s, w, row0, nrows, out); break;
+    case FMT_SQ8: hipLaunchKernelGGL(k_dequant_smx<FMT_SQ8>, g, b, 0, s, w, row0, nrows, out); break;
+    case FMT_SQ4: hipLaunchKernelGGL(k_dequant_smx<FMT_SQ4>, g, b, 0, s, w, row0, nrows, out); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -54,7 +54,7 @@ int type_block_elems(int type)
 {
     switch (type) {
     case SMX_TYPE_F32: case SMX_TYPE_F16: return 1;
-    case SMX_TYPE_Q4_0: case SMX_TYPE_Q8_0: return 32;
+    case SMX_TYPE_Q4_0: case SMX_TYPE_Q8_0: case SMX_TYPE_SMQ_Q8: case SMX_TYPE_SMQ_Q4: return 32;
     case SMX_TYPE_Q4_K: case SMX_TYPE_Q5_K: case SMX_TYPE_Q6_K: return 256;
     default: return 0;
     }
@@ -70,6 +70,8 @@ int type_block_bytes(int type)
     case SMX_TYPE_Q4_K: return 144;
     case SMX_TYPE_Q5_K: return 176;
     case SMX_TYPE_Q6_K: return 210;
+    case SMX_TYPE_SMQ_Q8: return 36;
+    case SMX_TYPE_SMQ_Q4: return 20;
     default: return 0;
     }
 }
@@ -97,7 +99,7 @@ struct Mat {
     {
         if (fmt < 0) return 0;
         const int64_t nb = cols / fmt_block_elems(fmt);
-        return rows * nb * (fmt_main_bytes(fmt) + (fmt_has_d(fmt) ? 2 : 0));
+        return rows * nb * (fmt_main_bytes(fmt) + fmt_d_bytes(fmt));
     }
     void release()
     {
@@ -120,7 +122,7 @@ int mat_alloc(Mat &m, int fmt, int64_t rows, int64_t cols)
     }
     const int64_t nb = cols / fmt_block_elems(fmt);
     SMX_HIP(hipMalloc((void **)&m.q, (size_t)(rows * nb * fmt_main_bytes(fmt))));
-    if (fmt_has_d(fmt)) SMX_HIP(hipMalloc((void **)&m.d, (size_t)(rows * nb * 2)));
+    if (fmt_has_d(fmt)) SMX_HIP(hipMalloc((void **)&m.d, (size_t)(rows * nb * fmt_d_bytes(fmt))));
     m.fmt = fmt;
     m.rows = rows;
     m.cols = cols;
@@ -240,6 +242,7 @@ struct smx_model {
     float *d_out_g = nullptr, *d_out_b = nullptr;
     std::vector<Layer> layers;
     float *rope_cos = nullptr, *rope_sin = nullptr;
+    bool dense_layers = false;   // some layer matrix is F16 / F32 (no folded norms)
     bool finalized = false;
     std::atomic<int> sessions{0};
 };
@@ -478,6 +481,8 @@ int setup_persistent(smx_session *S)
     const int fmt = m->layers[0].qkv.fmt;
     for (const Layer &L : m->layers)
         if (L.qkv.fmt != fmt || L.o.fmt != fmt || L.gu.fmt != fmt || L.down.fmt != fmt) return SMX_OK;
+    // the persistent kernel decodes the GGUF block formats only
+    if (m->tok.fmt > FMT_Q6_K || m->head.fmt > FMT_Q6_K || (!m->llama && m->pos.fmt > FMT_Q6_K)) return SMX_OK;
     const size_t lds = (size_t)S->max_ctx * 4;
     const int grid = decode_grid(fmt, m->hd, lds, m->ctx->device);
     if (grid <= 0) return SMX_OK;
@@ -652,7 +657,7 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
     // Up to 16 tokens, RMSNorm is folded into the GEMMs around it: the O and down projections
     // write the next norm's input as parts of gamma (.) x plus per-tile sums of x^2, and the
     // QKV (after layer 0) and gate/up GEMMs scale by 1 / rms -- no k_qprep launch per norm.
-    const bool fold = m->llama && M <= 16 && d % 256 == 0 && m->hidden % 256 == 0;
+    const bool fold = m->llama && M <= 16 && d % 256 == 0 && m->hidden % 256 == 0 && !m->dense_layers;
     WView posw = m->pos.view();
     SMX_HIP(launch_embed_tokens(m->tok.view(), m->llama ? nullptr : &posw, B.ids, B.pos, B.x, d, M, s));
     for (int l = 0; l < c.n_layer; l++) {
@@ -739,7 +744,21 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
         }
         SMX_HIP(launch_qgemm(dn, nullptr, m->hidden, PRO_NONE, nullptr, nullptr, 0.0f, s));
     }
-    if (head_from < M) {
+    if (head_from < M && fmt_dense(m->head.fmt)) {
+        // an unquantized head: the fused GEMV (norm prologue per row), one pass per row
+        GemvArgs hg{};
+        hg.w = m->head.view();
+        hg.x = B.x + (int64_t)head_from * d;
+        hg.x_stride = d;
+        hg.out = B.logits;
+        hg.out_stride = c.vocab;
+        hg.gamma = m->d_out_g;
+        hg.beta = m->d_out_b;
+        hg.eps = c.norm_eps;
+        hg.pro = pro;
+        hg.epi = EPI_STORE;
+        SMX_HIP(launch_gemv(hg, M - head_from, s));
+    } else if (head_from < M) {
         QgemmArgs hq{};
         hq.w = m->head.view();
         hq.xp = B.xp;
@@ -864,7 +883,7 @@ SMX_API int smx_weight_create(int type, int64_t rows, int64_t cols, const void *
     if (!out || !blocks) SMX_FAIL(SMX_EINVAL, "smx_weight_create: null argument");
     *out = nullptr;
     const int fmt = fmt_from_type(type);
-    if (fmt < 0) SMX_FAIL(SMX_EUNSUPPORTED, "smx_weight_create: type %d has no quantized GEMV", type);
+    if (fmt < 0) SMX_FAIL(SMX_EUNSUPPORTED, "smx_weight_create: type %d is not a weight-matrix type", type);
     if (rows <= 0 || cols <= 0 || cols % fmt_block_elems(fmt))
         SMX_FAIL(SMX_EINVAL, "smx_weight_create: cols=%lld must be a positive multiple of %d",
                  (long long)cols, fmt_block_elems(fmt));
@@ -1408,6 +1427,8 @@ SMX_API int smx_model_upload_tensor(smx_model *m, const char *name, int type, co
     if (cols != t.cols || rows != t.rows)
         SMX_FAIL(SMX_EINVAL, "%s: shape [%lld x %lld], expected [%lld x %lld]", name, (long long)rows,
                  (long long)cols, (long long)t.rows, (long long)t.cols);
+    // F16 / F32 matrices load like the block formats (GgufModelLoader.cs:438-462 loads any 2-D
+    // tensor so): the GEMV and the matrix-core GEMM take them unquantized
     if (cols > 16384) SMX_FAIL(SMX_EUNSUPPORTED, "%s: ne0=%lld exceeds 16384", name, (long long)cols);
     int rc = mat_alloc(*t.mat, fmt, t.rows_total, t.cols);
     if (rc != SMX_OK) return rc;
@@ -1441,6 +1462,8 @@ SMX_API int smx_model_finalize(smx_model *m)
         if (L.attn_g.empty() || L.ffn_g.empty()) SMX_FAIL(SMX_ESTATE, "finalize: layer %d norm weights missing", l);
         if (!m->llama && (L.attn_b.empty() || L.ffn_b.empty()))
             SMX_FAIL(SMX_ESTATE, "finalize: layer %d LayerNorm biases missing", l);
+        m->dense_layers = m->dense_layers || fmt_dense(L.qkv.fmt) || fmt_dense(L.o.fmt) || fmt_dense(L.gu.fmt) ||
+                          fmt_dense(L.down.fmt);
         int rc;
         if ((rc = upload_floats(&L.d_attn_g, L.attn_g, s)) || (rc = upload_floats(&L.d_attn_b, L.attn_b, s)) ||
             (rc = upload_floats(&L.d_ffn_g, L.ffn_g, s)) || (rc = upload_floats(&L.d_ffn_b, L.ffn_b, s)) ||

@@ -27,7 +27,32 @@ __device__ __forceinline__ uint32_t kq_scale6(uint32_t h1, uint32_t h2, uint32_t
 template <int F>
 __device__ __forceinline__ void decode_chunk_exact(const WView &w, int64_t row, int c, float *y)
 {
-    if constexpr (F == FMT_Q4_0 || F == FMT_Q8_0) {
+    if constexpr (F == FMT_F16 || F == FMT_F32) {   // ConvertF16Tensor / F32 (GgufModelLoader.cs:438-462)
+        const uint8_t *q = w.q + (row * w.nb + c) * fmt_main_bytes(F);
+#pragma unroll
+        for (int i = 0; i < 32; i++)
+            y[i] = F == FMT_F16 ? h2f_exact(((const uint16_t *)q)[i]) : ((const float *)q)[i];
+    } else if constexpr (F == FMT_SQ8 || F == FMT_SQ4) {
+        // Q8Tensor.Dequantize / Q4Tensor.Dequantize (Q8Tensor.cs:130-160, Q4Tensor.cs:150-178):
+        // code * scale, one fp32 multiply
+        const int64_t blk = row * w.nb + c;
+        const float d = __uint_as_float(((const uint32_t *)w.d)[blk]);
+        const uint8_t *q = w.q + blk * fmt_main_bytes(F);
+        if constexpr (F == FMT_SQ4) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t b = q[i];
+                int lo = (int)(b & 15u), hi = (int)(b >> 4);
+                lo = lo < 8 ? lo : lo - 16;   // Q4Tensor.DecodeNibble (Q4Tensor.cs:140-143)
+                hi = hi < 8 ? hi : hi - 16;
+                y[2 * i] = (float)lo * d;
+                y[2 * i + 1] = (float)hi * d;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; i++) y[i] = (float)(int8_t)q[i] * d;
+        }
+    } else if constexpr (F == FMT_Q4_0 || F == FMT_Q8_0) {
         const int64_t blk = row * w.nb + c;
         const float d = h2f_exact(w.d[blk]);
         const uint8_t *q = w.q + blk * fmt_main_bytes(F);

@@ -252,6 +252,122 @@ template <> struct Raw<FMT_Q6_K> {
     }
 };
 
+// F16 / F32 rows (unquantized GGUF matrices): a chunk is 32 values; fp16 converts exactly.
+template <> struct Raw<FMT_F16> {
+    uint4 v[4];
+    __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
+    {
+        const uint4 *p = (const uint4 *)(w.q + (row * w.nb + c) * 64);
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = p[i];
+    }
+    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    {
+        const uint4 *p = (const uint4 *)(w.q + (row_blk + (uint32_t)c) * 64u);
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = p[i];
+    }
+    __device__ __forceinline__ float dot(const float4 *xv, float, float, int) const
+    {
+        const uint32_t u[16] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w,
+                                v[2].x, v[2].y, v[2].z, v[2].w, v[3].x, v[3].y, v[3].z, v[3].w};
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            s0 = __builtin_fmaf(h2f(u[k] & 0xFFFFu), xget(xv, 2 * k), s0);
+            s1 = __builtin_fmaf(h2f(u[k] >> 16), xget(xv, 2 * k + 1), s1);
+        }
+        return s0 + s1;
+    }
+};
+
+template <> struct Raw<FMT_F32> {
+    float4 v[8];
+    __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
+    {
+        const float4 *p = (const float4 *)(w.q + (row * w.nb + c) * 128);
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = p[i];
+    }
+    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    {
+        const float4 *p = (const float4 *)(w.q + (row_blk + (uint32_t)c) * 128u);
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = p[i];
+    }
+    __device__ __forceinline__ float dot(const float4 *xv, float, float, int) const
+    {
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            s0 = __builtin_fmaf(v[i].x, xv[i].x, s0);
+            s1 = __builtin_fmaf(v[i].y, xv[i].y, s1);
+            s0 = __builtin_fmaf(v[i].z, xv[i].z, s0);
+            s1 = __builtin_fmaf(v[i].w, xv[i].w, s1);
+        }
+        return s0 + s1;
+    }
+};
+
+// SMQ blocks (Q8Tensor / Q4Tensor): the Q8_0 / Q4_0 codes with an fp32 scale per 32 elements
+// (the d stream read as 32-bit words).
+template <> struct Raw<FMT_SQ8> {
+    Raw<FMT_Q8_0> b;
+    __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
+    {
+        const int64_t blk = row * w.nb + c;
+        const uint4 *p = (const uint4 *)(w.q + blk * 32);
+        b.q0 = p[0];
+        b.q1 = p[1];
+        b.d = ((const uint32_t *)w.d)[blk];
+    }
+    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    {
+        const uint32_t blk = row_blk + (uint32_t)c;
+        b.q0 = *(const uint4 *)(w.q + blk * 32u);
+        b.q1 = *(const uint4 *)(w.q + blk * 32u + 16u);
+        b.d = ((const uint32_t *)w.d)[blk];
+    }
+    __device__ __forceinline__ float dot(const float4 *xv, float, float, int) const
+    {
+        const uint32_t v[8] = {b.q0.x, b.q0.y, b.q0.z, b.q0.w, b.q1.x, b.q1.y, b.q1.z, b.q1.w};
+        float s[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                s[k & 1] = __builtin_fmaf((float)(int8_t)(v[k] >> (8 * j)), xget(xv, 4 * k + j), s[k & 1]);
+        return __uint_as_float(b.d) * (s[0] + s[1]);
+    }
+};
+
+template <> struct Raw<FMT_SQ4> {
+    uint4 q; uint32_t d;
+    __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
+    {
+        const int64_t blk = row * w.nb + c;
+        q = *(const uint4 *)(w.q + blk * 16);
+        d = ((const uint32_t *)w.d)[blk];
+    }
+    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    {
+        const uint32_t blk = row_blk + (uint32_t)c;
+        q = *(const uint4 *)(w.q + blk * 16u);
+        d = ((const uint32_t *)w.d)[blk];
+    }
+    __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int) const
+    {
+        // as Q4_0: codes n ^ 8 = value + 8, sums scaled by 2^-9 (dot8_nib), the scale by 512
+        const uint32_t v[4] = {q.x ^ 0x88888888u, q.y ^ 0x88888888u, q.z ^ 0x88888888u, q.w ^ 0x88888888u};
+        float s0 = 0.0f, s1 = 0.0f;
+        s0 = dot8_nib(v[0] & 0x0F0F0F0Fu, (v[0] >> 4) & 0x0F0F0F0Fu, xv, 0, s0);
+        s1 = dot8_nib(v[1] & 0x0F0F0F0Fu, (v[1] >> 4) & 0x0F0F0F0Fu, xv, 1, s1);
+        s0 = dot8_nib(v[2] & 0x0F0F0F0Fu, (v[2] >> 4) & 0x0F0F0F0Fu, xv, 2, s0);
+        s1 = dot8_nib(v[3] & 0x0F0F0F0Fu, (v[3] >> 4) & 0x0F0F0F0Fu, xv, 3, s1);
+        return (__uint_as_float(d) * 512.0f) * ((s0 + s1) - 0.015625f * (xa + xb));
+    }
+};
+
 // ---- prologue: per-wave norm statistics --------------------------------------------------
 struct NormStat {
     float scale, mean;

@@ -28,25 +28,48 @@ namespace smx {
 //  Q6_K  main: [row][sb][208]   ql 128 B | qh' 64 B | int8 scales 16 B;  d: [row][sb] fp16.
 //                               qh' chunk c = dwords (D0, D1) at 128 + 8c; D_p byte k bits
 //                               (2g, 2g+1) hold the two high bits of element 32c + 8g + 2k + p.
+//  F16   main: [row][chunk][64]  fp16 values (GGUF F16 rows unchanged)
+//  F32   main: [row][chunk][128] fp32 values (GGUF F32 rows unchanged)
+//  SQ8   main: [row][blk][32]   int8 codes of SmallMind's Q8Tensor (SMQ files);
+//        d   : [row][blk] fp32 scale (the scale of the SMQ block holding the 32 elements)
+//  SQ4   main: [row][blk][16]   nibbles of Q4Tensor (element 2i low, 2i+1 high, two's complement);
+//        d   : [row][blk] fp32 scale
 //
 // The permutations put the high bits of the four elements that share one byte position of a
 // 4-byte group of ql at the same bit offset of four consecutive bytes, so one shift and one
 // and-or rebuild four 5-/6-bit codes.
+//
+// Upload ("source") layouts: the GGUF blocks for the GGUF formats and F16 / F32 rows; for SQ8 /
+// SQ4 blocks of 32 elements, each the fp32 scale followed by the codes (36 / 20 bytes), which
+// an SMQ tensor of any block size that is a multiple of 32 is re-laid into without rounding.
 
-enum Fmt { FMT_Q4_0 = 0, FMT_Q8_0 = 1, FMT_Q4_K = 2, FMT_Q5_K = 3, FMT_Q6_K = 4, FMT_COUNT = 5 };
+enum Fmt {
+    FMT_Q4_0 = 0, FMT_Q8_0 = 1, FMT_Q4_K = 2, FMT_Q5_K = 3, FMT_Q6_K = 4,
+    FMT_F16 = 5, FMT_F32 = 6, FMT_SQ8 = 7, FMT_SQ4 = 8, FMT_COUNT = 9
+};
 
-__host__ __device__ constexpr int fmt_block_elems(int f) { return f <= FMT_Q8_0 ? 32 : 256; }
+__host__ __device__ constexpr bool fmt_kquant(int f) { return f == FMT_Q4_K || f == FMT_Q5_K || f == FMT_Q6_K; }
+__host__ __device__ constexpr bool fmt_dense(int f) { return f == FMT_F16 || f == FMT_F32; }
+__host__ __device__ constexpr int fmt_block_elems(int f) { return fmt_kquant(f) ? 256 : 32; }
 __host__ __device__ constexpr int fmt_main_bytes(int f)
 {
-    return f == FMT_Q4_0 ? 16 : f == FMT_Q8_0 ? 32 : f == FMT_Q4_K ? 144 : f == FMT_Q5_K ? 176 : 208;
+    return f == FMT_Q4_0 ? 16 : f == FMT_Q8_0 ? 32 : f == FMT_Q4_K ? 144 : f == FMT_Q5_K ? 176 : f == FMT_Q6_K ? 208
+         : f == FMT_F16 ? 64 : f == FMT_F32 ? 128 : f == FMT_SQ8 ? 32 : 16;
 }
-__host__ __device__ constexpr bool fmt_has_d(int f) { return f == FMT_Q4_0 || f == FMT_Q8_0 || f == FMT_Q6_K; }
+__host__ __device__ constexpr bool fmt_has_d(int f)
+{
+    return f == FMT_Q4_0 || f == FMT_Q8_0 || f == FMT_Q6_K || f == FMT_SQ8 || f == FMT_SQ4;
+}
+// bytes per block of the d stream
+__host__ __device__ constexpr int fmt_d_bytes(int f) { return f == FMT_SQ8 || f == FMT_SQ4 ? 4 : fmt_has_d(f) ? 2 : 0; }
+// bytes per block of the upload layout
 __host__ __device__ constexpr int fmt_gguf_bytes(int f)
 {
-    return f == FMT_Q4_0 ? 18 : f == FMT_Q8_0 ? 34 : f == FMT_Q4_K ? 144 : f == FMT_Q5_K ? 176 : 210;
+    return f == FMT_Q4_0 ? 18 : f == FMT_Q8_0 ? 34 : f == FMT_Q4_K ? 144 : f == FMT_Q5_K ? 176 : f == FMT_Q6_K ? 210
+         : f == FMT_F16 ? 64 : f == FMT_F32 ? 128 : f == FMT_SQ8 ? 36 : 20;
 }
 
-int fmt_from_type(int type);   // -1 if not a block-quantized type
+int fmt_from_type(int type);   // -1 if not a weight-matrix type
 
 struct WView {
     int fmt;              // Fmt

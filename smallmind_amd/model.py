@@ -68,13 +68,26 @@ class ModelConfig:
         return c
 
 
+def _config_from_c(c: ModelConfigC) -> ModelConfig:
+    return ModelConfig("gpt2" if c.arch == ARCH_GPT2 else "llama", c.vocab, c.ctx, c.d_model, c.n_layer,
+                       c.n_head, c.n_kv_head, c.d_ff, float(c.rope_theta), float(c.norm_eps))
+
+
 def read_gguf_config(path: str) -> ModelConfig:
     """The ModelConfig a GGUF file's metadata describes (smx_gguf_read_config; no device work)."""
     c = ModelConfigC()
     n = ctypes.c_int64()
     call("smx_gguf_read_config", str(path).encode(), ctypes.byref(c), ctypes.byref(n))
-    return ModelConfig("gpt2" if c.arch == ARCH_GPT2 else "llama", c.vocab, c.ctx, c.d_model, c.n_layer,
-                       c.n_head, c.n_kv_head, c.d_ff, float(c.rope_theta), float(c.norm_eps))
+    return _config_from_c(c)
+
+
+def read_smq_config(path: str) -> ModelConfig:
+    """The GPT-2 ModelConfig an .smq file's metadata describes (vocab_size, block_size,
+    embed_dim, num_layers, num_heads; smx_smq_read_config; no device work)."""
+    c = ModelConfigC()
+    n = ctypes.c_int64()
+    call("smx_smq_read_config", str(path).encode(), ctypes.byref(c), ctypes.byref(n))
+    return _config_from_c(c)
 
 
 class GpuContext:
@@ -107,7 +120,24 @@ class GpuTransformerModel:
         """Loads a GGUF file (GgufModelLoader, GgufModelLoader.cs:63-77): configuration from the
         metadata (ModelConfig.FromGgufMetadata, ModelConfig.cs:142-214), every tensor uploaded
         from a memory map of the file, the model finalized (smx_model_load_gguf)."""
-        config = read_gguf_config(path)
+        return cls._loaded(read_gguf_config(path), context, device,
+                           lambda ctx, out: call("smx_model_load_gguf", ctx, str(path).encode(), out))
+
+    @classmethod
+    def from_smq(cls, path: str, config: ModelConfig | None = None, context: GpuContext | None = None,
+                 device: int = 0) -> "GpuTransformerModel":
+        """Loads a SmallMind .smq file into the GPT-2 TransformerModel (SmqModelLoader.LoadFromSmq,
+        SmqModelLoader.cs:29-100): `config` plays the reference's ModelConfig argument, None
+        takes it from the file's metadata; Q8_0 / Q4_0 weight matrices stay quantized on the
+        device with the file's scales (smx_model_load_smq)."""
+        config = config or read_smq_config(path)
+        cfg = config.to_c()
+        return cls._loaded(config, context, device,
+                           lambda ctx, out: call("smx_model_load_smq", ctx, str(path).encode(), ctypes.byref(cfg),
+                                                 out))
+
+    @classmethod
+    def _loaded(cls, config: ModelConfig, context, device: int, load) -> "GpuTransformerModel":
         self = cls.__new__(cls)
         self.config = config
         self.context = context or GpuContext(device)
@@ -116,7 +146,7 @@ class GpuTransformerModel:
         self._h = ctypes.c_void_p()
         self._sessions = []
         try:
-            call("smx_model_load_gguf", self.context._h, str(path).encode(), ctypes.byref(self._h))
+            load(self.context._h, ctypes.byref(self._h))
         except Exception:
             if self._own_ctx:
                 self.context.close()

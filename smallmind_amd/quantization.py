@@ -20,7 +20,9 @@ from ._lib import SmxError, call
 
 
 class GgufTensorType(IntEnum):
-    """GGUF tensor type ids (GgufTensorType.cs:6-52) the backend implements."""
+    """GGUF tensor type ids (GgufTensorType.cs:6-52) the backend implements, and SmallMind's own
+    SMQ Q8Tensor / Q4Tensor blocks (1000 + QuantScheme id, QuantScheme.cs) in their upload
+    layout (per 32 elements: the fp32 scale of their SMQ block, then the codes; smq_pack)."""
     F32 = 0
     F16 = 1
     Q4_0 = 2
@@ -28,10 +30,24 @@ class GgufTensorType(IntEnum):
     Q4_K = 12
     Q5_K = 13
     Q6_K = 14
+    SMQ_Q8 = 1010
+    SMQ_Q4 = 1011
 
 
-BLOCK_ELEMS = {0: 1, 1: 1, 2: 32, 8: 32, 12: 256, 13: 256, 14: 256}
-BLOCK_BYTES = {0: 4, 1: 2, 2: 18, 8: 34, 12: 144, 13: 176, 14: 210}
+BLOCK_ELEMS = {0: 1, 1: 1, 2: 32, 8: 32, 12: 256, 13: 256, 14: 256, 1010: 32, 1011: 32}
+BLOCK_BYTES = {0: 4, 1: 2, 2: 18, 8: 34, 12: 144, 13: 176, 14: 210, 1010: 36, 1011: 20}
+
+
+def smq_pack(qtype: int, data, scales, rows: int, cols: int, block_size: int) -> np.ndarray:
+    """A Q8Tensor / Q4Tensor (codes as stored in an .smq file, fp32 scales per block_size
+    elements of the flattened tensor) re-laid as SMX_TYPE_SMQ_Q8 / _Q4 upload bytes; no value
+    changes (smx_smq_pack, host memory)."""
+    d = np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+    sc = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+    out = np.empty(rows * cols // 32 * BLOCK_BYTES[int(qtype)], np.uint8)
+    call("smx_smq_pack", int(qtype), d.ctypes.data_as(ctypes.c_void_p), sc.ctypes.data_as(ctypes.c_void_p),
+         rows, cols, block_size, out.ctypes.data_as(ctypes.c_void_p), out.size)
+    return out
 
 
 def _torch():

@@ -7,14 +7,28 @@ import numpy as np
 import oracle as O
 
 TYPES = {"Q4_0": O.Q4_0, "Q8_0": O.Q8_0, "Q4_K": O.Q4_K, "Q5_K": O.Q5_K, "Q6_K": O.Q6_K}
+# every weight-matrix format of the backend: the GGUF blocks, SmallMind's SMQ blocks and the
+# unquantized F16 / F32 matrices
+ALL_TYPES = dict(TYPES, SMQ_Q8=O.SMQ_Q8, SMQ_Q4=O.SMQ_Q4, F16=O.F16, F32=O.F32)
 
 
 def random_blocks(qtype: int, nblocks: int, seed: int) -> np.ndarray:
     """Random bytes for every field, with the fp16 scale fields forced finite (the reference's
     HalfToFloat keeps NaN payloads, which no fp32 product reproduces bit-for-bit)."""
     rng = np.random.default_rng(seed)
+    if qtype == O.F32:   # finite values over a wide range of magnitudes
+        v = rng.normal(0, 1, nblocks) * np.exp2(rng.integers(-30, 30, nblocks))
+        return v.astype(np.float32).view(np.uint8)
     bb = O.BLOCK_BYTES[qtype]
     b = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+    if qtype == O.F16:   # every finite half pattern
+        h = b.reshape(-1).view(np.uint16)
+        h[(h & 0x7C00) == 0x7C00] &= 0xBBFF
+        return b.reshape(-1)
+    if qtype in (O.SMQ_Q8, O.SMQ_Q4):   # random codes, finite fp32 scales of moderate size
+        sc = (rng.normal(0, 1, nblocks) * np.exp2(rng.integers(-12, 4, nblocks))).astype(np.float32)
+        b[:, :4] = sc.view(np.uint8).reshape(nblocks, 4)
+        return b.reshape(-1)
 
     def finite_half(col):
         h = b[:, col].astype(np.uint16) | (b[:, col + 1].astype(np.uint16) << 8)

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from tests.helpers import TYPES, quantized, random_blocks, rel_err
+from tests.helpers import ALL_TYPES as TYPES, quantized, random_blocks, rel_err
 
 pytestmark = pytest.mark.gpu
 

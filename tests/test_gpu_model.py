@@ -24,6 +24,12 @@ SMALL = {
     # Q8_0 layers + Q6_K head (configs[3] formats), and Q4_0 layers
     "llama-q8_0": (ModelConfig("llama", 1000, 160, 256, 2, 8, 2, 512), O.Q8_0, O.Q6_K, O.Q6_K),
     "llama-q4_0": (ModelConfig("llama", 1000, 160, 256, 2, 8, 2, 512), O.Q4_0, O.Q8_0, O.Q4_0),
+    # SmallMind's SMQ blocks (Q8Tensor / Q4Tensor, fp32 scales) in every matrix
+    "gpt2-smq_q8": (ModelConfig("gpt2", 1000, 160, 256, 2, 4, 4, 1024), O.SMQ_Q8, O.SMQ_Q8, O.SMQ_Q8),
+    "llama-smq_q4": (ModelConfig("llama", 1000, 160, 256, 2, 8, 2, 512), O.SMQ_Q4, O.SMQ_Q8, O.SMQ_Q4),
+    # unquantized F16 / F32 matrices (GgufModelLoader.ConvertF16Tensor / F32; the FP32 Linear)
+    "llama-f16": (ModelConfig("llama", 1000, 160, 256, 2, 8, 2, 512), O.F16, O.F16, O.F32),
+    "gpt2-f32": (ModelConfig("gpt2", 1000, 160, 256, 2, 4, 4, 1024), O.F32, O.F32, O.F16),
 }
 
 
@@ -132,7 +138,7 @@ def test_sampled_generation_follows_the_reference_pipeline(pairs, key):
     s.close()
 
 
-@pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0", "smollm-q5k"])
+@pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0", "smollm-q5k", "llama-f16", "gpt2-f32"])
 def test_model_from_gguf_equals_direct_upload(key, tmp_path):
     """A model written to a GGUF file (64-byte alignment, so Q8_0 tensors are padded) and loaded
     with smx_model_load_gguf generates the same tokens and bit-identical logits as the same
@@ -163,7 +169,7 @@ def test_model_from_gguf_equals_direct_upload(key, tmp_path):
     gm.close()
 
 
-@pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0"])
+@pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0", "llama-f16", "llama-smq_q4"])
 def test_forward_api_matches_nocache_reference(pairs, key):
     """GpuInferenceSession.forward mirrors TransformerModel.Forward(idx, positionOffset) with the
     cache on; compared with the reference's no-cache full-context forward."""
@@ -269,7 +275,7 @@ def test_prefill_across_chunks_matches_reference():
 
 
 @pytest.mark.parametrize("n_sess", [17, 12])
-@pytest.mark.parametrize("key", ["smollm-q5k", "llama-q4k", "gpt2-q8_0"])
+@pytest.mark.parametrize("key", ["smollm-q5k", "llama-q4k", "gpt2-q8_0", "llama-f16", "gpt2-smq_q8"])
 def test_batch_generate_lockstep_matches_single_sessions_and_reference(pairs, key, n_sess):
     """several sessions stepping together (smx_batch_generate) produce, per
     session, the greedy tokens of the reference run alone; prompts of different lengths, so
