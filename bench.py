@@ -25,6 +25,16 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "decode tok/s batch1 + quant GEMV HBM GB/s (% of peak), LLaMA-1B Q4_K"
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def layer_gemm_flops(cfg) -> float:
+    """FLOPs of one token through the layer matrices (QKV, O, gate/up or up, down): 2 N K each."""
+    d, kv, hid = cfg.embedding_length, cfg.kv_dim, cfg.hidden_dim
+    gu = 2 * hid if cfg.architecture == "llama" else hid
+    return 2.0 * cfg.block_count * ((d + 2 * kv) * d + d * d + gu * d + d * hid)
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -137,8 +147,11 @@ def other_configs():
         toks, st = sess.generate_greedy(prompt, wl.new_tokens)
         tok_s = wl.new_tokens / (st["decode_ms"] * 1e-3)
         step_bytes = decode_step_bytes(wl, mean_attended(wl))
+        pre_tok_s = (wl.prompt_len - 1) / (st["prefill_ms"] * 1e-3)
         out[key] = {"prompt_len": wl.prompt_len, "new_tokens": wl.new_tokens,
-                    "prefill_tok_s": round((wl.prompt_len - 1) / (st["prefill_ms"] * 1e-3), 1),
+                    "prefill_tok_s": round(pre_tok_s, 1),
+                    "prefill_mfma_frac": round(layer_gemm_flops(wl.config) * pre_tok_s / 1e12
+                                               / MFMA_BF16_PEAK_TFLOPS, 4),
                     "decode_tok_s": round(tok_s, 1),
                     "weight_bytes": int(model.weight_bytes()),
                     "bytes_per_token": step_bytes,
@@ -161,6 +174,8 @@ def other_configs():
     out["smollm-1.7b-q5_k"] = {
         "sessions": wl.sessions, "prompt_len": wl.prompt_len, "new_tokens": wl.new_tokens,
         "prefill_tok_s": round(st["prefill_steps"] / (st["prefill_ms"] * 1e-3), 1),
+        "prefill_mfma_frac": round(layer_gemm_flops(wl.config) * st["prefill_steps"] / (st["prefill_ms"] * 1e-3)
+                                   / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         "decode_tok_s_aggregate": round(wl.sessions * wl.new_tokens / (st["decode_ms"] * 1e-3), 1),
         "decode_ms_per_step": round(st["decode_ms"] / wl.new_tokens, 4),
         "weight_bytes": int(model.weight_bytes()),
@@ -344,6 +359,10 @@ def main():
                                f"{wl.prompt_len}-token prompt + {wl.new_tokens} greedy tokens",
                    "batch": 1, "prompt_len": wl.prompt_len, "new_tokens": wl.new_tokens},
         "prefill_tok_s": round(pre_tok_s, 2),
+        # matrix-core use of the prefill: useful GEMM FLOPs of the layer matrices (2 N K per
+        # token) per second over the whole prefill time, against the 2.5 PFLOP/s bf16 dense peak
+        "prefill_gemm_tflops": round(layer_gemm_flops(cfg) * pre_tok_s / 1e12, 2),
+        "prefill_mfma_frac": round(layer_gemm_flops(cfg) * pre_tok_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         "decode_ms_per_token": round(dec_ms / (args.steps * wl.new_tokens), 4),
         "decode_effective_gbs": round(token_bytes / (dec_ms * 1e-3 / (args.steps * wl.new_tokens)) / 1e9, 1),
         "bytes_per_token": int(token_bytes),

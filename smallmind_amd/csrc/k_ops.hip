@@ -112,8 +112,35 @@ template <int HD> struct AttnCfg {
 //    so every slice of a head obtains the same bits), scales by 1/sum, and accumulates
 //    P.V for its slice (V is position-major, so a position's slice is 64 contiguous bytes).
 constexpr int kScorePB = 32;    // positions per score workgroup
+constexpr unsigned kPrefetchWgs = 128;   // prefetch workgroups appended to the decode attention
 constexpr int kPvSlice = 16;    // dimensions per P.V workgroup
 constexpr int kPvChunk = 2304;  // positions per workgroup of the two-chunk P.V (64 lanes x 36)
+
+// Workgroup w of nw reads its share of every prefetch range (16-byte loads, 8 per thread in
+// flight) so that the lines sit in the memory-side cache when the next kernels read them.  The
+// loaded values only feed an empty asm statement, which keeps the loads.
+__device__ __forceinline__ void prefetch_slice(const Prefetch &pf, int w, int nw, int nt)
+{
+    const uint32_t tid = threadIdx.x;
+    uint32_t acc = 0;
+    for (int r = 0; r < pf.n; r++) {
+        const uint32_t n16 = pf.bytes[r] >> 4;
+        const uint32_t b0 = (uint32_t)((uint64_t)n16 * (uint32_t)w / (uint32_t)nw);
+        const uint32_t b1 = (uint32_t)((uint64_t)n16 * (uint32_t)(w + 1) / (uint32_t)nw);
+        const uint4 *src = (const uint4 *)pf.p[r];
+        for (uint32_t i = b0 + tid; i < b1; i += 8u * (uint32_t)nt) {
+            uint4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t j = i + (uint32_t)k * (uint32_t)nt;
+                v[k] = j < b1 ? src[j] : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) acc ^= v[k].x ^ v[k].w;
+        }
+    }
+    asm volatile("" ::"v"(acc));
+}
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q, const float *__restrict__ kc,
@@ -386,8 +413,13 @@ template <int HD, int NT, int P>
 __global__ __launch_bounds__(NT) void k_attn_dec(const float *__restrict__ q, const float *__restrict__ kc,
                                                  const float *__restrict__ vc, float *__restrict__ out,
                                                  int n_head, int n_kv_head, int ctx_stride,
-                                                 const int32_t *__restrict__ pos_dev, int n_pos_fixed)
+                                                 const int32_t *__restrict__ pos_dev, int n_pos_fixed, Prefetch pf)
 {
+    if ((int)blockIdx.x >= n_head * (HD / kPvSlice)) {   // workgroups past the attention grid
+        prefetch_slice(pf, (int)blockIdx.x - n_head * (HD / kPvSlice),
+                       (int)gridDim.x - n_head * (HD / kPvSlice), NT);
+        return;
+    }
     constexpr int NW = NT / 64;
     constexpr int NS = HD / kPvSlice;   // slices per head
     constexpr int C4 = kPvSlice / 4;    // float4 columns per slice
@@ -897,10 +929,17 @@ hipError_t launch_attn_hd(dim3 g1, dim3 g2, size_t q_lds, size_t p_lds, int U, i
 
 template <int HD, int NT, int P>
 hipError_t launch_dec(dim3 g, const float *q, const float *kc, const float *vc, float *out, int n_head,
-                      int n_kv_head, int ctx_stride, const int32_t *pos_dev, int n_pos_fixed, hipStream_t s)
+                      int n_kv_head, int ctx_stride, const int32_t *pos_dev, int n_pos_fixed, hipStream_t s,
+                      const Prefetch *pf)
 {
-    hipLaunchKernelGGL((k_attn_dec<HD, NT, P>), g, dim3(NT), 0, s, q, kc, vc, out, n_head, n_kv_head, ctx_stride,
-                       pos_dev, n_pos_fixed);
+    Prefetch p{};
+    unsigned extra = 0;
+    if (pf && pf->n > 0) {
+        p = *pf;
+        extra = kPrefetchWgs;
+    }
+    hipLaunchKernelGGL((k_attn_dec<HD, NT, P>), dim3(g.x + extra), dim3(NT), 0, s, q, kc, vc, out, n_head, n_kv_head,
+                       ctx_stride, pos_dev, n_pos_fixed, p);
     return hipGetLastError();
 }
 
@@ -909,22 +948,22 @@ hipError_t launch_dec(dim3 g, const float *q, const float *kc, const float *vc, 
 template <int HD>
 hipError_t launch_dec_hd(dim3 g, int max_pos, const float *q, const float *kc, const float *vc, float *out,
                          int n_head, int n_kv_head, int ctx_stride, const int32_t *pos_dev, int n_pos_fixed,
-                         hipStream_t s)
+                         hipStream_t s, const Prefetch *pf)
 {
-    if (max_pos <= 256) return launch_dec<HD, 256, 1>(g, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
-    if (max_pos <= 512) return launch_dec<HD, 256, 2>(g, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
-    if (max_pos <= 768) return launch_dec<HD, 256, 3>(g, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
-    return launch_dec<HD, 512, 2>(g, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
+    if (max_pos <= 256) return launch_dec<HD, 256, 1>(g, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s, pf);
+    if (max_pos <= 512) return launch_dec<HD, 256, 2>(g, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s, pf);
+    if (max_pos <= 768) return launch_dec<HD, 256, 3>(g, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s, pf);
+    return launch_dec<HD, 512, 2>(g, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s, pf);
 }
 
 hipError_t launch_attn_dec(dim3 g, int max_pos, int hd, const float *q, const float *kc, const float *vc,
                            float *out, int n_head, int n_kv_head, int ctx_stride, const int32_t *pos_dev,
-                           int n_pos_fixed, hipStream_t s)
+                           int n_pos_fixed, hipStream_t s, const Prefetch *pf)
 {
     switch (hd) {
-    case 16: return launch_dec_hd<16>(g, max_pos, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
-    case 32: return launch_dec_hd<32>(g, max_pos, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
-    case 64: return launch_dec_hd<64>(g, max_pos, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s);
+    case 16: return launch_dec_hd<16>(g, max_pos, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s, pf);
+    case 32: return launch_dec_hd<32>(g, max_pos, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s, pf);
+    case 64: return launch_dec_hd<64>(g, max_pos, q, kc, vc, out, n_head, n_kv_head, ctx_stride, pos_dev, n_pos_fixed, s, pf);
     default: return hipErrorInvalidValue;
     }
 }
@@ -939,7 +978,7 @@ int attention_pv_chunks(int max_pos, int max_chunks)
 hipError_t launch_attention_split(const float *q, const float *kc, const float *vc, float *out,
                                   float *scores, int n_head, int n_kv_head, int hd, int ctx_stride,
                                   const int32_t *pos_dev, int n_pos_fixed, int max_pos, hipStream_t s,
-                                  int max_chunks)
+                                  int max_chunks, const Prefetch *pf)
 {
     if (hd % kPvSlice || hd > 128 || n_head % n_kv_head || max_pos > ctx_stride || max_pos < 1)
         return hipErrorInvalidValue;
@@ -950,7 +989,7 @@ hipError_t launch_attention_split(const float *q, const float *kc, const float *
     if (q_lds > 64 * 1024 || p_lds > 160 * 1024) return hipErrorInvalidValue;
     const dim3 g1((unsigned)(n_kv_head * nblk)), g2((unsigned)(n_head * (hd / kPvSlice)));
     if (hd <= 64 && max_pos <= 1024 && ctx_stride % 4 == 0) return launch_attn_dec(g2, max_pos, hd, q, kc, vc, out, n_head, n_kv_head,
-                                                             ctx_stride, pos_dev, n_pos_fixed, s);
+                                                             ctx_stride, pos_dev, n_pos_fixed, s, pf);
     // positions per lane sized to the session context so that every V row of the context is
     // loaded in the first batch, all of its loads in flight: 256 threads (64 position lanes)
     // up to 1024 positions, 512 threads (128 position lanes) up to 4608

@@ -266,10 +266,18 @@ hipError_t launch_softmax(float *scores, float scale, int seq, int k_seq, int ca
 // caller; attention_pv_chunks says how many partial outputs a call writes.
 size_t attention_scores_floats(int n_head, int max_pos);
 int attention_pv_chunks(int max_pos, int max_chunks);
+// Device ranges read ahead into the memory-side cache (MALL) by otherwise idle workgroups of the
+// one-launch decode attention: the weights of the GEMVs that follow it in the decode step.
+struct Prefetch {
+    static constexpr int kMax = 8;
+    const uint8_t *p[kMax];
+    uint32_t bytes[kMax];
+    int n;
+};
 hipError_t launch_attention_split(const float *q, const float *kc, const float *vc, float *out,
                                   float *scores, int n_head, int n_kv_head, int hd, int ctx_stride,
                                   const int32_t *pos_dev, int n_pos_fixed, int max_pos, hipStream_t s,
-                                  int max_chunks = 1);
+                                  int max_chunks = 1, const Prefetch *pf = nullptr);
 hipError_t launch_sample(const float *logits, int n, const int32_t *ctx, int n_ctx, const smx_sampling &sp,
                          double u, float *probs, int32_t *out, hipStream_t s);
 // Device state of a sampled generation: the options, the seed of the draw stream and the
