@@ -112,35 +112,9 @@ template <int HD> struct AttnCfg {
 //    so every slice of a head obtains the same bits), scales by 1/sum, and accumulates
 //    P.V for its slice (V is position-major, so a position's slice is 64 contiguous bytes).
 constexpr int kScorePB = 32;    // positions per score workgroup
-constexpr unsigned kPrefetchWgs = 128;   // prefetch workgroups appended to the decode attention
 constexpr int kPvSlice = 16;    // dimensions per P.V workgroup
 constexpr int kPvChunk = 2304;  // positions per workgroup of the two-chunk P.V (64 lanes x 36)
 
-// Workgroup w of nw reads its share of every prefetch range (16-byte loads, 8 per thread in
-// flight) so that the lines sit in the memory-side cache when the next kernels read them.  The
-// loaded values only feed an empty asm statement, which keeps the loads.
-__device__ __forceinline__ void prefetch_slice(const Prefetch &pf, int w, int nw, int nt)
-{
-    const uint32_t tid = threadIdx.x;
-    uint32_t acc = 0;
-    for (int r = 0; r < pf.n; r++) {
-        const uint32_t n16 = pf.bytes[r] >> 4;
-        const uint32_t b0 = (uint32_t)((uint64_t)n16 * (uint32_t)w / (uint32_t)nw);
-        const uint32_t b1 = (uint32_t)((uint64_t)n16 * (uint32_t)(w + 1) / (uint32_t)nw);
-        const uint4 *src = (const uint4 *)pf.p[r];
-        for (uint32_t i = b0 + tid; i < b1; i += 8u * (uint32_t)nt) {
-            uint4 v[8];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const uint32_t j = i + (uint32_t)k * (uint32_t)nt;
-                v[k] = j < b1 ? src[j] : make_uint4(0u, 0u, 0u, 0u);
-            }
-#pragma unroll
-            for (int k = 0; k < 8; k++) acc ^= v[k].x ^ v[k].w;
-        }
-    }
-    asm volatile("" ::"v"(acc));
-}
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q, const float *__restrict__ kc,

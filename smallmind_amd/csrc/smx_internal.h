@@ -92,6 +92,16 @@ enum Epi {
                      // -> *amax_out and, with `tokens`, tokens[*tok_pos + 1], ++*tok_pos
 };
 
+// Device ranges read ahead into the memory-side cache (MALL) by extra workgroups of the
+// one-launch decode attention: the weights of the GEMV that follows it in the decode step.
+struct Prefetch {
+    static constexpr int kMax = 8;
+    const uint8_t *p[kMax];
+    uint32_t bytes[kMax];
+    int n;
+};
+constexpr unsigned kPrefetchWgs = 128;   // workgroups appended to a launch that prefetches
+
 struct GemvArgs {
     WView w;
     const float *x;        // [m][cols]
@@ -266,14 +276,6 @@ hipError_t launch_softmax(float *scores, float scale, int seq, int k_seq, int ca
 // caller; attention_pv_chunks says how many partial outputs a call writes.
 size_t attention_scores_floats(int n_head, int max_pos);
 int attention_pv_chunks(int max_pos, int max_chunks);
-// Device ranges read ahead into the memory-side cache (MALL) by otherwise idle workgroups of the
-// one-launch decode attention: the weights of the GEMVs that follow it in the decode step.
-struct Prefetch {
-    static constexpr int kMax = 8;
-    const uint8_t *p[kMax];
-    uint32_t bytes[kMax];
-    int n;
-};
 hipError_t launch_attention_split(const float *q, const float *kc, const float *vc, float *out,
                                   float *scores, int n_head, int n_kv_head, int hd, int ctx_stride,
                                   const int32_t *pos_dev, int n_pos_fixed, int max_pos, hipStream_t s,
