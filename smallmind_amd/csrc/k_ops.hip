@@ -2,6 +2,7 @@
 #include "smx_device.h"
 #include "smx_formats.h"
 #include "smx_attn.h"
+#include "smx_prefetch.h"
 
 namespace smx {
 
