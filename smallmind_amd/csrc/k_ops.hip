@@ -649,38 +649,53 @@ __global__ void k_advance(int32_t *pos)
 }
 
 // Chunk c of a row of any weight layout, dequantised exactly (decode_chunk_exact).
-__device__ __forceinline__ void decode_chunk_any(const WView &w, int64_t row, int c, float *y)
-{
-    switch (w.fmt) {
-    case FMT_Q4_0: decode_chunk_exact<FMT_Q4_0>(w, row, c, y); break;
-    case FMT_Q8_0: decode_chunk_exact<FMT_Q8_0>(w, row, c, y); break;
-    case FMT_Q4_K: decode_chunk_exact<FMT_Q4_K>(w, row, c, y); break;
-    case FMT_Q5_K: decode_chunk_exact<FMT_Q5_K>(w, row, c, y); break;
-    case FMT_Q6_K: decode_chunk_exact<FMT_Q6_K>(w, row, c, y); break;
-    case FMT_F16: decode_chunk_exact<FMT_F16>(w, row, c, y); break;
-    case FMT_F32: decode_chunk_exact<FMT_F32>(w, row, c, y); break;
-    case FMT_SQ8: decode_chunk_exact<FMT_SQ8>(w, row, c, y); break;
-    default: decode_chunk_exact<FMT_SQ4>(w, row, c, y); break;
-    }
-}
-
-// Embedding gather (NeuralNet.cs:376-391, row copies :576-592) with the row dequantised
-// exactly, plus the learned position row for GPT-2 (TransformerModel.cs:299-326).
-__device__ void embed_row(const WView &w, int64_t row, float *y, const WView *pw, int64_t prow)
+// One pass over an embedding row: y = row (ADD = false) or y = y + row (ADD = true), each thread
+// decoding whole 32-element chunks in registers and writing them as float4.
+template <int F, bool ADD>
+__device__ __forceinline__ void embed_pass(const WView &w, int64_t row, float *y)
 {
     const int nch = (int)(w.cols / 32);
     for (int c = threadIdx.x; c < nch; c += blockDim.x) {
         float v[32];
-        decode_chunk_any(w, row, c, v);
-        if (pw) {
-            float p[32];
-            decode_chunk_any(*pw, prow, c, p);
+        decode_chunk_exact<F>(w, row, c, v);
+        float4 *y4 = (float4 *)(y + (int64_t)c * 32);
 #pragma unroll
-            for (int i = 0; i < 32; i++) v[i] = v[i] + p[i];
+        for (int i = 0; i < 8; i++) {
+            float4 o = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+            if constexpr (ADD) {
+                const float4 a = y4[i];
+                o = make_float4(a.x + o.x, a.y + o.y, a.z + o.z, a.w + o.w);
+            }
+            y4[i] = o;
         }
-#pragma unroll
-        for (int i = 0; i < 32; i++) y[c * 32 + i] = v[i];
     }
+}
+
+template <bool ADD>
+__device__ void embed_pass_any(const WView &w, int64_t row, float *y)
+{
+    switch (w.fmt) {
+    case FMT_Q4_0: embed_pass<FMT_Q4_0, ADD>(w, row, y); break;
+    case FMT_Q8_0: embed_pass<FMT_Q8_0, ADD>(w, row, y); break;
+    case FMT_Q4_K: embed_pass<FMT_Q4_K, ADD>(w, row, y); break;
+    case FMT_Q5_K: embed_pass<FMT_Q5_K, ADD>(w, row, y); break;
+    case FMT_Q6_K: embed_pass<FMT_Q6_K, ADD>(w, row, y); break;
+    case FMT_F16: embed_pass<FMT_F16, ADD>(w, row, y); break;
+    case FMT_F32: embed_pass<FMT_F32, ADD>(w, row, y); break;
+    case FMT_SQ8: embed_pass<FMT_SQ8, ADD>(w, row, y); break;
+    default: embed_pass<FMT_SQ4, ADD>(w, row, y); break;
+    }
+}
+
+// Embedding gather (NeuralNet.cs:376-391, row copies :576-592) with the row dequantised
+// exactly, plus the learned position row for GPT-2 (TransformerModel.cs:299-326): the token row
+// is stored, then the position row added to it (tok + pos, the reference's operand order); each
+// thread handles the same chunks in both passes.
+__device__ __forceinline__ void embed_row(const WView &w, int64_t row, float *y, const WView &pw, bool has_pos,
+                                          int64_t prow)
+{
+    embed_pass_any<false>(w, row, y);
+    if (has_pos) embed_pass_any<true>(pw, prow, y);
 }
 
 __global__ __launch_bounds__(kThreads) void k_embed(WView w, WView pw, int has_pos,
@@ -691,8 +706,7 @@ __global__ __launch_bounds__(kThreads) void k_embed(WView w, WView pw, int has_p
     const int p = *pos;
     int64_t tok = tokens[p];
     if (tok < 0 || tok >= w.rows) tok = 0;   // the host validates tokens; never read out of bounds
-    const WView *pp = has_pos ? &pw : nullptr;
-    embed_row(w, tok, x, pp, p);
+    embed_row(w, tok, x, pw, has_pos != 0, p);
 }
 
 // End of a decode step with the next step's embedding folded in: argmax over the head's
@@ -743,8 +757,7 @@ __global__ __launch_bounds__(kThreads) void k_argmax_embed(const float *__restri
     // the learned position row of the next position (clamped: after the last step of a full
     // context it is never used)
     const int64_t prow = has_pos ? (p + 1 < pw.rows ? p + 1 : pw.rows - 1) : 0;
-    const WView *pp = has_pos ? &pw : nullptr;
-    embed_row(w, tok, x_next, pp, prow);
+    embed_row(w, tok, x_next, pw, has_pos != 0, prow);
 }
 
 // Embedding rows of a token batch: x[t] = emb[tok[t]] (+ pos_emb[pos[t]]), one workgroup per
@@ -759,8 +772,7 @@ __global__ __launch_bounds__(kThreads) void k_embed_tokens(WView w, WView pw, in
     if (id < 0 || id >= w.rows) id = 0;   // the host validates tokens; never read out of bounds
     const int p = pos[t];
     float *xr = x + (int64_t)t * x_stride;
-    const WView *pp = has_pos ? &pw : nullptr;
-    embed_row(w, id, xr, pp, p);
+    embed_row(w, id, xr, pw, has_pos != 0, p);
 }
 
 // Decode attention for a token batch: token t (its own position and KV cache) x head h.

@@ -636,7 +636,11 @@ __device__ __forceinline__ void decode_chunk_any(const WView &w, int64_t row, in
     case FMT_Q8_0: decode_chunk_exact<FMT_Q8_0>(w, row, c, y); break;
     case FMT_Q4_K: decode_chunk_exact<FMT_Q4_K>(w, row, c, y); break;
     case FMT_Q5_K: decode_chunk_exact<FMT_Q5_K>(w, row, c, y); break;
-    default: decode_chunk_exact<FMT_Q6_K>(w, row, c, y); break;
+    case FMT_Q6_K: decode_chunk_exact<FMT_Q6_K>(w, row, c, y); break;
+    case FMT_F16: decode_chunk_exact<FMT_F16>(w, row, c, y); break;
+    case FMT_F32: decode_chunk_exact<FMT_F32>(w, row, c, y); break;
+    case FMT_SQ8: decode_chunk_exact<FMT_SQ8>(w, row, c, y); break;
+    default: decode_chunk_exact<FMT_SQ4>(w, row, c, y); break;
     }
 }
 
