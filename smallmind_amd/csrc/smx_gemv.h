@@ -81,6 +81,31 @@ __device__ __forceinline__ uint32_t shl(uint32_t v)
     else return v >> (-S);
 }
 
+// Weight loads carry the non-temporal hint (the `nt` bit of global_load): a weight byte is
+// read once per launch and not again until the same matrix comes round in the next decode
+// step, hundreds of megabytes later, so it should not displace what the next kernels reuse
+// (the KV cache rows, activations, the matrices prefetched into the MALL).  Measured on the
+// configs[2] decode step: 1782 -> 1870 tok/s, and the gate/up GEMV alone 5.02 -> 4.89 us.
+__device__ __forceinline__ uint4 ldw4(const uint8_t *p)
+{
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    const u4 v = __builtin_nontemporal_load((const u4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldw2(const uint8_t *p)
+{
+    typedef unsigned u2 __attribute__((ext_vector_type(2)));
+    const u2 v = __builtin_nontemporal_load((const u2 *)p);
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ldw1(const void *p) { return __builtin_nontemporal_load((const uint32_t *)p); }
+__device__ __forceinline__ uint32_t ldwh(const void *p) { return __builtin_nontemporal_load((const uint16_t *)p); }
+__device__ __forceinline__ float4 ldwf4(const uint8_t *p)
+{
+    const uint4 v = ldw4(p);
+    return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+
 // ---- per-format raw chunk data + dot ------------------------------------------------------
 template <int F> struct Raw;
 
@@ -89,15 +114,15 @@ template <> struct Raw<FMT_Q4_0> {
     __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
     {
         const int64_t blk = row * w.nb + c;
-        q = *(const uint4 *)(w.q + blk * 16);
-        d = w.d[blk];
+        q = ldw4(w.q + blk * 16);
+        d = ldwh(w.d + blk);
     }
     // 32-bit offsets (the whole matrix is below 4 GiB): `row_blk` = row * blocks per row.
     __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t blk = row_blk + (uint32_t)c;
-        q = *(const uint4 *)(w.q + blk * 16u);
-        d = w.d[blk];
+        q = ldw4(w.q + blk * 16u);
+        d = ldwh(w.d + blk);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int) const
     {
@@ -118,17 +143,16 @@ template <> struct Raw<FMT_Q8_0> {
     __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
     {
         const int64_t blk = row * w.nb + c;
-        const uint4 *p = (const uint4 *)(w.q + blk * 32);
-        q0 = p[0];
-        q1 = p[1];
-        d = w.d[blk];
+        q0 = ldw4(w.q + blk * 32);
+        q1 = ldw4(w.q + blk * 32 + 16);
+        d = ldwh(w.d + blk);
     }
     __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t blk = row_blk + (uint32_t)c;
-        q0 = *(const uint4 *)(w.q + blk * 32u);
-        q1 = *(const uint4 *)(w.q + blk * 32u + 16u);
-        d = w.d[blk];
+        q0 = ldw4(w.q + blk * 32u);
+        q1 = ldw4(w.q + blk * 32u + 16u);
+        d = ldwh(w.d + blk);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float, float, int) const
     {
@@ -148,14 +172,14 @@ template <> struct Raw<FMT_Q4_K> {
     __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
     {
         const uint8_t *base = w.q + (row * w.nb + (c >> 3)) * 144;
-        h = *(const uint4 *)base;
-        q = *(const uint4 *)(base + 16 + 16 * (c & 7));
+        h = ldw4(base);
+        q = ldw4(base + 16 + 16 * (c & 7));
     }
     __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t off = (row_blk + ((uint32_t)c >> 3)) * 144u;
-        h = *(const uint4 *)(w.q + off);
-        q = *(const uint4 *)(w.q + off + 16u + 16u * ((uint32_t)c & 7u));
+        h = ldw4(w.q + off);
+        q = ldw4(w.q + off + 16u + 16u * ((uint32_t)c & 7u));
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int c) const
     {
@@ -178,16 +202,16 @@ template <> struct Raw<FMT_Q5_K> {
     {
         const uint8_t *base = w.q + (row * w.nb + (c >> 3)) * 176;
         const int j = c & 7;
-        h = *(const uint4 *)base;
-        H = *(const uint32_t *)(base + 16 + 4 * j);
-        q = *(const uint4 *)(base + 48 + 16 * j);
+        h = ldw4(base);
+        H = ldw1(base + 16 + 4 * j);
+        q = ldw4(base + 48 + 16 * j);
     }
     __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t off = (row_blk + ((uint32_t)c >> 3)) * 176u, j = (uint32_t)c & 7u;
-        h = *(const uint4 *)(w.q + off);
-        H = *(const uint32_t *)(w.q + off + 16u + 4u * j);
-        q = *(const uint4 *)(w.q + off + 48u + 16u * j);
+        h = ldw4(w.q + off);
+        H = ldw1(w.q + off + 16u + 4u * j);
+        q = ldw4(w.q + off + 48u + 16u * j);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int c) const
     {
@@ -218,18 +242,18 @@ template <> struct Raw<FMT_Q6_K> {
         const int64_t sbi = row * w.nb + (c >> 3);
         const uint8_t *base = w.q + sbi * 208;
         const int cc = c & 7;
-        q = *(const uint4 *)(base + 16 * cc);
-        D = *(const uint2 *)(base + 128 + 8 * cc);
-        scw = *(const uint16_t *)(base + 192 + 2 * cc);
-        d = w.d[sbi];
+        q = ldw4(base + 16 * cc);
+        D = ldw2(base + 128 + 8 * cc);
+        scw = ldwh(base + 192 + 2 * cc);
+        d = ldwh(w.d + sbi);
     }
     __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t sb = row_blk + ((uint32_t)c >> 3), off = sb * 208u, cc = (uint32_t)c & 7u;
-        q = *(const uint4 *)(w.q + off + 16u * cc);
-        D = *(const uint2 *)(w.q + off + 128u + 8u * cc);
-        scw = *(const uint16_t *)(w.q + off + 192u + 2u * cc);
-        d = w.d[sb];
+        q = ldw4(w.q + off + 16u * cc);
+        D = ldw2(w.q + off + 128u + 8u * cc);
+        scw = ldwh(w.q + off + 192u + 2u * cc);
+        d = ldwh(w.d + sb);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int) const
     {
@@ -257,15 +281,15 @@ template <> struct Raw<FMT_F16> {
     uint4 v[4];
     __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
     {
-        const uint4 *p = (const uint4 *)(w.q + (row * w.nb + c) * 64);
+        const uint8_t *p = w.q + (row * w.nb + c) * 64;
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = p[i];
+        for (int i = 0; i < 4; i++) v[i] = ldw4(p + 16 * i);
     }
     __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
-        const uint4 *p = (const uint4 *)(w.q + (row_blk + (uint32_t)c) * 64u);
+        const uint8_t *p = w.q + (row_blk + (uint32_t)c) * 64u;
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = p[i];
+        for (int i = 0; i < 4; i++) v[i] = ldw4(p + 16 * i);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float, float, int) const
     {
@@ -285,15 +309,15 @@ template <> struct Raw<FMT_F32> {
     float4 v[8];
     __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
     {
-        const float4 *p = (const float4 *)(w.q + (row * w.nb + c) * 128);
+        const uint8_t *p = w.q + (row * w.nb + c) * 128;
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = p[i];
+        for (int i = 0; i < 8; i++) v[i] = ldwf4(p + 16 * i);
     }
     __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
-        const float4 *p = (const float4 *)(w.q + (row_blk + (uint32_t)c) * 128u);
+        const uint8_t *p = w.q + (row_blk + (uint32_t)c) * 128u;
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = p[i];
+        for (int i = 0; i < 8; i++) v[i] = ldwf4(p + 16 * i);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float, float, int) const
     {
@@ -316,17 +340,16 @@ template <> struct Raw<FMT_SQ8> {
     __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
     {
         const int64_t blk = row * w.nb + c;
-        const uint4 *p = (const uint4 *)(w.q + blk * 32);
-        b.q0 = p[0];
-        b.q1 = p[1];
-        b.d = ((const uint32_t *)w.d)[blk];
+        b.q0 = ldw4(w.q + blk * 32);
+        b.q1 = ldw4(w.q + blk * 32 + 16);
+        b.d = ldw1((const uint32_t *)w.d + blk);
     }
     __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t blk = row_blk + (uint32_t)c;
-        b.q0 = *(const uint4 *)(w.q + blk * 32u);
-        b.q1 = *(const uint4 *)(w.q + blk * 32u + 16u);
-        b.d = ((const uint32_t *)w.d)[blk];
+        b.q0 = ldw4(w.q + blk * 32u);
+        b.q1 = ldw4(w.q + blk * 32u + 16u);
+        b.d = ldw1((const uint32_t *)w.d + blk);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float, float, int) const
     {
@@ -346,14 +369,14 @@ template <> struct Raw<FMT_SQ4> {
     __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
     {
         const int64_t blk = row * w.nb + c;
-        q = *(const uint4 *)(w.q + blk * 16);
-        d = ((const uint32_t *)w.d)[blk];
+        q = ldw4(w.q + blk * 16);
+        d = ldw1((const uint32_t *)w.d + blk);
     }
     __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t blk = row_blk + (uint32_t)c;
-        q = *(const uint4 *)(w.q + blk * 16u);
-        d = ((const uint32_t *)w.d)[blk];
+        q = ldw4(w.q + blk * 16u);
+        d = ldw1((const uint32_t *)w.d + blk);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int) const
     {
