@@ -81,28 +81,49 @@ __device__ __forceinline__ uint32_t shl(uint32_t v)
     else return v >> (-S);
 }
 
-// Weight loads carry the non-temporal hint (the `nt` bit of global_load): a weight byte is
-// read once per launch and not again until the same matrix comes round in the next decode
-// step, hundreds of megabytes later, so it should not displace what the next kernels reuse
-// (the KV cache rows, activations, the matrices prefetched into the MALL).  Measured on the
-// configs[2] decode step: 1782 -> 1870 tok/s, and the gate/up GEMV alone 5.02 -> 4.89 us.
+// Weight loads.  NT = true sets the non-temporal hint (the `nt` bit of global_load): the
+// bytes of a large matrix are read once per launch and not again until the same matrix comes
+// round in the next decode step, hundreds of megabytes later, so they should not displace what
+// the next kernels reuse (the KV cache rows, activations, matrices kept in the MALL).  Matrices
+// the runtime keeps resident in the 256 MB MALL (WView::cache) are read with plain loads.
+template <bool NT>
 __device__ __forceinline__ uint4 ldw4(const uint8_t *p)
 {
-    typedef unsigned u4 __attribute__((ext_vector_type(4)));
-    const u4 v = __builtin_nontemporal_load((const u4 *)p);
-    return make_uint4(v.x, v.y, v.z, v.w);
+    if constexpr (NT) {
+        typedef unsigned u4 __attribute__((ext_vector_type(4)));
+        const u4 v = __builtin_nontemporal_load((const u4 *)p);
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return *(const uint4 *)p;
+    }
 }
+template <bool NT>
 __device__ __forceinline__ uint2 ldw2(const uint8_t *p)
 {
-    typedef unsigned u2 __attribute__((ext_vector_type(2)));
-    const u2 v = __builtin_nontemporal_load((const u2 *)p);
-    return make_uint2(v.x, v.y);
+    if constexpr (NT) {
+        typedef unsigned u2 __attribute__((ext_vector_type(2)));
+        const u2 v = __builtin_nontemporal_load((const u2 *)p);
+        return make_uint2(v.x, v.y);
+    } else {
+        return *(const uint2 *)p;
+    }
 }
-__device__ __forceinline__ uint32_t ldw1(const void *p) { return __builtin_nontemporal_load((const uint32_t *)p); }
-__device__ __forceinline__ uint32_t ldwh(const void *p) { return __builtin_nontemporal_load((const uint16_t *)p); }
+template <bool NT>
+__device__ __forceinline__ uint32_t ldw1(const void *p)
+{
+    if constexpr (NT) return __builtin_nontemporal_load((const uint32_t *)p);
+    else return *(const uint32_t *)p;
+}
+template <bool NT>
+__device__ __forceinline__ uint32_t ldwh(const void *p)
+{
+    if constexpr (NT) return __builtin_nontemporal_load((const uint16_t *)p);
+    else return *(const uint16_t *)p;
+}
+template <bool NT>
 __device__ __forceinline__ float4 ldwf4(const uint8_t *p)
 {
-    const uint4 v = ldw4(p);
+    const uint4 v = ldw4<NT>(p);
     return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
 }
 
@@ -114,15 +135,15 @@ template <> struct Raw<FMT_Q4_0> {
     __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
     {
         const int64_t blk = row * w.nb + c;
-        q = ldw4(w.q + blk * 16);
-        d = ldwh(w.d + blk);
+        q = ldw4<true>(w.q + blk * 16);
+        d = ldwh<true>(w.d + blk);
     }
     // 32-bit offsets (the whole matrix is below 4 GiB): `row_blk` = row * blocks per row.
-    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    template <bool NT = true> __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t blk = row_blk + (uint32_t)c;
-        q = ldw4(w.q + blk * 16u);
-        d = ldwh(w.d + blk);
+        q = ldw4<NT>(w.q + blk * 16u);
+        d = ldwh<NT>(w.d + blk);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int) const
     {
@@ -143,16 +164,16 @@ template <> struct Raw<FMT_Q8_0> {
     __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
     {
         const int64_t blk = row * w.nb + c;
-        q0 = ldw4(w.q + blk * 32);
-        q1 = ldw4(w.q + blk * 32 + 16);
-        d = ldwh(w.d + blk);
+        q0 = ldw4<true>(w.q + blk * 32);
+        q1 = ldw4<true>(w.q + blk * 32 + 16);
+        d = ldwh<true>(w.d + blk);
     }
-    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    template <bool NT = true> __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t blk = row_blk + (uint32_t)c;
-        q0 = ldw4(w.q + blk * 32u);
-        q1 = ldw4(w.q + blk * 32u + 16u);
-        d = ldwh(w.d + blk);
+        q0 = ldw4<NT>(w.q + blk * 32u);
+        q1 = ldw4<NT>(w.q + blk * 32u + 16u);
+        d = ldwh<NT>(w.d + blk);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float, float, int) const
     {
@@ -172,14 +193,14 @@ template <> struct Raw<FMT_Q4_K> {
     __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
     {
         const uint8_t *base = w.q + (row * w.nb + (c >> 3)) * 144;
-        h = ldw4(base);
-        q = ldw4(base + 16 + 16 * (c & 7));
+        h = ldw4<true>(base);
+        q = ldw4<true>(base + 16 + 16 * (c & 7));
     }
-    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    template <bool NT = true> __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t off = (row_blk + ((uint32_t)c >> 3)) * 144u;
-        h = ldw4(w.q + off);
-        q = ldw4(w.q + off + 16u + 16u * ((uint32_t)c & 7u));
+        h = ldw4<NT>(w.q + off);
+        q = ldw4<NT>(w.q + off + 16u + 16u * ((uint32_t)c & 7u));
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int c) const
     {
@@ -202,16 +223,16 @@ template <> struct Raw<FMT_Q5_K> {
     {
         const uint8_t *base = w.q + (row * w.nb + (c >> 3)) * 176;
         const int j = c & 7;
-        h = ldw4(base);
-        H = ldw1(base + 16 + 4 * j);
-        q = ldw4(base + 48 + 16 * j);
+        h = ldw4<true>(base);
+        H = ldw1<true>(base + 16 + 4 * j);
+        q = ldw4<true>(base + 48 + 16 * j);
     }
-    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    template <bool NT = true> __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t off = (row_blk + ((uint32_t)c >> 3)) * 176u, j = (uint32_t)c & 7u;
-        h = ldw4(w.q + off);
-        H = ldw1(w.q + off + 16u + 4u * j);
-        q = ldw4(w.q + off + 48u + 16u * j);
+        h = ldw4<NT>(w.q + off);
+        H = ldw1<NT>(w.q + off + 16u + 4u * j);
+        q = ldw4<NT>(w.q + off + 48u + 16u * j);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int c) const
     {
@@ -242,18 +263,18 @@ template <> struct Raw<FMT_Q6_K> {
         const int64_t sbi = row * w.nb + (c >> 3);
         const uint8_t *base = w.q + sbi * 208;
         const int cc = c & 7;
-        q = ldw4(base + 16 * cc);
-        D = ldw2(base + 128 + 8 * cc);
-        scw = ldwh(base + 192 + 2 * cc);
-        d = ldwh(w.d + sbi);
+        q = ldw4<true>(base + 16 * cc);
+        D = ldw2<true>(base + 128 + 8 * cc);
+        scw = ldwh<true>(base + 192 + 2 * cc);
+        d = ldwh<true>(w.d + sbi);
     }
-    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    template <bool NT = true> __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t sb = row_blk + ((uint32_t)c >> 3), off = sb * 208u, cc = (uint32_t)c & 7u;
-        q = ldw4(w.q + off + 16u * cc);
-        D = ldw2(w.q + off + 128u + 8u * cc);
-        scw = ldwh(w.q + off + 192u + 2u * cc);
-        d = ldwh(w.d + sb);
+        q = ldw4<NT>(w.q + off + 16u * cc);
+        D = ldw2<NT>(w.q + off + 128u + 8u * cc);
+        scw = ldwh<NT>(w.q + off + 192u + 2u * cc);
+        d = ldwh<NT>(w.d + sb);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int) const
     {
@@ -283,13 +304,13 @@ template <> struct Raw<FMT_F16> {
     {
         const uint8_t *p = w.q + (row * w.nb + c) * 64;
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = ldw4(p + 16 * i);
+        for (int i = 0; i < 4; i++) v[i] = ldw4<true>(p + 16 * i);
     }
-    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    template <bool NT = true> __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint8_t *p = w.q + (row_blk + (uint32_t)c) * 64u;
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = ldw4(p + 16 * i);
+        for (int i = 0; i < 4; i++) v[i] = ldw4<NT>(p + 16 * i);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float, float, int) const
     {
@@ -311,13 +332,13 @@ template <> struct Raw<FMT_F32> {
     {
         const uint8_t *p = w.q + (row * w.nb + c) * 128;
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = ldwf4(p + 16 * i);
+        for (int i = 0; i < 8; i++) v[i] = ldwf4<true>(p + 16 * i);
     }
-    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    template <bool NT = true> __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint8_t *p = w.q + (row_blk + (uint32_t)c) * 128u;
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = ldwf4(p + 16 * i);
+        for (int i = 0; i < 8; i++) v[i] = ldwf4<NT>(p + 16 * i);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float, float, int) const
     {
@@ -340,16 +361,16 @@ template <> struct Raw<FMT_SQ8> {
     __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
     {
         const int64_t blk = row * w.nb + c;
-        b.q0 = ldw4(w.q + blk * 32);
-        b.q1 = ldw4(w.q + blk * 32 + 16);
-        b.d = ldw1((const uint32_t *)w.d + blk);
+        b.q0 = ldw4<true>(w.q + blk * 32);
+        b.q1 = ldw4<true>(w.q + blk * 32 + 16);
+        b.d = ldw1<true>((const uint32_t *)w.d + blk);
     }
-    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    template <bool NT = true> __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t blk = row_blk + (uint32_t)c;
-        b.q0 = ldw4(w.q + blk * 32u);
-        b.q1 = ldw4(w.q + blk * 32u + 16u);
-        b.d = ldw1((const uint32_t *)w.d + blk);
+        b.q0 = ldw4<NT>(w.q + blk * 32u);
+        b.q1 = ldw4<NT>(w.q + blk * 32u + 16u);
+        b.d = ldw1<NT>((const uint32_t *)w.d + blk);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float, float, int) const
     {
@@ -369,14 +390,14 @@ template <> struct Raw<FMT_SQ4> {
     __device__ __forceinline__ void load(const WView &w, int64_t row, int c)
     {
         const int64_t blk = row * w.nb + c;
-        q = ldw4(w.q + blk * 16);
-        d = ldw1((const uint32_t *)w.d + blk);
+        q = ldw4<true>(w.q + blk * 16);
+        d = ldw1<true>((const uint32_t *)w.d + blk);
     }
-    __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
+    template <bool NT = true> __device__ __forceinline__ void load32(const WView &w, uint32_t row_blk, int c)
     {
         const uint32_t blk = row_blk + (uint32_t)c;
-        q = ldw4(w.q + blk * 16u);
-        d = ldw1((const uint32_t *)w.d + blk);
+        q = ldw4<NT>(w.q + blk * 16u);
+        d = ldw1<NT>((const uint32_t *)w.d + blk);
     }
     __device__ __forceinline__ float dot(const float4 *xv, float xa, float xb, int) const
     {

@@ -73,6 +73,9 @@ int fmt_from_type(int type);   // -1 if not a weight-matrix type
 
 struct WView {
     int fmt;              // Fmt
+    // 1: the matrix is kept resident in the MALL and read with plain loads; 0: its loads
+    // carry the non-temporal hint (streamed past the caches)
+    int cache = 0;
     const uint8_t *q;     // main stream
     const uint16_t *d;    // fp16 scale stream or nullptr
     int64_t rows, cols;
