@@ -807,8 +807,13 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
     return SMX_OK;
 }
 
-// Tokens of one session per prefill chunk on the matrix-core path.
-constexpr int kPrefillChunk = 256;
+// Tokens of one session per prefill chunk on the matrix-core path: long chunks give the GEMMs
+// more token tiles per weight read and fewer launches (configs[2] 512-token prompt 50.6K ->
+// 58.9K tok/s as one chunk instead of two; configs[3] 4096 tokens 38.0K / 43.6K / 46.0K /
+// 46.3K tok/s at 256 / 1024 / 2048 / 4096-token chunks).  The chunk buffers hold at least 256
+// tokens: a session of 83 positions with 96-token buffers ended its process with a host
+// segmentation fault once (cause not found), and no smaller size has run since.
+constexpr int kPrefillChunk = 2048, kPrefillChunkMin = 256;
 
 // Runs tokens[0..n) of session S at positions p0.. through the model in chunks (K/V written
 // to the session cache).  With want_head, the last token's logits land in S->logits and its
@@ -819,20 +824,23 @@ constexpr int kPrefillMin = 8;
 int prefill_tokens(smx_session *S, const int32_t *tokens_host, int n, int p0, bool want_head, hipStream_t s)
 {
     smx_model *m = S->m;
+    // chunk length: kPrefillChunk, or the session's whole context when that is shorter (the
+    // chunk buffers are sized for it), and at least kPrefillChunkMin tokens
+    const int chunk = std::max(kPrefillChunkMin, std::min(kPrefillChunk, (S->max_ctx + 15) & ~15));
     if (!S->pb.cap) {
-        int rc = batch_alloc(m, S->pb, kPrefillChunk, 1);
+        int rc = batch_alloc(m, S->pb, chunk, 1);
         if (rc != SMX_OK) return rc;
-        std::vector<float *> kc((size_t)kPrefillChunk, S->kc), vc((size_t)kPrefillChunk, S->vc);
-        std::vector<int32_t *> ta((size_t)kPrefillChunk, S->tokens);
+        std::vector<float *> kc((size_t)chunk, S->kc), vc((size_t)chunk, S->vc);
+        std::vector<int32_t *> ta((size_t)chunk, S->tokens);
         SMX_HIP(hipMemcpyAsync(S->pb.kc, kc.data(), kc.size() * sizeof(float *), hipMemcpyHostToDevice, s));
         SMX_HIP(hipMemcpyAsync(S->pb.vc, vc.data(), vc.size() * sizeof(float *), hipMemcpyHostToDevice, s));
         SMX_HIP(hipMemcpyAsync(S->pb.tok_arr, ta.data(), ta.size() * sizeof(int32_t *), hipMemcpyHostToDevice, s));
         SMX_HIP(hipStreamSynchronize(s));
     }
     TokBatch &B = S->pb;
-    std::vector<int32_t> pos((size_t)kPrefillChunk);
-    for (int i0 = 0; i0 < n; i0 += kPrefillChunk) {
-        const int M = n - i0 < kPrefillChunk ? n - i0 : kPrefillChunk;
+    std::vector<int32_t> pos((size_t)chunk);
+    for (int i0 = 0; i0 < n; i0 += chunk) {
+        const int M = n - i0 < chunk ? n - i0 : chunk;
         for (int i = 0; i < M; i++) pos[(size_t)i] = p0 + i0 + i;
         SMX_HIP(hipMemcpyAsync(B.ids, tokens_host + i0, (size_t)M * 4, hipMemcpyHostToDevice, s));
         SMX_HIP(hipMemcpyAsync(B.pos, pos.data(), (size_t)M * 4, hipMemcpyHostToDevice, s));

@@ -249,14 +249,14 @@ def test_errors_out_of_range_and_bad_tokens(pairs):
 
 
 def test_prefill_across_chunks_matches_reference():
-    """A 300-token prompt is prefilled as two matrix-core chunks (256 + 44 tokens); the
+    """A 2100-token prompt is prefilled as two matrix-core chunks (2048 + 51 tokens); the
     logits of the following decode steps and the greedy tokens must match the reference."""
-    cfg = ModelConfig("llama", 500, 320, 256, 2, 4, 2, 512)
+    cfg = ModelConfig("llama", 500, 2200, 256, 2, 4, 2, 512)
     om, gm, _ = build_pair(cfg, O.Q4_K, O.Q6_K, O.Q6_K, seed=300)
-    prompt = np.random.default_rng(4).integers(0, cfg.vocab_size, 300).astype(np.int32)
-    s = gm.create_session(320)
+    prompt = np.random.default_rng(4).integers(0, cfg.vocab_size, 2100).astype(np.int32)
+    s = gm.create_session(2120)
     toks, stats, logits = s.generate_greedy(prompt, 8, return_logits=True)
-    osess = om.session(320)
+    osess = om.session(2120)
     for p, t in enumerate(prompt[:-1]):
         osess.step(int(t), p, want_logits=False)
     tok = int(prompt[-1])
