@@ -1157,17 +1157,28 @@ template <int F>
 hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
 {
     // Rows of whole 256-element super-blocks: LDS-staged weight tiles.  Up to 16 tokens: one
-    // token tile per workgroup (16 waves splitting K from 8192 up).  More: tiles of 64 tokens x
-    // 32 rows per wave, 8 waves splitting long K (or short K over few rows), else 4 waves
-    // (K-quants: 64 rows x 32 tokens on tall matrices; Q6_K 16 rows).  Chosen by measurement
-    // over the prefill shapes of the five formats at 256 tokens.
+    // token tile per workgroup (16 waves splitting K from 8192 up).  More: per wave RT x 16
+    // rows by TT x 16 tokens, NW waves splitting K; chosen by measurement (matrix-core GEMM
+    // with its k_qprep, weights resident) at 256-token chunks and at the 512 / 2048-token
+    // chunks of the configs[2] / configs[3] prompts:
+    //  - K-quants (Q4_K / Q5_K): tall matrices 64 rows x 32 tokens, 4 waves; few rows or long
+    //    K (O, down) the same from 512 tokens (Q4_K O 47.8 -> 39.7 us, down 92.0 -> 82.0 at
+    //    512), 32 x 64 with 8 waves below; other shapes (QKV) 32 x 32, 4 waves (Q4_K QKV 52.5
+    //    -> 45.9 us at 512, Q5_K 52.1 -> 50.4 at 256);
+    //  - Q8_0 / Q4_0 / SMQ: 32 x 64, 4 waves; few rows or long K with 8 waves below 1024
+    //    tokens (Q8_0 O 165 -> 131 us, down 346 -> 317 at 2048 tokens with 4);
+    //  - Q6_K: 32 x 64 with 8 waves on few rows or long K, else 16 x 64.
     if (a.w.cols % 256 == 0) {
         const bool tall = a.w.rows >= 8192;
         if (a.M > 16) {
-            if (a.w.cols > 4096 || a.w.rows <= 2048) return launch_st<F, 2, 4, 8>(a, s);
-            if constexpr (F == FMT_Q4_K || F == FMT_Q5_K)
-                if (tall) return launch_st<F, 4, 2, 4>(a, s);
-            if constexpr (F == FMT_Q6_K) return launch_st<F, 1, 4, 8>(a, s);
+            const bool narrow = a.w.cols > 4096 || a.w.rows <= 2048;
+            if constexpr (F == FMT_Q4_K || F == FMT_Q5_K) {
+                if (tall || (narrow && a.M >= 512)) return launch_st<F, 4, 2, 4>(a, s);
+                if (narrow) return launch_st<F, 2, 4, 8>(a, s);
+                return launch_st<F, 2, 2, 4>(a, s);
+            }
+            if constexpr (F == FMT_Q6_K) return narrow ? launch_st<F, 2, 4, 8>(a, s) : launch_st<F, 1, 4, 8>(a, s);
+            if (narrow && a.M < 1024) return launch_st<F, 2, 4, 8>(a, s);
             return launch_st<F, 2, 4, 4>(a, s);
         }
         if constexpr (F != FMT_Q6_K)   // 16 waves of >= 2 super-blocks (Q6_K would spill at 128 registers)
