@@ -1162,8 +1162,8 @@ hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
     // with its k_qprep, weights resident) at 256-token chunks and at the 512 / 2048-token
     // chunks of the configs[2] / configs[3] prompts:
     //  - K-quants (Q4_K / Q5_K): tall matrices 64 rows x 32 tokens, 4 waves; few rows or long
-    //    K (O, down) the same from 512 tokens (Q4_K O 47.8 -> 39.7 us, down 92.0 -> 82.0 at
-    //    512), 32 x 64 with 8 waves below; other shapes (QKV) 32 x 32, 4 waves (Q4_K QKV 52.5
+    //    K (O, down) the same above 320 tokens (Q4_K O 47.8 -> 39.7 us, down 92.0 -> 82.0 at
+    //    512), 32 x 64 with 8 waves up to 320; other shapes (QKV) 32 x 32, 4 waves (Q4_K QKV 52.5
     //    -> 45.9 us at 512, Q5_K 52.1 -> 50.4 at 256);
     //  - Q8_0 / Q4_0 / SMQ: 32 x 64, 4 waves; few rows or long K with 8 waves below 1024
     //    tokens (Q8_0 O 165 -> 131 us, down 346 -> 317 at 2048 tokens with 4);
@@ -1173,7 +1173,7 @@ hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
         if (a.M > 16) {
             const bool narrow = a.w.cols > 4096 || a.w.rows <= 2048;
             if constexpr (F == FMT_Q4_K || F == FMT_Q5_K) {
-                if (tall || (narrow && a.M >= 512)) return launch_st<F, 4, 2, 4>(a, s);
+                if (tall || (narrow && a.M > 320)) return launch_st<F, 4, 2, 4>(a, s);
                 if (narrow) return launch_st<F, 2, 4, 8>(a, s);
                 return launch_st<F, 2, 2, 4>(a, s);
             }
