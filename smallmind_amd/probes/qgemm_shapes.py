@@ -1,6 +1,6 @@
 """Measurement probe: the matrix-core GEMM (IWeightTensor.MatMul with m >= 4 -> k_qprep +
-k_qgemm_st) at the layer shapes of the prefill chunks (256 tokens) and of the 16-session
-lockstep decode, for the block formats of configs[2] (Q4_K), configs[3] (Q8_0) and configs[4]
+k_qgemm_st) at the layer shapes of the prefill chunks (256 tokens, and the 511 / 2048-token
+chunks of the configs[2] / configs[3] prompts) and of the 16-session lockstep decode, for the block formats of configs[2] (Q4_K), configs[3] (Q8_0) and configs[4]
 (Q5_K).  Launches are eager (no graph) so that rocprofv3 counter passes see every dispatch.
 
 Prints one line per shape: microseconds per call (HIP events over `--reps` calls, weights
@@ -20,7 +20,9 @@ sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspa
 # (label, GGUF type, rows N, cols K): the four layer matrices of each model
 LLAMA_1B = [("qkv", 2560, 2048), ("o", 2048, 2048), ("gate_up", 11264, 2048), ("down", 2048, 5632)]
 SMOLLM_17B = [("qkv", 6144, 2048), ("o", 2048, 2048), ("gate_up", 16384, 2048), ("down", 2048, 8192)]
-CASES = ([("configs[2] Q4_K", 12, LLAMA_1B, (256,)), ("configs[3] Q8_0", 8, LLAMA_1B, (256,)),
+# M: 256-token chunks, the prefill chunks of the configs' prompts (configs[2]: 511 tokens in one
+# chunk; configs[3]: 2048-token chunks) and the 16-session lockstep step
+CASES = ([("configs[2] Q4_K", 12, LLAMA_1B, (256, 511)), ("configs[3] Q8_0", 8, LLAMA_1B, (256, 2048)),
           ("configs[4] Q5_K", 13, SMOLLM_17B, (256, 16))])
 
 
@@ -47,7 +49,7 @@ def main():
                 torch.cuda.synchronize()
                 us = e0.elapsed_time(e1) * 1e3 / args.reps
                 tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
-                print(f"{label:16s} {name:8s} M={M:4d} N={N:6d} K={K:5d}  {us:8.2f} us  {tf:7.2f} TFLOP/s  "
+                print(f"{label:16s} {name:8s} M={M:5d} N={N:6d} K={K:5d}  {us:8.2f} us  {tf:7.2f} TFLOP/s  "
                       f"{tf / 2500.0:.4f} of bf16 peak", flush=True)
             w.close()
 
