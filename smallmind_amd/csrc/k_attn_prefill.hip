@@ -68,7 +68,7 @@ __device__ __forceinline__ float rows_sum(float v)
 __global__ __launch_bounds__(kWaves * 64) void k_attn_prefill(
     const float *__restrict__ q, int q_stride, const float *__restrict__ kc, const float *__restrict__ vc,
     float *__restrict__ out, int out_stride, int n_head, int n_kv_head, int ctx_stride, int p_first, int M,
-    uint8_t *__restrict__ out_parts)
+    uint8_t *__restrict__ out_parts, int tok_off)
 {
     extern __shared__ float s_out[];          // [kWaves][kRows][kPitch]
     __shared__ float s_max[kWaves][kRows], s_sum[kWaves][kRows], s_inv[kRows];
@@ -241,10 +241,10 @@ __global__ __launch_bounds__(kWaves * 64) void k_attn_prefill(
         const int h = kvh * G + r % G;
         if (out_parts) {
             const int nsb = n_head * kHD / 32, k = h * kHD + d4;
-            xp_store(out_parts, nsb, t, k, acc.x);
-            xp_store(out_parts, nsb, t, k + 1, acc.y);
-            xp_store(out_parts, nsb, t, k + 2, acc.z);
-            xp_store(out_parts, nsb, t, k + 3, acc.w);
+            xp_store(out_parts, nsb, tok_off + t, k, acc.x);
+            xp_store(out_parts, nsb, tok_off + t, k + 1, acc.y);
+            xp_store(out_parts, nsb, tok_off + t, k + 2, acc.z);
+            xp_store(out_parts, nsb, tok_off + t, k + 3, acc.w);
         } else {
             *(float4 *)(out + (int64_t)t * out_stride + (int64_t)h * kHD + d4) = acc;
         }
@@ -262,10 +262,10 @@ bool attention_prefill_supported(int n_head, int n_kv_head, int hd)
 
 hipError_t launch_attention_prefill(const float *q, int q_stride, const float *kc, const float *vc, float *out,
                                     int out_stride, int n_head, int n_kv_head, int hd, int ctx_stride,
-                                    int p_first, int M, hipStream_t s, uint8_t *out_parts)
+                                    int p_first, int M, hipStream_t s, uint8_t *out_parts, int tok_off)
 {
     if (!attention_prefill_supported(n_head, n_kv_head, hd) || M <= 0 || p_first < 0 || ((n_head * hd) & 31) ||
-        p_first + M > ctx_stride || (q_stride & 3) || (out_stride & 3))
+        p_first + M > ctx_stride || (q_stride & 3) || (out_stride & 3) || tok_off < 0)
         return hipErrorInvalidValue;
     const size_t lds = (size_t)kWaves * kRows * kPitch * 4;
     const hipError_t e = hipFuncSetAttribute((const void *)k_attn_prefill,
@@ -274,7 +274,7 @@ hipError_t launch_attention_prefill(const float *q, int q_stride, const float *k
     const int TT = kRows / (n_head / n_kv_head);
     const dim3 grid((unsigned)((M + TT - 1) / TT), (unsigned)n_kv_head);
     hipLaunchKernelGGL(k_attn_prefill, grid, dim3(kWaves * 64), lds, s, q, q_stride, kc, vc, out, out_stride,
-                       n_head, n_kv_head, ctx_stride, p_first, M, out_parts);
+                       n_head, n_kv_head, ctx_stride, p_first, M, out_parts, tok_off);
     return hipGetLastError();
 }
 

@@ -674,18 +674,20 @@ int batch_alloc(const smx_model *m, TokBatch &B, int cap, int logits_rows)
     return SMX_OK;
 }
 
-// Tokens p_first .. p_first+M-1 of one session (a prefill chunk): attention runs as one causal
-// block over the session cache instead of per (token, head).
+// Rows row0 .. row0+count-1 of a token batch are consecutive tokens p_first .. of one session
+// (a prefill chunk, or one session's part of a batch of several sessions' prompts): their
+// attention runs as one causal block over that session's cache instead of per (token, head).
 struct PrefillRun {
     const float *kc, *vc;
     int p_first;
+    int row0 = 0, count = -1;   // count < 0: all M rows
 };
 
 // Runs tokens 0..M-1 of B (ids, pos, kc, vc filled on the device) through every layer on the
 // matrix-core GEMM path, writing K/V into each token's cache; the final norm + head run on rows
 // head_from..M-1 into B.logits.  Same graph as enqueue_step, per token.
 int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_from, hipStream_t s,
-               const PrefillRun *run)
+               const PrefillRun *run, int n_run = 1)
 {
     const smx_model_config &c = m->cfg;
     const int d = c.d_model, hd = m->hd, Hkv = c.n_kv_head;
@@ -728,10 +730,15 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
             SMX_HIP(launch_qgemm(a, B.x, d, pro, L.d_attn_g, L.d_attn_b, c.norm_eps, s));
         }
         // attention writes the O projection's activation parts directly (no k_qprep launch)
-        if (run && attention_prefill_supported(c.n_head, Hkv, hd))
-            SMX_HIP(launch_attention_prefill(B.q, m->nqkv, run->kc + layer_off, run->vc + layer_off, B.att, d,
-                                             c.n_head, Hkv, hd, ctx_stride, run->p_first, M, s, B.xp2));
-        else
+        if (run && attention_prefill_supported(c.n_head, Hkv, hd)) {
+            for (int i = 0; i < n_run; i++) {
+                const PrefillRun &r = run[i];
+                const int cnt = r.count < 0 ? M : r.count;
+                SMX_HIP(launch_attention_prefill(B.q + (int64_t)r.row0 * m->nqkv, m->nqkv, r.kc + layer_off,
+                                                 r.vc + layer_off, B.att + (int64_t)r.row0 * d, d, c.n_head, Hkv, hd,
+                                                 ctx_stride, r.p_first, cnt, s, B.xp2, r.row0));
+            }
+        } else
             SMX_HIP(launch_attention_tokens(B.q, m->nqkv, B.kc, B.vc, layer_off, B.att, d, c.n_head, Hkv, hd,
                                             ctx_stride, B.pos, M, s, B.xp2));
         QgemmArgs o{};
@@ -860,6 +867,70 @@ int prefill_tokens(smx_session *S, const int32_t *tokens_host, int n, int p0, bo
         SMX_HIP(hipStreamSynchronize(s));
     }
     return SMX_OK;
+}
+
+// Chunk buffer size for a prefill of n tokens: up to kPrefillChunk, at least kPrefillChunkMin.
+int prefill_cap(int64_t n)
+{
+    const int64_t r = (n + 15) & ~(int64_t)15;
+    return (int)std::max<int64_t>(kPrefillChunkMin, std::min<int64_t>(kPrefillChunk, r));
+}
+
+// The prompts of several sessions of one model (all but each prompt's last token) through the
+// matrix-core path together: their tokens are packed into chunks of up to P.cap rows, each
+// row carrying its own session's cache and position, so the GEMMs see long chunks instead of
+// one short prompt at a time; each session's rows of a chunk attend over its own cache.
+int prefill_sessions(smx_model *m, TokBatch &P, smx_session *const *sessions, int n, const int32_t *prompts,
+                     const int64_t *off, const int *lens, hipStream_t s)
+{
+    const int cap = P.cap, ctx_stride = sessions[0]->ctx_stride;
+    std::vector<int32_t> ids((size_t)cap), pos((size_t)cap);
+    std::vector<float *> kc((size_t)cap), vc((size_t)cap);
+    std::vector<int32_t *> ta((size_t)cap);
+    std::vector<PrefillRun> runs;
+    int M = 0;
+    auto flush = [&]() -> int {
+        if (M == 0) return SMX_OK;
+        SMX_HIP(hipMemcpyAsync(P.ids, ids.data(), (size_t)M * 4, hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(P.pos, pos.data(), (size_t)M * 4, hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(P.kc, kc.data(), (size_t)M * sizeof(float *), hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(P.vc, vc.data(), (size_t)M * sizeof(float *), hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(P.tok_arr, ta.data(), (size_t)M * sizeof(int32_t *), hipMemcpyHostToDevice, s));
+        const int rc = run_tokens(m, P, M, ctx_stride, M, s, runs.data(), (int)runs.size());
+        if (rc != SMX_OK) return rc;
+        // the host arrays are reused by the next chunk: let this chunk's copies finish
+        SMX_HIP(hipStreamSynchronize(s));
+        M = 0;
+        runs.clear();
+        return SMX_OK;
+    };
+    for (int i = 0; i < n; i++) {
+        smx_session *S = sessions[i];
+        const int32_t *tp = prompts + off[i];
+        int left = lens[i] - 1, p = 0;
+        while (left > 0) {
+            const int take = std::min(left, cap - M);
+            PrefillRun r{S->kc, S->vc, p};
+            r.row0 = M;
+            r.count = take;
+            runs.push_back(r);
+            for (int j = 0; j < take; j++) {
+                ids[(size_t)(M + j)] = tp[p + j];
+                pos[(size_t)(M + j)] = p + j;
+                kc[(size_t)(M + j)] = S->kc;
+                vc[(size_t)(M + j)] = S->vc;
+                ta[(size_t)(M + j)] = S->tokens;
+            }
+            M += take;
+            p += take;
+            left -= take;
+            if (M == cap) {
+                const int rc = flush();
+                if (rc != SMX_OK) return rc;
+            }
+        }
+    }
+    return flush();
 }
 
 struct BusyGuard {
@@ -1889,18 +1960,25 @@ SMX_API int smx_batch_generate(smx_session *const *sessions, int n_sessions, con
     };
 #define SMX_BHIP(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { cleanup(); SMX_HIP(e_); } } while (0)
     for (auto &e : ev) SMX_BHIP(hipEventCreate(&e));
-    // prefill every session's prompt except its last token
-    SMX_BHIP(hipEventRecord(ev[0], s));
+    // prefill every session's prompt except its last token, all sessions together
     int64_t n_prefill = 0;
-    for (int i = 0; i < n; i++) {
-        smx_session *S = sessions[i];
-        const int len = prompt_lens[i];
-        SMX_BHIP(hipMemcpyAsync(S->tokens, prompts + off[(size_t)i], (size_t)len * 4, hipMemcpyHostToDevice, s));
-        if (len > 1 && (rc = prefill_tokens(S, prompts + off[(size_t)i], len - 1, 0, false, s)) != SMX_OK) {
+    for (int i = 0; i < n; i++) n_prefill += prompt_lens[i] - 1;
+    TokBatch P;   // allocated outside the timed region
+    if (n_prefill > 0 && (rc = batch_alloc(m, P, prefill_cap(n_prefill), 1)) != SMX_OK) {
+        cleanup();
+        return rc;
+    }
+    SMX_BHIP(hipEventRecord(ev[0], s));
+    for (int i = 0; i < n; i++)
+        SMX_BHIP(hipMemcpyAsync(sessions[i]->tokens, prompts + off[(size_t)i], (size_t)prompt_lens[i] * 4,
+                                hipMemcpyHostToDevice, s));
+    if (n_prefill > 0) {
+        rc = prefill_sessions(m, P, sessions, n, prompts, off.data(), prompt_lens, s);
+        batch_free(P);
+        if (rc != SMX_OK) {
             cleanup();
             return rc;
         }
-        n_prefill += len - 1;
     }
     SMX_BHIP(hipEventRecord(ev[1], s));
     // one token per session per step

@@ -330,10 +330,11 @@ hipError_t launch_embed_tokens(const WView &tok, const WView *posw, const int32_
 // ([n_kv_head][hd][ctx_stride] / [n_kv_head][ctx_stride][hd]), out [M][out_stride].
 bool attention_prefill_supported(int n_head, int n_kv_head, int hd);
 // With out_parts set, the outputs are written as the activation parts of the next GEMM
-// (xp_store, token t, element h*hd + d) instead of out.
+// (xp_store, token tok_off + t, element h*hd + d) instead of out.
 hipError_t launch_attention_prefill(const float *q, int q_stride, const float *kc, const float *vc, float *out,
                                     int out_stride, int n_head, int n_kv_head, int hd, int ctx_stride,
-                                    int p_first, int M, hipStream_t s, uint8_t *out_parts = nullptr);
+                                    int p_first, int M, hipStream_t s, uint8_t *out_parts = nullptr,
+                                    int tok_off = 0);
 hipError_t launch_attention_tokens(const float *q, int64_t q_stride, float *const *kc_tok,
                                    float *const *vc_tok, int64_t layer_off, float *out,
                                    int64_t out_stride, int n_head, int n_kv_head, int hd,
