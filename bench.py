@@ -5,8 +5,9 @@ through the KV cache) and 256 greedy tokens, all on the device.  `value` is deco
 (GPU-event time of the token-producing steps).  The metric's kernel -- the fused Q4_K GEMV at
 the gate/up shape (11264 x 2048), the largest weight stream of the decode step -- is then timed
 on its own with HIP events around replays of a captured graph of launches over rotating weight
-copies larger than the 256 MB MALL, giving the roofline figure; the configs[1] Q4_0 GEMV shapes
-are timed the same way.  The CPU baseline is the oracle on the same model at the same
+copies larger than the 256 MB MALL, giving the roofline figure, next to a plain streaming read of
+the same bytes per launch and of 1 GiB per launch timed the same way (measured ceilings); the
+configs[1] Q4_0 GEMV shapes are timed the same way.  The CPU baseline is the oracle on the same model at the same
 positions: reference-faithful (fp32 weights dequantized at load, one thread) and on all cores.
 """
 from __future__ import annotations
@@ -78,6 +79,38 @@ def gemv_timing(qt: int, N: int, K: int, seed: int, min_bytes: int = 600 << 20, 
         w.close()
     return {"avg_us": avg_s * 1e6, "bytes": alg, "gbs": alg / avg_s / 1e9, "copies": copies,
             "launches": reps * n_launch}
+
+
+def stream_read_timing(n_bytes: int, min_bytes: int = 600 << 20, reps: int = 10):
+    """The HBM streaming-read ceiling (smx_stream_read: 16-byte loads over the whole GPU, nothing
+    written), timed like gemv_timing: HIP events around replays of a captured graph of launches
+    that each read n_bytes of a different buffer, cycling over >= 600 MB."""
+    import torch
+
+    from smallmind_amd._lib import call
+    n_bytes = (n_bytes + 15) // 16 * 16
+    copies = max(2, min_bytes // n_bytes + 1)
+    bufs = [torch.empty(n_bytes, dtype=torch.uint8, device="cuda").fill_(1) for _ in range(copies)]
+    n_launch = max(copies, 64)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        for b in bufs:
+            call("smx_stream_read", b.data_ptr(), n_bytes, s.cuda_stream)
+        with torch.cuda.graph(g, stream=s):
+            for i in range(n_launch):
+                call("smx_stream_read", bufs[i % copies].data_ptr(), n_bytes, s.cuda_stream)
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            g.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    avg_s = e0.elapsed_time(e1) * 1e-3 / (reps * n_launch)
+    del g, bufs
+    return {"bytes": n_bytes, "avg_us": round(avg_s * 1e6, 3), "gbs": round(n_bytes / avg_s / 1e9, 1)}
 
 
 def gemv_roofline():
@@ -380,6 +413,15 @@ def main():
                            "traffic": traffic_from_profiles(),
                            "kernel": g["kernel"], "avg_us": round(g["avg_us"], 3),
                            "bytes_per_launch": g["bytes"]}
+        # measured ceilings: a plain streaming read of the same bytes per launch (same launch
+        # floor, same ramp) and of 1 GiB per launch (the sustained read rate)
+        log("timing the streaming-read ceiling")
+        same = stream_read_timing(g["bytes"])
+        big = stream_read_timing(1 << 30, min_bytes=2 << 30, reps=3)
+        out["roofline"]["read_ceiling"] = {
+            "same_bytes": same, "one_gib": big,
+            "frac_of_same_bytes_read": round(g["gbs"] / same["gbs"], 4),
+            "frac_of_sustained_read": round(g["gbs"] / big["gbs"], 4)}
         log("timing the configs[1] Q4_0 GEMV shapes")
         out["c2_q4_0_gemv"] = c2_gemv_lines()
     sess.close()

@@ -162,6 +162,10 @@ SMX_API int smx_gelu(const float *x_dev, float *y_dev, int64_t n, void *stream);
 /* Greedy next-token selection (replaces the T->0 limit of InferenceSession.cs:565-606):
  * index of the maximum, lowest index on ties. */
 SMX_API int smx_argmax(const float *x_dev, int n, int32_t *out_dev, void *stream);
+/* Measurement helper; it has no counterpart in the reference.  Reads `bytes` of device
+ * memory (a multiple of 16, < 4 GiB) with 16-byte loads spread over the whole GPU and writes
+ * nothing: the streaming-read ceiling a GEMV's bandwidth is compared with (bench.py). */
+SMX_API int smx_stream_read(const void *src_dev, uint64_t bytes, void *stream);
 /* Next-token sampling options (ProductionInferenceOptions.cs:19-87); each stage is skipped at
  * its neutral value. */
 typedef struct smx_sampling {

@@ -25,7 +25,7 @@ EXPORTS = [
     "smx_weight_create", "smx_weight_info", "smx_weight_matmul", "smx_weight_matmul_noalloc",
     "smx_weight_matmul_host", "smx_weight_to_float32", "smx_weight_to_float32_host",
     "smx_weight_destroy", "smx_rmsnorm", "smx_layernorm", "smx_rope_tables", "smx_rope",
-    "smx_scale_mask_softmax", "smx_attention_decode", "smx_attention_prefill", "smx_silu_mul", "smx_gelu", "smx_argmax",
+    "smx_scale_mask_softmax", "smx_attention_decode", "smx_attention_prefill", "smx_silu_mul", "smx_gelu", "smx_argmax", "smx_stream_read",
     "smx_context_create", "smx_context_destroy", "smx_model_create", "smx_model_upload_tensor",
     "smx_model_finalize", "smx_model_weight_bytes", "smx_model_destroy", "smx_session_create",
     "smx_session_forward", "smx_session_generate", "smx_batch_generate", "smx_session_reset",
@@ -111,6 +111,7 @@ def load() -> ctypes.CDLL:
         "smx_silu_mul": (i32, [vp, vp, vp, i64, vp]),
         "smx_gelu": (i32, [vp, vp, i64, vp]),
         "smx_argmax": (i32, [vp, i32, vp, vp]),
+        "smx_stream_read": (i32, [vp, u64, vp]),
         "smx_sample": (i32, [vp, i32, vp, i32, ctypes.POINTER(SamplingC), ctypes.c_double, vp, vp, vp]),
         "smx_context_create": (i32, [i32, pp]),
         "smx_context_destroy": (i32, [vp]),

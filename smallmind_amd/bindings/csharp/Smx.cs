@@ -82,6 +82,7 @@ namespace SmallMind.Backends.Rocm
         [DllImport(Lib)] public static extern int smx_silu_mul(float* gateDev, float* upDev, float* yDev, long n, IntPtr stream);
         [DllImport(Lib)] public static extern int smx_gelu(float* xDev, float* yDev, long n, IntPtr stream);
         [DllImport(Lib)] public static extern int smx_argmax(float* xDev, int n, int* outDev, IntPtr stream);
+        [DllImport(Lib)] public static extern int smx_stream_read(void* srcDev, ulong bytes, IntPtr stream);
         [DllImport(Lib)] public static extern int smx_sample(float* logitsDev, int n, int* contextDev, int nContext,
             in Sampling p, double u, float* probsDev, int* tokenDev, IntPtr stream);
 

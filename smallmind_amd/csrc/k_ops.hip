@@ -1007,6 +1007,23 @@ hipError_t launch_gelu(const float *x, float *y, int64_t n, hipStream_t s)
     return hipGetLastError();
 }
 
+// Streaming read of one device range (16-byte loads, 8 per thread in flight; the values only
+// feed an empty asm statement): the HBM read ceiling the GEMV is measured against.
+__global__ __launch_bounds__(256) void k_stream_read(Prefetch pf) { prefetch_slice(pf, (int)blockIdx.x, (int)gridDim.x, 256); }
+
+hipError_t launch_stream_read(const void *src, uint64_t bytes, hipStream_t s)
+{
+    if (!src || bytes == 0 || bytes % 16 || bytes >= (1ull << 32)) return hipErrorInvalidValue;
+    Prefetch pf{};
+    pf.p[0] = (const uint8_t *)src;
+    pf.bytes[0] = (uint32_t)bytes;
+    pf.n = 1;
+    // one workgroup per 16 KB, 256 to 4096 workgroups
+    const uint64_t wgs = bytes / 16384 < 256 ? 256 : bytes / 16384 > 4096 ? 4096 : bytes / 16384;
+    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)wgs), dim3(256), 0, s, pf);
+    return hipGetLastError();
+}
+
 hipError_t launch_argmax(const float *x, int n, int32_t *out, int32_t *tokens, int32_t *pos,
                          hipStream_t s)
 {

@@ -1380,6 +1380,14 @@ SMX_API int smx_argmax(const float *x, int n, int32_t *out, void *stream)
     return SMX_OK;
 }
 
+SMX_API int smx_stream_read(const void *src, uint64_t bytes, void *stream)
+{
+    if (!src || bytes == 0 || bytes % 16 || bytes >= (1ull << 32))
+        SMX_FAIL(SMX_EINVAL, "smx_stream_read: need a device pointer and 0 < bytes < 4 GiB, a multiple of 16");
+    SMX_HIP(launch_stream_read(src, bytes, (hipStream_t)stream));
+    return SMX_OK;
+}
+
 SMX_API int smx_sample(const float *logits, int n, const int32_t *context, int n_context, const smx_sampling *p,
                        double u, float *probs, int32_t *token, void *stream)
 {

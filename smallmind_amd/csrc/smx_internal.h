@@ -308,6 +308,8 @@ hipError_t launch_sample_step(const float *logits, int n, int32_t *tokens, int32
                               float *probs, hipStream_t s);
 hipError_t launch_silu_mul(const float *g, const float *u, float *y, int64_t n, hipStream_t s);
 hipError_t launch_gelu(const float *x, float *y, int64_t n, hipStream_t s);
+// Reads bytes (a multiple of 16, < 4 GiB) of device memory and discards them (smx_stream_read).
+hipError_t launch_stream_read(const void *src, uint64_t bytes, hipStream_t s);
 hipError_t launch_argmax(const float *x, int n, int32_t *out, int32_t *tokens, int32_t *pos,
                          hipStream_t s);
 // Argmax over n (value, index) pairs, lowest index on ties; same outputs as launch_argmax.

@@ -197,3 +197,21 @@ def test_sample_vs_oracle(gpu, n, opts):
         cdf = np.cumsum(op.astype(np.float64))
         if np.min(np.abs(cdf - u)) > 2e-4:
             assert tok == otok, (u, tok, otok)
+
+
+def test_stream_read_runs_and_checks_its_size(gpu):
+    """smx_stream_read (the bench's streaming-read ceiling) reads device memory without writing
+    it, and refuses sizes that are not a positive multiple of 16 bytes."""
+    import torch
+
+    from smallmind_amd._lib import SmxError, call
+    buf = torch.arange(1 << 18, dtype=torch.int32, device="cuda")
+    before = buf.clone()
+    s = torch.cuda.current_stream().cuda_stream
+    for n in (16, 4096, buf.numel() * 4):
+        call("smx_stream_read", buf.data_ptr(), n, s)
+    torch.cuda.synchronize()
+    assert torch.equal(buf, before)
+    for n in (0, 24, 4095):
+        with pytest.raises(SmxError):
+            call("smx_stream_read", buf.data_ptr(), n, s)
