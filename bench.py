@@ -275,8 +275,9 @@ def copy_calibration(n_bytes: int = 1 << 30, reps: int = 5):
 def cpu_baseline(kept, wl, budget_s: float = 12.0):
     """The oracle on the host's cores, on the headline workload's positions: the 511 prompt
     tokens are prefilled (all cores, untimed), then decode steps from position 511 on are timed
-    -- first the reference-faithful way (fp32 weights dequantized at load, GEMV on one thread,
-    BASELINE.md mode R), then on every core (mode A: the same fp32 arithmetic over all threads).
+    -- first the reference-faithful way (fp32 weights dequantized at load, the single-threaded
+    M = 1 GEMV of MatMulOps.cs:1176), then on every core (the same fp32 arithmetic over all
+    threads; not the reference's threading).
     Each mode runs about budget_s seconds."""
     import numpy as np
 
@@ -339,7 +340,9 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each box has one "
-              "MI355X; see DESIGN.md for how the path would shard).", file=sys.stderr)
+              "MI355X). A single session would shard as tensor parallelism (QKV and gate/up rows "
+              "split, O and down split over K with two 8 KB all-reduces per layer); independent "
+              "sessions as data parallelism.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
