@@ -47,12 +47,18 @@ __device__ __forceinline__ void attention_head(const float *__restrict__ qh, con
 
     // K and V of one KV head span less than 4 GiB, so every load is a uniform base plus a
     // 32-bit byte offset (no 64-bit address per load held in registers).
-    const char *Kb = (const char *)K, *Vb = (const char *)V;
+    // The pointers are cast to the global address space: global loads are counted by the
+    // vector-memory counter alone (flat loads also by the LDS counter), so the waits for the
+    // LDS reads of q do not also wait for every K load in flight.
+    typedef const __attribute__((address_space(1))) char gchar;
+    typedef const __attribute__((address_space(1))) float gfloat;
+    typedef float gf4 __attribute__((ext_vector_type(4)));
+    gchar *Kb = (gchar *)K, *Vb = (gchar *)V;
     float mx = -INFINITY;
     for (int j = tid; j < n_pos; j += NT) {
         float kv[HD];
 #pragma unroll
-        for (int e = 0; e < HD; e++) kv[e] = *(const float *)(Kb + 4u * ((uint32_t)e * (uint32_t)ctx_stride + (uint32_t)j));
+        for (int e = 0; e < HD; e++) kv[e] = *(gfloat *)(Kb + 4u * ((uint32_t)e * (uint32_t)ctx_stride + (uint32_t)j));
         // q is read from LDS (broadcast) at each use: held in registers across the position
         // loop it would take HD VGPRs and, at 1024 threads, force the K loads to serialize.
         int z = 0;
@@ -92,8 +98,9 @@ __device__ __forceinline__ void attention_head(const float *__restrict__ qh, con
         for (int u = 0; u < U; u++) {
             const int j = j0 + u * NPL;
             const bool ok = j < n_pos;
-            vv[u] = ok ? *(const float4 *)(Vb + 16u * ((uint32_t)j * (HD / 4) + (uint32_t)c4))
-                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const gf4 t = ok ? *(const __attribute__((address_space(1))) gf4 *)(Vb + 16u * ((uint32_t)j * (HD / 4) + (uint32_t)c4))
+                             : gf4{0.0f, 0.0f, 0.0f, 0.0f};
+            vv[u] = make_float4(t.x, t.y, t.z, t.w);
             pp[u] = ok ? sc[j] : 0.0f;
         }
 #pragma unroll
