@@ -289,13 +289,26 @@ __device__ __forceinline__ float accumulate2(float acc, float sc, float sc2, flo
 }
 constexpr uint32_t kOnes = 0x3F803F80u;   // bf16 1.0 pair
 
+// Inputs of the EPI_QKV epilogue for one (token, row) value, loaded by the caller ahead of the
+// epilogue: the token's position, the RoPE factors of the row's pair (when it is rotated) and
+// the token's K or V cache base (for K / V rows).
+struct QkvPre {
+    int pos;
+    float c, sn;
+    float *cache;
+};
+
 // Epilogue of one output value per (token, weight row); all lanes of the wave must call it
 // (adjacent weight rows are exchanged with DPP for the paired SwiGLU / RoPE epilogues).
 // Returns the new residual value for EPI_RESID with a.np set (0 for rows / tokens outside the
 // output), else 0.  With pre, EPI_RESID takes the residual and the next norm's gamma from
-// pres / pg (loaded by the caller at kernel entry) instead of loading them here.
+// pres / pg, and EPI_QKV its position, RoPE factors and cache base from qp (all loaded by the
+// caller before the epilogue) instead of loading them here, so the epilogue's stores do not
+// wait for loads: vector-memory waits count stores as well, so a load between two stores
+// would also wait for the first store.
 __device__ __forceinline__ float qgemm_epilogue(const QgemmArgs &a, float v, uint32_t row, int tok, bool live,
-                                                bool pre = false, float pres = 0.0f, float pg = 0.0f)
+                                                bool pre = false, float pres = 0.0f, float pg = 0.0f,
+                                                QkvPre qp = QkvPre{0, 0.0f, 0.0f, nullptr})
 {
     const uint32_t N = (uint32_t)a.w.rows;
     if (a.bias && row < N) v = v + a.bias[row];
@@ -329,11 +342,12 @@ __device__ __forceinline__ float qgemm_epilogue(const QgemmArgs &a, float v, uin
     case EPI_QKV: {
         if (row & 1) break;
         const int d = a.d_model, kv = a.kv_dim, hd = a.head_dim, r = (int)row;
-        const int pos = a.tok_pos[tok];
+        const int pos = pre ? qp.pos : a.tok_pos[tok];
         float v0 = v, v1 = nb;
         if (a.use_rope && r < d + kv) {
             const int pair = ((r < d ? r : r - d) % hd) / 2, half = hd / 2;
-            const float c = a.rope_cos[(int64_t)pos * half + pair], sn = a.rope_sin[(int64_t)pos * half + pair];
+            const float c = pre ? qp.c : a.rope_cos[(int64_t)pos * half + pair];
+            const float sn = pre ? qp.sn : a.rope_sin[(int64_t)pos * half + pair];
             const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;   // RotaryEmbedding.cs:115-116
             v0 = t0 - t1;
             v1 = t2 + t3;
@@ -342,12 +356,12 @@ __device__ __forceinline__ float qgemm_epilogue(const QgemmArgs &a, float v, uin
             yr[r] = v0;
             yr[r + 1] = v1;
         } else if (r < d + kv) {
-            float *dst = a.kc_tok[tok] + a.layer_off + (int64_t)(r - d) * a.ctx_stride + pos;
+            float *dst = (pre ? qp.cache : a.kc_tok[tok]) + a.layer_off + (int64_t)(r - d) * a.ctx_stride + pos;
             dst[0] = v0;
             dst[a.ctx_stride] = v1;
         } else {
             const int vr = r - d - kv;
-            float *dst = a.vc_tok[tok] + a.layer_off + ((int64_t)(vr / hd) * a.ctx_stride + pos) * hd + (vr % hd);
+            float *dst = (pre ? qp.cache : a.vc_tok[tok]) + a.layer_off + ((int64_t)(vr / hd) * a.ctx_stride + pos) * hd + (vr % hd);
             dst[0] = v0;
             dst[1] = v1;
         }
@@ -737,15 +751,24 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
     }
 
     // EPI_RESID with one 16 x 16 tile per wave: wave 0's residual values (and the next norm's
-    // gamma) are requested at entry, so the epilogue waits for no load
+    // gamma) are requested at entry, so the epilogue waits for no load.  EPI_QKV likewise: the
+    // positions of wave 0's tokens at entry, their RoPE factors and cache bases (which depend
+    // on the positions) right after the main loop, ahead of the cross-wave reduction.
     constexpr bool PRE = TT == 1 && RT == 1;
-    const bool pre = PRE && a.epi == EPI_RESID;
+    const bool pre = PRE && (a.epi == EPI_RESID || a.epi == EPI_QKV);
+    const bool preq = PRE && a.epi == EPI_QKV;
     float pres[4] = {0.0f, 0.0f, 0.0f, 0.0f}, pg = 0.0f;
+    QkvPre qp[4] = {};
     if (pre && wv == 0) {
         const uint32_t rc = min(row_base + (uint32_t)li, N - 1);
+        if (preq) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) pres[i] = a.y[(int64_t)min(tt0 * 16 + 4 * g + i, M - 1) * a.y_stride + rc];
-        if (a.np) pg = a.ngamma[rc];
+            for (int i = 0; i < 4; i++) qp[i].pos = a.tok_pos[min(tt0 * 16 + 4 * g + i, M - 1)];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) pres[i] = a.y[(int64_t)min(tt0 * 16 + 4 * g + i, M - 1) * a.y_stride + rc];
+            if (a.np) pg = a.ngamma[rc];
+        }
     }
 
     // staging loads of one super-block: piece p -> (row p / (kBytes/16), 16-byte column)
@@ -881,6 +904,19 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
         }
     }
 
+    if (preq && wv == 0) {
+        const int d = a.d_model, kv = a.kv_dim, hd = a.head_dim, half = hd / 2;
+        const int r = (int)min(row_base + (uint32_t)li, N - 1);
+        const int pair = ((r < d ? r : r - d) % hd) / 2;
+        const bool rot = a.use_rope && r < d + kv && !(r & 1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tk = min(tt0 * 16 + 4 * g + i, M - 1);
+            qp[i].c = rot ? a.rope_cos[(int64_t)qp[i].pos * half + pair] : 0.0f;
+            qp[i].sn = rot ? a.rope_sin[(int64_t)qp[i].pos * half + pair] : 0.0f;
+            qp[i].cache = r < d ? nullptr : (r < d + kv ? a.kc_tok[tk] : a.vc_tok[tk]);
+        }
+    }
     if (fold) {   // r = 1 / sqrt(sum x^2 / K + eps) (RMSNormOps.cs:114)
 #pragma unroll
         for (int j = 0; j < RJ; j++) {
@@ -921,7 +957,8 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
             const uint32_t row = row_base + 16 * r + li;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float xn = qgemm_epilogue(a, v[i] * rs[i], row, (tt0 + t) * 16 + 4 * g + i, true, pre, pres[i], pg);
+                const float xn = qgemm_epilogue(a, v[i] * rs[i], row, (tt0 + t) * 16 + 4 * g + i, true, pre, pres[i], pg,
+                                                qp[i]);
                 sq[t][i] = xn * xn;
             }
         }
