@@ -747,17 +747,19 @@ __global__ __launch_bounds__(kThreads) void k_argmax_embed(const float *__restri
     for (int k = 1; k < kWaves; k++)
         if (bv[k] > best || (bv[k] == best && bi[k] < bidx)) { best = bv[k]; bidx = bi[k]; }
     if (bidx == 0x7FFFFFFF) bidx = 0;
-    if (threadIdx.x == 0) {
-        if (out) *out = bidx;
-        tokens[p + 1] = bidx;
-        *pos = p + 1;
-    }
     int64_t tok = bidx;
     if (tok < 0 || tok >= w.rows) tok = 0;
     // the learned position row of the next position (clamped: after the last step of a full
     // context it is never used)
     const int64_t prow = has_pos ? (p + 1 < pw.rows ? p + 1 : pw.rows - 1) : 0;
     embed_row(w, tok, x_next, pw, has_pos != 0, prow);
+    // token and position stores last: a wait for the embedding row's loads also waits for
+    // every earlier store of the wave (the vector-memory counter counts both)
+    if (threadIdx.x == 0) {
+        if (out) *out = bidx;
+        tokens[p + 1] = bidx;
+        *pos = p + 1;
+    }
 }
 
 // Embedding rows of a token batch: x[t] = emb[tok[t]] (+ pos_emb[pos[t]]), one workgroup per
