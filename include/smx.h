@@ -36,7 +36,11 @@ enum smx_status {
     SMX_EBUSY = -4,         /* session already in use on another thread (InferenceSession.cs:127-144) */
     SMX_EUNSUPPORTED = -5,  /* tensor type or shape the backend does not implement */
     SMX_ESTATE = -6,        /* call out of order (e.g. model not finalized) */
-    SMX_ERANGE = -7         /* position / token out of range (TransformerModel.cs:282-285) */
+    SMX_ERANGE = -7,        /* position / token out of range (TransformerModel.cs:282-285) */
+    SMX_ECANCELED = -8,     /* generation stopped by smx_session_cancel (the OperationCanceledException of
+                               InferenceSession's CancellationToken checks, InferenceSession.cs:211, :481) */
+    SMX_ETIMEDOUT = -9      /* generation stopped at the session's time limit (InferenceTimeoutException,
+                               InferenceSession.cs:164-172, :287-291) */
 };
 
 /* GGUF tensor type ids (src/SmallMind.Quantization/IO/Gguf/GgufTensorType.cs:6-52). */
@@ -283,7 +287,10 @@ SMX_API int smx_model_destroy(smx_model *m);
  * n_steps steps for all members at once (one token each, at each member's own position)
  * and writes out_tokens[member][n_steps] in member order: members keep the order they were added
  * in, a removal closes the gap.  Members may join and leave between steps.  The model cannot be
- * destroyed while a batcher exists. */
+ * destroyed while a batcher exists.  Before each step smx_batcher_step checks every member's cancel
+ * request and time limit: on one it stops after the steps already run, returns SMX_ECANCELED /
+ * SMX_ETIMEDOUT with those steps' tokens in out_tokens (the rest -1), and every member stays a
+ * member (a timed-out member stays timed out until removed). */
 typedef struct smx_batcher smx_batcher;
 SMX_API int smx_batcher_create(smx_model *m, int max_members, int max_ctx, smx_batcher **out);
 SMX_API int smx_batcher_add(smx_batcher *b, smx_session *s, const int32_t *prompt, int n_prompt);
@@ -304,14 +311,40 @@ SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out);
 SMX_API int smx_session_forward(smx_session *s, const int32_t *tokens, int n_tokens,
                                 int pos_offset, float *logits_out);
 /* Greedy generation entirely on the device: prefill the prompt, then n_new tokens by argmax.
- * out_tokens (host, n_new).  logits_out (host, n_new*vocab) may be NULL. */
+ * out_tokens (host, n_new).  logits_out (host, n_new*vocab) may be NULL.
+ * A prompt longer than the session context is cropped to its last max_ctx tokens, as
+ * InferenceSession crops the context before prefill (InferenceSession.cs:494-508); the n_new
+ * tokens must then fit: cropped length + n_new - 1 <= max_ctx, else SMX_ERANGE (the block-size
+ * check of TransformerModel.cs:280-283 that a later decode step would fail).
+ * The host checks, before the prefill and between graph launches (every 8 tokens at most), for
+ * a cancel request (smx_session_cancel) and the session's time limit (smx_session_set_max_time).
+ * On either it stops, and returns SMX_ECANCELED or SMX_ETIMEDOUT: out_tokens then holds the k
+ * tokens produced so far (the first k tokens of the uninterrupted run) followed by -1, and
+ * stats->n_decode_steps = k.  The session is left as after a generation of k tokens (untouched
+ * when the stop comes before the prefill). */
 SMX_API int smx_session_generate(smx_session *s, const int32_t *prompt, int n_prompt, int n_new,
                                  int32_t *out_tokens, float *logits_out, smx_gen_stats *stats);
+/* Requests that the generation running on the session stop (the CancellationToken that
+ * InferenceSession.GenerateAsync checks before every token, InferenceSession.cs:211, :481).
+ * Callable from any thread, also while another thread is inside a call on s; it takes no lock
+ * and touches no device state.  The request stays set until a generation call on s observes it
+ * (smx_session_generate, smx_session_generate_sampled, smx_batch_generate, smx_batcher_step of a
+ * batcher s belongs to): that call returns SMX_ECANCELED and clears it, so a request made
+ * while no call runs cancels the next one at its first check, as an already-cancelled token does.
+ * smx_session_reset clears it too.  s must stay alive for the duration of the call. */
+SMX_API int smx_session_cancel(smx_session *s);
+/* The MaxTimeMs limit (ProductionInferenceOptions.cs:124, applied at InferenceSession.cs:164-172):
+ * a generation call on s that is still running max_time_ms after it started stops at its next
+ * check with SMX_ETIMEDOUT.  For a batcher member the clock starts when it joins.  0 = no limit
+ * (the default); negative values give SMX_EINVAL, as ProductionInferenceOptions.Validate
+ * (ProductionInferenceOptions.cs:188-190).  Callable from any thread. */
+SMX_API int smx_session_set_max_time(smx_session *s, int32_t max_time_ms);
 /* Generation with the reference's sampling pipeline (InferenceSession.GenerateNextTokenAsync,
  * InferenceSession.cs:478-606) on the device: as smx_session_generate, but every new token is
  * drawn by the stages of smx_sample over the context so far (prompt and generated tokens), with
  * draw i = the top 53 bits of splitmix64(seed + i) as a double in [0, 1) (the reference draws
- * from System.Random, which is not reproduced).  SMX_EINVAL on a persistent-decode session. */
+ * from System.Random, which is not reproduced).  Prompt cropping, cancellation and the time limit
+ * as in smx_session_generate (checks between tokens). */
 SMX_API int smx_session_generate_sampled(smx_session *s, const int32_t *prompt, int n_prompt, int n_new,
                                          const smx_sampling *params, uint64_t seed, int32_t *out_tokens,
                                          float *logits_out, smx_gen_stats *stats);
@@ -321,7 +354,9 @@ SMX_API int smx_session_generate_sampled(smx_session *s, const int32_t *prompt, 
  * BatchedInferenceEngine, InferenceSession.cs:478-546 per session).  prompts holds the prompts
  * back to back, prompt_lens[i] tokens for session i; out_tokens is [n_sessions][n_new] (host).
  * The sessions must be distinct, share one model and have the same max_ctx; each ends as
- * smx_session_generate would leave it.  stats (may be NULL) sums the prefill steps. */
+ * smx_session_generate would leave it.  stats (may be NULL) sums the prefill steps.  A cancel
+ * request or time limit of any listed session stops all of them between steps (SMX_ECANCELED /
+ * SMX_ETIMEDOUT, the first k tokens of every session in out_tokens, the rest -1). */
 SMX_API int smx_batch_generate(smx_session *const *sessions, int n_sessions, const int32_t *prompts,
                                const int32_t *prompt_lens, int n_new, int32_t *out_tokens,
                                smx_gen_stats *stats);

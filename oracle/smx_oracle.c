@@ -1396,8 +1396,14 @@ static int64_t now_ns(void)
 int smxo_generate_greedy(smxo_model *m, const int32_t *prompt, int n_prompt, int n_new,
                          int32_t *out_tokens, int64_t *prefill_ns, int64_t *decode_ns)
 {
+    /* InferenceSession.GenerateNextTokenAsync crops the context to its last blockSize tokens
+     * before the prefill (InferenceSession.cs:494-508) */
+    if (n_prompt > m->ctx) {
+        prompt += n_prompt - m->ctx;
+        n_prompt = m->ctx;
+    }
     if (n_prompt <= 0 || n_new <= 0 || n_prompt + n_new - 1 > m->ctx) return -1;
-    smxo_session *s = smxo_session_create(m, n_prompt + n_new);
+    smxo_session *s = smxo_session_create(m, n_prompt + n_new - 1);
     if (!s) return -2;
     float *logits = (float *)malloc(sizeof(float) * (size_t)m->vocab);
     int64_t t0 = now_ns();

@@ -16,7 +16,9 @@ F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 8, 12, 13, 14
 ARCH_LLAMA, ARCH_GPT2 = 0, 1
 
 STATUS = {0: "SMX_OK", -1: "SMX_EINVAL", -2: "SMX_ENOMEM", -3: "SMX_EDEVICE", -4: "SMX_EBUSY",
-          -5: "SMX_EUNSUPPORTED", -6: "SMX_ESTATE", -7: "SMX_ERANGE"}
+          -5: "SMX_EUNSUPPORTED", -6: "SMX_ESTATE", -7: "SMX_ERANGE", -8: "SMX_ECANCELED",
+          -9: "SMX_ETIMEDOUT"}
+ECANCELED, ETIMEDOUT = -8, -9
 
 # Every function include/smx.h declares.
 EXPORTS = [
@@ -28,7 +30,8 @@ EXPORTS = [
     "smx_scale_mask_softmax", "smx_attention_decode", "smx_attention_prefill", "smx_silu_mul", "smx_gelu", "smx_argmax", "smx_stream_read",
     "smx_context_create", "smx_context_destroy", "smx_model_create", "smx_model_upload_tensor",
     "smx_model_finalize", "smx_model_weight_bytes", "smx_model_destroy", "smx_session_create",
-    "smx_session_forward", "smx_session_generate", "smx_batch_generate", "smx_session_reset",
+    "smx_session_forward", "smx_session_generate", "smx_session_cancel", "smx_session_set_max_time",
+    "smx_batch_generate", "smx_session_reset",
     "smx_session_destroy", "smx_model_load_gguf", "smx_gguf_read_config", "smx_model_load_smq",
     "smx_smq_read_config", "smx_smq_pack", "smx_sample",
     "smx_session_generate_sampled", "smx_batcher_create", "smx_batcher_add", "smx_batcher_add_sampled", "smx_batcher_remove",
@@ -40,6 +43,19 @@ class SmxError(RuntimeError):
     def __init__(self, func: str, code: int, msg: str):
         super().__init__(f"{func} -> {STATUS.get(code, code)}: {msg}")
         self.code = code
+
+
+class GenerationCancelled(SmxError):
+    """SMX_ECANCELED: the generation stopped on a cancel request (the OperationCanceledException
+    of InferenceSession's CancellationToken, InferenceSession.cs:211, :481).  `tokens` holds what
+    was produced before the stop (the first tokens of the uninterrupted run)."""
+    tokens = None
+
+
+class GenerationTimeout(SmxError):
+    """SMX_ETIMEDOUT: the generation stopped at the session's time limit (InferenceTimeoutException,
+    InferenceSession.cs:164-172, :287-291).  `tokens` holds what was produced before the stop."""
+    tokens = None
 
 
 class ModelConfigC(ctypes.Structure):
@@ -129,6 +145,8 @@ def load() -> ctypes.CDLL:
         "smx_session_create": (i32, [vp, i32, pp]),
         "smx_session_forward": (i32, [vp, vp, i32, i32, vp]),
         "smx_session_generate": (i32, [vp, vp, i32, i32, vp, vp, ctypes.POINTER(GenStatsC)]),
+        "smx_session_cancel": (i32, [vp]),
+        "smx_session_set_max_time": (i32, [vp, ctypes.c_int32]),
         "smx_batch_generate": (i32, [vp, i32, vp, vp, i32, vp, ctypes.POINTER(GenStatsC)]),
         "smx_session_generate_sampled": (i32, [vp, vp, i32, i32, ctypes.POINTER(SamplingC), ctypes.c_uint64, vp, vp,
                                                ctypes.POINTER(GenStatsC)]),
@@ -151,9 +169,11 @@ def load() -> ctypes.CDLL:
 
 
 def call(name: str, *args) -> int:
-    """Calls a status-returning C-ABI function and raises SmxError on failure."""
+    """Calls a status-returning C-ABI function and raises SmxError on failure (GenerationCancelled
+    / GenerationTimeout for a stopped generation)."""
     L = load()
     rc = getattr(L, name)(*args)
     if rc != 0:
-        raise SmxError(name, rc, (L.smx_last_error() or b"").decode(errors="replace"))
+        cls = {ECANCELED: GenerationCancelled, ETIMEDOUT: GenerationTimeout}.get(rc, SmxError)
+        raise cls(name, rc, (L.smx_last_error() or b"").decode(errors="replace"))
     return rc

@@ -6,8 +6,13 @@
 // KV cache (TransformerModel.cs:272-344, ResetKVCache :476-506), InferenceSession's sampling
 // options (ProductionInferenceOptions.cs:19-87).
 using System;
+using System.Collections.Generic;
+using System.Diagnostics;
 using System.Runtime.InteropServices;
+using System.Threading;
+using SmallMind.Core.Exceptions;
 using SmallMind.Quantization.Abstractions;
+using SmallMind.Runtime.Cache;
 using SmallMind.Runtime.Execution;
 
 namespace SmallMind.Backends.Rocm
@@ -17,7 +22,7 @@ namespace SmallMind.Backends.Rocm
         const string Lib = "smx";   // resolves libsmx.so
 
         public const int OK = 0, EINVAL = -1, ENOMEM = -2, EDEVICE = -3, EBUSY = -4,
-                         EUNSUPPORTED = -5, ESTATE = -6, ERANGE = -7;
+                         EUNSUPPORTED = -5, ESTATE = -6, ERANGE = -7, ECANCELED = -8, ETIMEDOUT = -9;
         public const int F32 = 0, F16 = 1, Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14;
         // SMQ Q8Tensor / Q4Tensor blocks in their upload layout (smx_smq_pack)
         public const int SMQ_Q8 = 1010, SMQ_Q4 = 1011;
@@ -112,6 +117,9 @@ namespace SmallMind.Backends.Rocm
             int posOffset, float* logitsOut);
         [DllImport(Lib)] public static extern int smx_session_generate(IntPtr session, int* prompt, int nPrompt, int nNew,
             int* outTokens, float* logitsOut, GenStats* stats);
+        // callable from any thread while another thread is inside a generate call on the session
+        [DllImport(Lib)] public static extern int smx_session_cancel(IntPtr session);
+        [DllImport(Lib)] public static extern int smx_session_set_max_time(IntPtr session, int maxTimeMs);
         [DllImport(Lib)] public static extern int smx_session_generate_sampled(IntPtr session, int* prompt,
             int nPrompt, int nNew, in Sampling p, ulong seed, int* outTokens, float* logitsOut, GenStats* stats);
         [DllImport(Lib)] public static extern int smx_batch_generate(IntPtr* sessions, int nSessions, int* prompts,
@@ -129,8 +137,9 @@ namespace SmallMind.Backends.Rocm
         [DllImport(Lib)] public static extern int smx_session_reset(IntPtr session);
         [DllImport(Lib)] public static extern int smx_session_destroy(IntPtr session);
 
-        // Status -> the exception the reference throws at the same point.
-        public static void Check(int rc)
+        // Status -> the exception the reference throws at the same point.  maxTimeMs is the
+        // session's time limit, reported by InferenceTimeoutException (InferenceSession.cs:287-291).
+        public static void Check(int rc, int maxTimeMs = 0)
         {
             if (rc == OK) return;
             string msg = Marshal.PtrToStringUTF8(smx_last_error()) ?? "libsmx error";
@@ -139,18 +148,25 @@ namespace SmallMind.Backends.Rocm
                 EINVAL => new ArgumentException(msg),            // Q8WeightTensor.cs:43-48
                 ERANGE => new ArgumentOutOfRangeException(msg),  // TransformerModel.cs:282-285
                 EBUSY => new InvalidOperationException(msg),     // InferenceSession.cs:127-144
+                ECANCELED => new OperationCanceledException(msg),   // InferenceSession.cs:211, :481
+                ETIMEDOUT => new InferenceTimeoutException(maxTimeMs, msg),   // InferenceSession.cs:287-291
                 _ => new InvalidOperationException(msg),
             };
         }
     }
 
     // IWeightTensor (IWeightTensor.cs:7-42) on the device, injected through
-    // Linear.SetQuantizedWeight (NeuralNet.cs:84-107).  The reference checks k == Rows and
-    // n == Cols (Q8WeightTensor.cs:43-48): Rows = input features, Cols = output features.  The
-    // device matrix holds the GGUF [out][in] rows, and the library computes
-    // output[m][n] = activations[m][k] . W[n][k]^T, the product the reference defines for its
-    // [k][n] weight.  Operands stay in host memory; libsmx.so stages them on the device itself
-    // (kept per weight, so repeated calls allocate nothing).
+    // Linear.SetQuantizedWeight (NeuralNet.cs:84-107).  That injection checks
+    // Rows == outFeatures and Cols == inFeatures (NeuralNet.cs:89), and Linear.ForwardQuantized then
+    // calls MatMul(input, output, m, k: inFeatures, n: outFeatures) (NeuralNet.cs:168-173, :211-216),
+    // so this tensor reports Rows = output features, Cols = input features and accepts
+    // k == Cols, n == Rows.  (IWeightTensor.cs:31-32 documents k == Rows and n == Cols, which the
+    // reference's own Q8WeightTensor checks (Q8WeightTensor.cs:43-44); for a non-square layer the two
+    // reference checks cannot both hold, and this class follows the one Linear enforces.)  The device
+    // matrix holds the GGUF [out][in] rows, and the library computes
+    // output[m][n] = activations[m][k] . W[n][k]^T.  ToFloat32 returns Rows x Cols = [out][in].
+    // Operands stay in host memory; libsmx.so stages them on the device itself (kept per weight, so
+    // repeated calls allocate nothing).
     internal sealed unsafe class GpuWeightTensor : IWeightTensor, IDisposable
     {
         readonly IntPtr _w;
@@ -166,15 +182,17 @@ namespace SmallMind.Backends.Rocm
                 Smx.Check(Smx.smx_weight_create(ggmlType, outFeatures, inFeatures, p, 0, out _w));
         }
 
-        public int Rows => _in;
-        public int Cols => _out;
+        public int Rows => _out;
+        public int Cols => _in;
         public QuantScheme Scheme { get; }
 
         public void MatMul(ReadOnlySpan<float> activations, Span<float> output, int m, int k, int n)
         {
-            if (k != Rows) throw new ArgumentException($"k={k} must equal Rows={Rows}");   // Q8WeightTensor.cs:43-48
-            if (n != Cols) throw new ArgumentException($"n={n} must equal Cols={Cols}");
-            if (activations.Length < m * k || output.Length < m * n) throw new ArgumentException("span too short");
+            if (k != Cols) throw new ArgumentException($"k={k} must equal Cols={Cols} (input features)");
+            if (n != Rows) throw new ArgumentException($"n={n} must equal Rows={Rows} (output features)");
+            if (activations.Length < m * k)
+                throw new ArgumentException($"activations.Length {activations.Length} < m*k {m * k}");
+            if (output.Length < m * n) throw new ArgumentException($"output.Length {output.Length} < m*n {m * n}");
             fixed (float* a = activations)
             fixed (float* o = output)
                 Smx.Check(Smx.smx_weight_matmul_host(_w, a, o, m, k, n));   // output fully overwritten
@@ -182,7 +200,7 @@ namespace SmallMind.Backends.Rocm
 
         public float[] ToFloat32()
         {
-            var r = new float[_in * _out];   // [out][in] rows, bit-identical to GgufModelLoader's dequantization
+            var r = new float[_out * _in];   // [Rows = out][Cols = in], bit-identical to GgufModelLoader's dequantization
             fixed (float* o = r)
                 Smx.Check(Smx.smx_weight_to_float32_host(_w, o));
             return r;
@@ -191,45 +209,114 @@ namespace SmallMind.Backends.Rocm
         public void Dispose() => Smx.smx_weight_destroy(_w);
     }
 
-    // IRuntimeExecutor (Execution/IRuntimeExecutor.cs) on the device: RuntimeExecutor's Prefill
-    // and Decode (RuntimeExecutor.cs:40-178) are TransformerModel.Forward calls at position 0 and
-    // at context.CurrentPosition with the KV cache on; here each is one smx_session_forward on the
-    // session that stands for the context's cache (smx_session_reset = ResetKVCache).
-    internal sealed unsafe class GpuRuntimeExecutor : IDisposable
+    // IRuntimeExecutor (Execution/IRuntimeExecutor.cs:8-27) on the device, in place of
+    // RuntimeExecutor (RuntimeExecutor.cs:13-178).  Compiled into SmallMind.Runtime, whose internal
+    // types it implements and constructs.  Prefill follows RuntimeExecutor.Prefill step by step: the
+    // same argument and state checks, the prompt cropped to its last blockSize tokens (:55-57), the
+    // forward at position 0, a KvCacheHandle rented from the pool and stored in the context,
+    // context.CurrentPosition = the processed length, and PrefillMetrics from a stopwatch.  The KV
+    // cache itself is a device session (smx_session) keyed to that handle: the rented entry is a
+    // zero-layer placeholder (ModelShape(0, heads, headDim)), so it holds no host K/V arrays.
+    // Decode reads context.CurrentPosition, runs one token on the handle's session and advances the
+    // position, as RuntimeExecutor.Decode does (:117-176).
+    internal sealed unsafe class GpuRuntimeExecutor : IRuntimeExecutor, IDisposable
     {
-        readonly GpuSession _session;
-        readonly int _blockSize, _vocab;
+        readonly GpuTransformerBackend _backend;
+        readonly KvCachePool _cachePool;
+        readonly int _blockSize, _vocab, _heads, _headDim;
+        readonly Dictionary<KvCacheHandle, GpuSession> _sessions = new(ReferenceEqualityComparer.Instance);
 
-        public GpuRuntimeExecutor(GpuTransformerBackend backend, int blockSize, int vocabSize)
+        public GpuRuntimeExecutor(GpuTransformerBackend backend, KvCachePool cachePool, int blockSize, int vocabSize,
+                                  int numHeads, int headDim)
         {
-            _session = backend.CreateSession(blockSize);
+            _backend = backend ?? throw new ArgumentNullException(nameof(backend));
+            _cachePool = cachePool ?? throw new ArgumentNullException(nameof(cachePool));
             _blockSize = blockSize;
             _vocab = vocabSize;
+            _heads = numHeads;
+            _headDim = headDim;
         }
 
-        // The prompt, cropped to its last blockSize tokens (RuntimeExecutor.cs:55-57), at
-        // position 0; returns the last position's logits and the number of tokens processed.
-        public (float[] logits, int processed) Prefill(ReadOnlySpan<int> promptTokens)
+        public PrefillResult Prefill(ReadOnlySpan<int> promptTokens, ExecutionContext context)
         {
-            if (promptTokens.Length == 0) throw new ArgumentException("Prompt tokens cannot be empty");
-            int start = Math.Max(0, promptTokens.Length - _blockSize);
-            var slice = promptTokens.Slice(start);
-            var logits = new float[_vocab];
-            _session.ResetKVCache();
-            _session.ForwardLastRow(slice, 0, logits);
-            return (logits, slice.Length);
+            if (context == null) throw new ArgumentNullException(nameof(context));
+            if (promptTokens.Length == 0)
+                throw new ArgumentException("Prompt tokens cannot be empty", nameof(promptTokens));
+            if (context.HasCache)
+                throw new InvalidOperationException("Context already has a cache. Call Reset() before prefill.");
+            var sw = Stopwatch.StartNew();
+            int startIdx = Math.Max(0, promptTokens.Length - _blockSize);
+            int promptLength = promptTokens.Length - startIdx;
+            var promptSlice = promptTokens.Slice(startIdx, promptLength);
+
+            var entry = _cachePool.Rent(new ModelShape(0, _heads, _headDim), _blockSize,
+                                        new SessionId(Guid.NewGuid().ToString()));
+            var handle = new KvCacheHandle(entry);
+            var session = _backend.CreateSession(_blockSize);
+            var lastLogits = new float[_vocab];
+            try
+            {
+                session.ForwardLastRow(promptSlice, 0, lastLogits);   // ResetKVCache + Forward(pos 0)
+            }
+            catch
+            {
+                session.Dispose();
+                _cachePool.Return(entry);
+                throw;
+            }
+            _sessions[handle] = session;
+            context.CacheHandle = handle;
+            context.CurrentPosition = promptLength;
+            sw.Stop();
+            var metrics = new PrefillMetrics(promptLength, sw.Elapsed.TotalMilliseconds);
+            if (context.Options.EnableTelemetry)
+                context.Telemetry.RecordPrefillEnd(promptLength, sw.Elapsed.TotalMilliseconds);
+            return new PrefillResult(new ReadOnlyMemory<float>(lastLogits), handle, promptLength, metrics);
         }
 
-        // One token at the context's current position (RuntimeExecutor.cs:125-145).
-        public float[] Decode(int nextToken, int currentPosition)
+        public DecodeResult Decode(int nextToken, ExecutionContext context)
         {
-            var logits = new float[_vocab];
+            if (context == null) throw new ArgumentNullException(nameof(context));
+            if (!context.HasCache)
+            {
+                if (context.Options.RequireKvCache)
+                    throw new InvalidOperationException(
+                        "Context does not have a cache. Call Prefill() first or disable RequireKvCache.");
+                throw new InvalidOperationException("Decode requires prefill to be called first");
+            }
+            if (!_sessions.TryGetValue(context.CacheHandle!, out var session))
+                throw new InvalidOperationException("The context's cache was not created by this executor");
+            var sw = Stopwatch.StartNew();
+            var decodedLogits = new float[_vocab];
             Span<int> t = stackalloc int[1] { nextToken };
-            _session.ForwardLastRow(t, currentPosition, logits);
-            return logits;
+            session.ForwardLastRow(t, context.CurrentPosition, decodedLogits);   // Forward(pos = CurrentPosition)
+            context.CurrentPosition++;
+            sw.Stop();
+            var metrics = new DecodeMetrics(sw.Elapsed.TotalMilliseconds, context.CurrentPosition, cacheUsed: true);
+            if (context.Options.EnableTelemetry)
+                context.Telemetry.RecordDecodeEnd(sw.Elapsed.TotalMilliseconds);
+            return new DecodeResult(new ReadOnlyMemory<float>(decodedLogits), context.CacheHandle!, metrics);
         }
 
-        public void Dispose() => _session.Dispose();
+        // Releases the device session of a context's cache (the context is then Reset or disposed).
+        public void Release(ExecutionContext context)
+        {
+            if (context?.CacheHandle is KvCacheHandle h && _sessions.Remove(h, out var session))
+            {
+                session.Dispose();
+                _cachePool.Return(h.CacheEntry);
+            }
+        }
+
+        public void Dispose()
+        {
+            foreach (var kv in _sessions)
+            {
+                kv.Value.Dispose();
+                _cachePool.Return(kv.Key.CacheEntry);
+            }
+            _sessions.Clear();
+        }
     }
 
     // The model on the device: loaded from a GGUF or .smq file in one call, or tensor by tensor.
@@ -283,14 +370,60 @@ namespace SmallMind.Backends.Rocm
                 Smx.Check(Smx.smx_session_forward(_s, t, tokens.Length, positionOffset, l));
         }
 
-        public int[] GenerateGreedy(ReadOnlySpan<int> prompt, int nNew)
+        // Greedy generation on the device.  The prompt is cropped to its last maxCtx tokens by the
+        // library (InferenceSession.cs:494-508).  The token's cancellation is forwarded to
+        // smx_session_cancel, which the library checks between graph launches; maxTimeMs is
+        // ProductionInferenceOptions.MaxTimeMs (0 = none).  A stopped generation throws
+        // OperationCanceledException / InferenceTimeoutException like GenerateAsync
+        // (InferenceSession.cs:164-172, :287-291); the tokens produced before the stop are in
+        // `produced` (the first tokens of the uninterrupted run).
+        public int[] GenerateGreedy(ReadOnlySpan<int> prompt, int nNew, CancellationToken cancellationToken = default,
+                                    int maxTimeMs = 0)
         {
+            return Generate(prompt, nNew, null, 0, cancellationToken, maxTimeMs);
+        }
+
+        // As GenerateGreedy, with the reference's sampling pipeline (InferenceSession.cs:565-606).
+        public int[] GenerateSampled(ReadOnlySpan<int> prompt, int nNew, in Smx.Sampling options, ulong seed,
+                                     CancellationToken cancellationToken = default, int maxTimeMs = 0)
+        {
+            return Generate(prompt, nNew, options, seed, cancellationToken, maxTimeMs);
+        }
+
+        int[] Generate(ReadOnlySpan<int> prompt, int nNew, Smx.Sampling? options, ulong seed,
+                       CancellationToken cancellationToken, int maxTimeMs)
+        {
+            if (maxTimeMs < 0) throw new ArgumentOutOfRangeException(nameof(maxTimeMs));
+            cancellationToken.ThrowIfCancellationRequested();
             var outTokens = new int[nNew];
-            fixed (int* p = prompt)
-            fixed (int* o = outTokens)
-                Smx.Check(Smx.smx_session_generate(_s, p, prompt.Length, nNew, o, null, null));
+            Smx.GenStats stats;
+            Smx.Check(Smx.smx_session_set_max_time(_s, maxTimeMs));
+            int rc;
+            using (cancellationToken.Register(() => Smx.smx_session_cancel(_s)))
+            {
+                fixed (int* p = prompt)
+                fixed (int* o = outTokens)
+                {
+                    if (options is Smx.Sampling so)
+                        rc = Smx.smx_session_generate_sampled(_s, p, prompt.Length, nNew, in so, seed, o, null, &stats);
+                    else
+                        rc = Smx.smx_session_generate(_s, p, prompt.Length, nNew, o, null, &stats);
+                }
+            }
+            // the registration is disposed: no callback runs from here on.  One that ran after the
+            // call had finished left its request pending, which would stop the next call; clear it
+            // (smx_session_reset only rewinds the device position, which every call sets itself).
+            if (rc == Smx.OK && cancellationToken.IsCancellationRequested) Smx.smx_session_reset(_s);
+            if (rc == Smx.ECANCELED || rc == Smx.ETIMEDOUT)
+                _produced = outTokens.AsSpan(0, stats.NDecode).ToArray();
+            Smx.Check(rc, maxTimeMs);
+            _produced = outTokens;
             return outTokens;
         }
+
+        int[] _produced = Array.Empty<int>();
+        // The tokens of the last generation, or those produced before it stopped.
+        public int[] Produced => _produced;
 
         public void ResetKVCache() => Smx.Check(Smx.smx_session_reset(_s));
 

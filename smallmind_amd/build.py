@@ -16,13 +16,12 @@ OUT = os.path.join(HERE, "libsmx.so")
 BUILD = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-# (source, object name, extra flags); the GEMV and the persistent decode kernel are built once
-# per block format so their instantiations compile in parallel.
+# (source, object name, extra flags); the GEMV is built once per block format so its
+# instantiations compile in parallel.
 SOURCES = [("k_quant.hip", "k_quant", []), ("k_ops.hip", "k_ops", []), ("runtime.cpp", "runtime", []),
-           ("decode_dispatch.cpp", "decode_dispatch", []), ("gemv_dispatch.cpp", "gemv_dispatch", []), ("k_qgemm.hip", "k_qgemm", []),
+           ("gemv_dispatch.cpp", "gemv_dispatch", []), ("k_qgemm.hip", "k_qgemm", []),
            ("k_attn_prefill.hip", "k_attn_prefill", []), ("gguf.cpp", "gguf", []), ("smq.cpp", "smq", []), ("k_sample.hip", "k_sample", [])] + [
-           ("k_gemv.hip", f"k_gemv_f{f}", [f"-DSMX_GEMV_FMT={f}"]) for f in range(9)] + [
-           ("k_decode.hip", f"k_decode_f{f}", [f"-DSMX_DECODE_FMT={f}"]) for f in range(5)]
+           ("k_gemv.hip", f"k_gemv_f{f}", [f"-DSMX_GEMV_FMT={f}"]) for f in range(9)]
 
 FLAGS = [
     "-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-fvisibility=hidden",

@@ -16,6 +16,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <map>
 #include <mutex>
 #include <memory>
@@ -296,22 +297,10 @@ struct smx_session {
     TokBatch pb;            // prefill chunks on the matrix cores (allocated on first use)
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     std::atomic<int> busy{0};
-    // persistent decode (one cooperative launch per prefill / generation)
-    bool persistent = false;
-    int grid = 0, fmt = -1;
-    size_t lds = 0;
-    DecodeArgs dargs{};
-    LayerDesc *d_layers = nullptr;
-    unsigned *bar = nullptr;
-    int *abort_flag = nullptr;
-    float *wg_val = nullptr;
-    int32_t *wg_idx = nullptr;
-    float *logits_all = nullptr;
-    size_t logits_all_cap = 0;
-    // SMX_DECODE_TRACE=<file>: barrier timestamps of the last persistent launch are appended
-    unsigned long long *trace = nullptr;
-    int trace_cap = 0;
-    std::string trace_path;
+    // generation control: smx_session_cancel sets `cancel` from any thread (the generation that
+    // observes it stops and clears it); smx_session_set_max_time sets the time limit (0 = none)
+    std::atomic<int> cancel{0};
+    std::atomic<int32_t> max_time_ms{0};
 };
 
 namespace {
@@ -484,6 +473,61 @@ int enqueue_step(smx_session *S, bool with_head, bool with_embed, hipStream_t s,
 
 constexpr int kDecodeBlock = 8;
 
+// Between graph launches a generation stops early on the caller's request: smx_session_cancel
+// (the reference checks its CancellationToken before every token, InferenceSession.cs:211,
+// :481) or the session's time limit (MaxTimeMs, InferenceSession.cs:164-172, :287-291).
+struct StopCheck {
+    std::vector<std::atomic<int> *> flags;
+    std::chrono::steady_clock::time_point deadline{};
+    bool timed = false;
+    // one deadline for the call: the smallest positive limit among the sessions
+    void add(smx_session *S, std::chrono::steady_clock::time_point t0)
+    {
+        flags.push_back(&S->cancel);
+        const int32_t ms = S->max_time_ms.load();
+        if (ms > 0) {
+            const auto d = t0 + std::chrono::milliseconds(ms);
+            if (!timed || d < deadline) deadline = d;
+            timed = true;
+        }
+    }
+    // SMX_OK to go on, else the status the call returns; a cancel request is consumed
+    int poll()
+    {
+        for (std::atomic<int> *f : flags)
+            if (f->exchange(0) != 0) return SMX_ECANCELED;
+        if (timed && std::chrono::steady_clock::now() >= deadline) return SMX_ETIMEDOUT;
+        return SMX_OK;
+    }
+};
+
+// Keeps the host at most `depth` launches ahead of the device: after each launch an event is
+// recorded, and the host waits for the one `depth` launches back.  The device always has queued
+// work, and a stop request takes effect within `depth` launches.
+class Pacer {
+    static constexpr int kRing = 16;
+    hipEvent_t ev_[kRing] = {};
+    hipStream_t s_;
+    int depth_;
+    long n_ = 0;
+
+public:
+    Pacer(hipStream_t s, int depth) : s_(s), depth_(std::min(std::max(depth, 1), kRing - 1)) {}
+    ~Pacer()
+    {
+        for (hipEvent_t e : ev_) if (e) (void)hipEventDestroy(e);
+    }
+    hipError_t launched()
+    {
+        hipEvent_t &e = ev_[n_ % kRing];
+        hipError_t r = e ? hipSuccess : hipEventCreateWithFlags(&e, hipEventDisableTiming);
+        if (r == hipSuccess) r = hipEventRecord(e, s_);
+        n_++;
+        if (r == hipSuccess && n_ > depth_) r = hipEventSynchronize(ev_[(n_ - 1 - depth_) % kRing]);
+        return r;
+    }
+};
+
 // Captures `steps` consecutive steps (steps > 1: chained decode steps) into one graph.
 int capture_step(smx_session *S, bool with_head, bool with_embed, hipGraphExec_t *out, int steps = 1,
                  bool sample = false)
@@ -502,139 +546,6 @@ int capture_step(smx_session *S, bool with_head, bool with_embed, hipGraphExec_t
     e = hipGraphInstantiate(out, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
     SMX_HIP(e);
-    return SMX_OK;
-}
-
-// Prepares the persistent decode path (one cooperative kernel per generate call) when
-// SMX_DECODE=persistent is set, the device supports cooperative launches and every layer matrix
-// shares one block format; otherwise the session uses the per-kernel graph path, which is the
-// faster of the two on MI355X (a grid-wide barrier costs about as much as a kernel boundary).
-int setup_persistent(smx_session *S)
-{
-    smx_model *m = S->m;
-    const char *mode = getenv("SMX_DECODE");
-    if (!mode || strcmp(mode, "persistent")) return SMX_OK;
-    const int fmt = m->layers[0].qkv.fmt;
-    for (const Layer &L : m->layers)
-        if (L.qkv.fmt != fmt || L.o.fmt != fmt || L.gu.fmt != fmt || L.down.fmt != fmt) return SMX_OK;
-    // the persistent kernel decodes the GGUF block formats only
-    if (m->tok.fmt > FMT_Q6_K || m->head.fmt > FMT_Q6_K || (!m->llama && m->pos.fmt > FMT_Q6_K)) return SMX_OK;
-    const size_t lds = (size_t)S->max_ctx * 4;
-    const int grid = decode_grid(fmt, m->hd, lds, m->ctx->device);
-    if (grid <= 0) return SMX_OK;
-    const smx_model_config &c = m->cfg;
-    const size_t layer_cache = (size_t)c.n_kv_head * S->ctx_stride * m->hd;
-    std::vector<LayerDesc> hl((size_t)c.n_layer);
-    for (int l = 0; l < c.n_layer; l++) {
-        const Layer &L = m->layers[l];
-        LayerDesc &D = hl[(size_t)l];
-        D.qkv = L.qkv.view();
-        D.o = L.o.view();
-        D.gu = L.gu.view();
-        D.down = L.down.view();
-        D.attn_g = L.d_attn_g;
-        D.attn_b = L.d_attn_b;
-        D.ffn_g = L.d_ffn_g;
-        D.ffn_b = L.d_ffn_b;
-        D.bqkv = L.d_bqkv;
-        D.bo = L.d_bo;
-        D.bgu = L.d_bgu;
-        D.bdown = L.d_bdown;
-        D.kc = S->kc + l * layer_cache;
-        D.vc = S->vc + l * layer_cache;
-    }
-    SMX_HIP(hipMalloc((void **)&S->d_layers, sizeof(LayerDesc) * hl.size()));
-    SMX_HIP(hipMemcpy(S->d_layers, hl.data(), sizeof(LayerDesc) * hl.size(), hipMemcpyHostToDevice));
-    SMX_HIP(hipMalloc((void **)&S->bar, 256));
-    SMX_HIP(hipMalloc((void **)&S->abort_flag, 256));
-    SMX_HIP(hipMalloc((void **)&S->wg_val, (size_t)grid * 4));
-    SMX_HIP(hipMalloc((void **)&S->wg_idx, (size_t)grid * 4));
-    DecodeArgs &a = S->dargs;
-    a.layers = S->d_layers;
-    a.n_layer = c.n_layer;
-    a.llama = m->llama ? 1 : 0;
-    a.d = c.d_model;
-    a.hd = m->hd;
-    a.n_head = c.n_head;
-    a.n_kv_head = c.n_kv_head;
-    a.kv_dim = m->kvdim;
-    a.nqkv = m->nqkv;
-    a.hidden = m->hidden;
-    a.vocab = c.vocab;
-    a.max_ctx = S->ctx_stride;   // the kernel uses it as the cache row length
-    a.eps = c.norm_eps;
-    a.tok = m->tok.view();
-    a.posw = m->llama ? WView{} : m->pos.view();
-    a.head = m->head.view();
-    a.out_g = m->d_out_g;
-    a.out_b = m->d_out_b;
-    a.rope_cos = m->rope_cos;
-    a.rope_sin = m->rope_sin;
-    a.x = S->x;
-    a.q = S->q;
-    a.att = S->att;
-    a.h = S->h;
-    a.logits = S->logits;
-    a.wg_val = S->wg_val;
-    a.wg_idx = S->wg_idx;
-    a.tokens = S->tokens;
-    a.pos = S->pos;
-    a.bar = S->bar;
-    a.abort_flag = S->abort_flag;
-    S->grid = grid;
-    S->fmt = fmt;
-    S->lds = lds;
-    S->persistent = true;
-    const char *tp = getenv("SMX_DECODE_TRACE");
-    if (tp && *tp) {
-        S->trace_cap = 4096;
-        S->trace_path = tp;
-        SMX_HIP(hipMalloc((void **)&S->trace, (size_t)S->trace_cap * grid * 2 * 8));
-    }
-    return SMX_OK;
-}
-
-// Enqueues one persistent launch running steps at positions pos0 .. pos0+n_steps-1; steps
-// s >= head_from compute logits and the greedy token.
-int run_persistent(smx_session *S, int pos0, int n_steps, int head_from, float *logits_all)
-{
-    hipStream_t s = S->stream;
-    SMX_HIP(hipMemsetAsync(S->bar, 0, 4, s));
-    SMX_HIP(hipMemsetAsync(S->abort_flag, 0, 4, s));
-    DecodeArgs a = S->dargs;
-    a.pos0 = pos0;
-    a.n_steps = n_steps;
-    a.head_from = head_from;
-    a.logits_all = logits_all;
-    if (S->trace) {
-        SMX_HIP(hipMemsetAsync(S->trace, 0, (size_t)S->trace_cap * S->grid * 2 * 8, s));
-        a.trace = S->trace;
-        a.trace_cap = S->trace_cap;
-    }
-    SMX_HIP(launch_decode(a, S->fmt, S->grid, S->lds, s));
-    return SMX_OK;
-}
-
-// After the stream has been synchronised: reports an aborted persistent launch and, when
-// tracing, appends the last launch's barrier stamps (header: grid, events; then
-// [events][grid][arrive, release] of the 100 MHz realtime counter).
-int check_abort(smx_session *S)
-{
-    if (!S->persistent) return SMX_OK;
-    int f = 0;
-    SMX_HIP(hipMemcpy(&f, S->abort_flag, 4, hipMemcpyDeviceToHost));
-    if (f) SMX_FAIL(SMX_EDEVICE, "persistent decode aborted: a device-wide barrier wait exceeded its limit");
-    if (S->trace) {
-        std::vector<unsigned long long> t((size_t)S->trace_cap * S->grid * 2);
-        SMX_HIP(hipMemcpy(t.data(), S->trace, t.size() * 8, hipMemcpyDeviceToHost));
-        FILE *fp = fopen(S->trace_path.c_str(), "ab");
-        if (fp) {
-            const long long hdr[2] = {S->grid, S->trace_cap};
-            fwrite(hdr, 8, 2, fp);
-            fwrite(t.data(), 8, t.size(), fp);
-            fclose(fp);
-        }
-    }
     return SMX_OK;
 }
 
@@ -692,6 +603,18 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
     const smx_model_config &c = m->cfg;
     const int d = c.d_model, hd = m->hd, Hkv = c.n_kv_head;
     const int pro = m->llama ? PRO_RMS : PRO_LN;
+    // host-side bounds of the batch buffers: M rows fit the buffers, the head rows fit the logits
+    // buffer, and every prefill run lies inside the M rows
+    if (M <= 0 || M > B.cap) SMX_FAIL(SMX_EINVAL, "run_tokens: %d rows for a batch of %d", M, B.cap);
+    if (head_from < M && (head_from < 0 || M - head_from > B.logits_rows))
+        SMX_FAIL(SMX_EINVAL, "run_tokens: head rows %d..%d for %d logits rows", head_from, M - 1, B.logits_rows);
+    for (int i = 0; run && i < n_run; i++) {
+        const int cnt = run[i].count < 0 ? M : run[i].count;
+        if (run[i].row0 < 0 || cnt <= 0 || run[i].row0 + cnt > M || run[i].p_first < 0 ||
+            (int64_t)run[i].p_first + cnt > ctx_stride)
+            SMX_FAIL(SMX_EINVAL, "run_tokens: prefill run %d (rows %d + %d at position %d) outside the batch of %d "
+                     "rows or the cache row of %d", i, run[i].row0, cnt, run[i].p_first, M, ctx_stride);
+    }
     // Up to 16 tokens, RMSNorm is folded into the GEMMs around it: the O and down projections
     // write the next norm's input as parts of gamma (.) x plus per-tile sums of x^2, and the
     // QKV (after layer 0) and gate/up GEMMs scale by 1 / rms -- no k_qprep launch per norm.
@@ -819,7 +742,10 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
 // 58.9K tok/s as one chunk instead of two; configs[3] 4096 tokens 38.0K / 43.6K / 46.0K /
 // 46.3K tok/s at 256 / 1024 / 2048 / 4096-token chunks).  The chunk buffers hold at least 256
 // tokens: a session of 83 positions with 96-token buffers ended its process with a host
-// segmentation fault once (cause not found), and no smaller size has run since.
+// segmentation fault once.  Reading the paths that depend on the buffer size found no
+// out-of-bounds access (the GEMM clamps its part loads to the last token tile, the prefill
+// attention clamps keys to the cache row, the host arrays hold cap entries with M <= cap, and
+// run_tokens now checks those bounds); with no cause shown, no smaller size has run since.
 constexpr int kPrefillChunk = 2048, kPrefillChunkMin = 256;
 
 // Runs tokens[0..n) of session S at positions p0.. through the model in chunks (K/V written
@@ -845,6 +771,7 @@ int prefill_tokens(smx_session *S, const int32_t *tokens_host, int n, int p0, bo
         SMX_HIP(hipStreamSynchronize(s));
     }
     TokBatch &B = S->pb;
+    if (chunk > B.cap) SMX_FAIL(SMX_EINVAL, "prefill_tokens: chunk %d exceeds the buffers of %d rows", chunk, B.cap);
     std::vector<int32_t> pos((size_t)chunk);
     for (int i0 = 0; i0 < n; i0 += chunk) {
         const int M = n - i0 < chunk ? n - i0 : chunk;
@@ -1723,13 +1650,10 @@ SMX_API int smx_session_create(smx_model *m, int max_ctx, smx_session **out)
         smx_session_destroy(S);
         SMX_HIP(e);
     }
-    int rc = setup_persistent(S);
-    if (rc == SMX_OK && !S->persistent) {
-        rc = capture_step(S, false, true, &S->g_prefill);
-        if (rc == SMX_OK) rc = capture_step(S, true, true, &S->g_decode);
-        if (rc == SMX_OK) rc = capture_step(S, true, false, &S->g_decode_next);
-        if (rc == SMX_OK) rc = capture_step(S, true, false, &S->g_decode_block, kDecodeBlock);
-    }
+    int rc = capture_step(S, false, true, &S->g_prefill);
+    if (rc == SMX_OK) rc = capture_step(S, true, true, &S->g_decode);
+    if (rc == SMX_OK) rc = capture_step(S, true, false, &S->g_decode_next);
+    if (rc == SMX_OK) rc = capture_step(S, true, false, &S->g_decode_block, kDecodeBlock);
     if (rc != SMX_OK) {
         std::string msg = smx::last_error();
         smx_session_destroy(S);
@@ -1762,10 +1686,7 @@ SMX_API int smx_session_forward(smx_session *S, const int32_t *tokens, int n_tok
     const int32_t p0 = pos_offset;
     SMX_HIP(hipMemcpyAsync(S->tokens + pos_offset, tokens, (size_t)n_tokens * 4, hipMemcpyHostToDevice, s));
     SMX_HIP(hipMemcpyAsync(S->pos, &p0, 4, hipMemcpyHostToDevice, s));
-    if (S->persistent) {
-        rc = run_persistent(S, pos_offset, n_tokens, n_tokens - 1, nullptr);
-        if (rc != SMX_OK) return rc;
-    } else if (n_tokens >= kPrefillMin) {
+    if (n_tokens >= kPrefillMin) {
         if ((rc = prefill_tokens(S, tokens, n_tokens, pos_offset, true, s)) != SMX_OK) return rc;
     } else {
         for (int i = 0; i + 1 < n_tokens; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
@@ -1774,7 +1695,57 @@ SMX_API int smx_session_forward(smx_session *S, const int32_t *tokens, int n_tok
     if (logits_out)
         SMX_HIP(hipMemcpyAsync(logits_out, S->logits, (size_t)S->m->cfg.vocab * 4, hipMemcpyDeviceToHost, s));
     SMX_HIP(hipStreamSynchronize(s));
-    return check_abort(S);
+    return SMX_OK;
+}
+
+// The prompt a generation prefills: its last max_ctx tokens (InferenceSession.cs:494-508).
+static void crop_prompt(const smx_session *S, const int32_t *&prompt, int &n_prompt)
+{
+    if (n_prompt > S->max_ctx) {
+        prompt += n_prompt - S->max_ctx;
+        n_prompt = S->max_ctx;
+    }
+}
+
+// After a generation of n_new requested tokens stopped (rc != SMX_OK) or finished: copies the
+// `done` tokens produced to out_tokens, fills the rest with -1 and fills stats.
+static int finish_generation(smx_session *S, int n_prompt, int n_new, int done, int32_t *out_tokens,
+                             smx_gen_stats *stats, int rc)
+{
+    hipStream_t s = S->stream;
+    if (done > 0)
+        SMX_HIP(hipMemcpyAsync(out_tokens, S->tokens + n_prompt, (size_t)done * 4, hipMemcpyDeviceToHost, s));
+    SMX_HIP(hipStreamSynchronize(s));
+    for (int i = done; i < n_new; i++) out_tokens[i] = -1;
+    if (stats) {
+        float a = 0.0f, b = 0.0f;
+        SMX_HIP(hipEventElapsedTime(&a, S->ev[0], S->ev[1]));
+        SMX_HIP(hipEventElapsedTime(&b, S->ev[1], S->ev[2]));
+        stats->prefill_ms = a;
+        stats->decode_ms = b;
+        stats->n_prefill_steps = n_prompt - 1;
+        stats->n_decode_steps = done;
+    }
+    if (rc == SMX_ECANCELED) SMX_FAIL(rc, "generation cancelled after %d of %d tokens", done, n_new);
+    if (rc == SMX_ETIMEDOUT)
+        SMX_FAIL(rc, "generation stopped at the session's %d ms time limit after %d of %d tokens",
+                 (int)S->max_time_ms.load(), done, n_new);
+    return rc;
+}
+
+// Prefills all prompt tokens but the last (their logits are not needed) and leaves the device
+// position at the last one.
+static int prefill_prompt(smx_session *S, const int32_t *prompt, int n_prompt, hipStream_t s)
+{
+    int rc = SMX_OK;
+    if (n_prompt - 1 >= kPrefillMin) {
+        if ((rc = prefill_tokens(S, prompt, n_prompt - 1, 0, false, s)) != SMX_OK) return rc;
+        const int32_t plast = n_prompt - 1;
+        SMX_HIP(hipMemcpyAsync(S->pos, &plast, 4, hipMemcpyHostToDevice, s));
+    } else {
+        for (int i = 0; i + 1 < n_prompt; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
+    }
+    return SMX_OK;
 }
 
 SMX_API int smx_session_generate(smx_session *S, const int32_t *prompt, int n_prompt, int n_new,
@@ -1784,65 +1755,54 @@ SMX_API int smx_session_generate(smx_session *S, const int32_t *prompt, int n_pr
         SMX_FAIL(SMX_EINVAL, "smx_session_generate: bad arguments");
     BusyGuard guard(S->busy);
     if (!guard.ok) SMX_FAIL(SMX_EBUSY, "smx_session_generate: session in use on another thread");
+    crop_prompt(S, prompt, n_prompt);
     if ((int64_t)n_prompt + n_new - 1 > S->max_ctx)
         SMX_FAIL(SMX_ERANGE, "prompt %d + new tokens %d exceed the session context %d", n_prompt, n_new, S->max_ctx);
     int rc = check_tokens(S, prompt, n_prompt);
     if (rc != SMX_OK) return rc;
+    StopCheck stop;
+    stop.add(S, std::chrono::steady_clock::now());
     SMX_HIP(hipSetDevice(S->m->ctx->device));
     hipStream_t s = S->stream;
     const int V = S->m->cfg.vocab;
     const int32_t zero = 0;
-    SMX_HIP(hipMemcpyAsync(S->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s));
-    SMX_HIP(hipMemcpyAsync(S->pos, &zero, 4, hipMemcpyHostToDevice, s));
-    if (S->persistent && logits_out && S->logits_all_cap < (size_t)n_new * V) {
-        if (S->logits_all) (void)hipFree(S->logits_all);
-        S->logits_all = nullptr;
-        S->logits_all_cap = 0;
-        SMX_HIP(hipMalloc((void **)&S->logits_all, (size_t)n_new * V * 4));
-        S->logits_all_cap = (size_t)n_new * V;
-    }
     SMX_HIP(hipEventRecord(S->ev[0], s));
-    if (S->persistent) {
-        if (n_prompt > 1 && (rc = run_persistent(S, 0, n_prompt - 1, n_prompt - 1, nullptr)) != SMX_OK) return rc;
-    } else if (n_prompt - 1 >= kPrefillMin) {
-        if ((rc = prefill_tokens(S, prompt, n_prompt - 1, 0, false, s)) != SMX_OK) return rc;
-        const int32_t plast = n_prompt - 1;
-        SMX_HIP(hipMemcpyAsync(S->pos, &plast, 4, hipMemcpyHostToDevice, s));
-    } else {
-        for (int i = 0; i + 1 < n_prompt; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
+    int done = 0, halt = stop.poll();
+    if (halt == SMX_OK) {
+        SMX_HIP(hipMemcpyAsync(S->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(S->pos, &zero, 4, hipMemcpyHostToDevice, s));
+        if ((rc = prefill_prompt(S, prompt, n_prompt, s)) != SMX_OK) return rc;
     }
     SMX_HIP(hipEventRecord(S->ev[1], s));
-    if (S->persistent) {
-        if ((rc = run_persistent(S, n_prompt - 1, n_new, 0, logits_out ? S->logits_all : nullptr)) != SMX_OK)
-            return rc;
-        if (logits_out)
-            SMX_HIP(hipMemcpyAsync(logits_out, S->logits_all, (size_t)n_new * V * 4, hipMemcpyDeviceToHost, s));
-    } else {
-        for (int i = 0; i < n_new;) {
-            if (i > 0 && !logits_out && n_new - i >= kDecodeBlock) {
-                SMX_HIP(hipGraphLaunch(S->g_decode_block, s));
-                i += kDecodeBlock;
-                continue;
-            }
-            SMX_HIP(hipGraphLaunch(i == 0 ? S->g_decode : S->g_decode_next, s));
+    Pacer pace(s, logits_out ? 1 : 2);
+    while (halt == SMX_OK && done < n_new) {
+        if ((halt = stop.poll()) != SMX_OK) break;
+        if (done > 0 && !logits_out && n_new - done >= kDecodeBlock) {
+            SMX_HIP(hipGraphLaunch(S->g_decode_block, s));
+            done += kDecodeBlock;
+        } else {
+            SMX_HIP(hipGraphLaunch(done == 0 ? S->g_decode : S->g_decode_next, s));
             if (logits_out)
-                SMX_HIP(hipMemcpyAsync(logits_out + (size_t)i * V, S->logits, (size_t)V * 4, hipMemcpyDeviceToHost, s));
-            i++;
+                SMX_HIP(hipMemcpyAsync(logits_out + (size_t)done * V, S->logits, (size_t)V * 4, hipMemcpyDeviceToHost, s));
+            done++;
         }
+        SMX_HIP(pace.launched());
     }
     SMX_HIP(hipEventRecord(S->ev[2], s));
-    SMX_HIP(hipMemcpyAsync(out_tokens, S->tokens + n_prompt, (size_t)n_new * 4, hipMemcpyDeviceToHost, s));
-    SMX_HIP(hipStreamSynchronize(s));
-    if ((rc = check_abort(S)) != SMX_OK) return rc;
-    if (stats) {
-        float a = 0.0f, b = 0.0f;
-        SMX_HIP(hipEventElapsedTime(&a, S->ev[0], S->ev[1]));
-        SMX_HIP(hipEventElapsedTime(&b, S->ev[1], S->ev[2]));
-        stats->prefill_ms = a;
-        stats->decode_ms = b;
-        stats->n_prefill_steps = n_prompt - 1;
-        stats->n_decode_steps = n_new;
-    }
+    return finish_generation(S, n_prompt, n_new, done, out_tokens, stats, halt);
+}
+
+SMX_API int smx_session_cancel(smx_session *S)
+{
+    if (!S) SMX_FAIL(SMX_EINVAL, "smx_session_cancel: null session");
+    S->cancel.store(1);
+    return SMX_OK;
+}
+
+SMX_API int smx_session_set_max_time(smx_session *S, int32_t max_time_ms)
+{
+    if (!S || max_time_ms < 0) SMX_FAIL(SMX_EINVAL, "smx_session_set_max_time: bad arguments");
+    S->max_time_ms.store(max_time_ms);
     return SMX_OK;
 }
 
@@ -1856,12 +1816,13 @@ SMX_API int smx_session_generate_sampled(smx_session *S, const int32_t *prompt, 
         SMX_FAIL(SMX_EINVAL, "smx_session_generate_sampled: need temperature > 0, top_k >= 0, repetition_window >= 0");
     BusyGuard guard(S->busy);
     if (!guard.ok) SMX_FAIL(SMX_EBUSY, "smx_session_generate_sampled: session in use on another thread");
+    crop_prompt(S, prompt, n_prompt);
     if ((int64_t)n_prompt + n_new - 1 > S->max_ctx)
         SMX_FAIL(SMX_ERANGE, "prompt %d + new tokens %d exceed the session context %d", n_prompt, n_new, S->max_ctx);
-    if (S->persistent)
-        SMX_FAIL(SMX_EINVAL, "smx_session_generate_sampled: not available on a persistent-decode session");
     int rc = check_tokens(S, prompt, n_prompt);
     if (rc != SMX_OK) return rc;
+    StopCheck stop;
+    stop.add(S, std::chrono::steady_clock::now());
     SMX_HIP(hipSetDevice(S->m->ctx->device));
     hipStream_t s = S->stream;
     const int V = S->m->cfg.vocab;
@@ -1884,36 +1845,26 @@ SMX_API int smx_session_generate_sampled(smx_session *S, const int32_t *prompt, 
     if (!S->g_sample && (rc = capture_step(S, true, true, &S->g_sample, 1, true)) != SMX_OK) return rc;
     const SampleState st{*params, seed, 0};
     const int32_t zero = 0;
-    SMX_HIP(hipMemcpyAsync(S->samp, &st, sizeof(st), hipMemcpyHostToDevice, s));
-    SMX_HIP(hipMemcpyAsync(S->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s));
-    SMX_HIP(hipMemcpyAsync(S->pos, &zero, 4, hipMemcpyHostToDevice, s));
     SMX_HIP(hipEventRecord(S->ev[0], s));
-    if (n_prompt - 1 >= kPrefillMin) {
-        if ((rc = prefill_tokens(S, prompt, n_prompt - 1, 0, false, s)) != SMX_OK) return rc;
-        const int32_t plast = n_prompt - 1;
-        SMX_HIP(hipMemcpyAsync(S->pos, &plast, 4, hipMemcpyHostToDevice, s));
-    } else {
-        for (int i = 0; i + 1 < n_prompt; i++) SMX_HIP(hipGraphLaunch(S->g_prefill, s));
+    int done = 0, halt = stop.poll();
+    if (halt == SMX_OK) {
+        SMX_HIP(hipMemcpyAsync(S->samp, &st, sizeof(st), hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(S->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemcpyAsync(S->pos, &zero, 4, hipMemcpyHostToDevice, s));
+        if ((rc = prefill_prompt(S, prompt, n_prompt, s)) != SMX_OK) return rc;
     }
     SMX_HIP(hipEventRecord(S->ev[1], s));
-    for (int i = 0; i < n_new; i++) {
+    Pacer pace(s, 8);
+    while (halt == SMX_OK && done < n_new) {
+        if ((halt = stop.poll()) != SMX_OK) break;
         SMX_HIP(hipGraphLaunch(S->g_sample, s));
         if (logits_out)
-            SMX_HIP(hipMemcpyAsync(logits_out + (size_t)i * V, S->logits, (size_t)V * 4, hipMemcpyDeviceToHost, s));
+            SMX_HIP(hipMemcpyAsync(logits_out + (size_t)done * V, S->logits, (size_t)V * 4, hipMemcpyDeviceToHost, s));
+        done++;
+        SMX_HIP(pace.launched());
     }
     SMX_HIP(hipEventRecord(S->ev[2], s));
-    SMX_HIP(hipMemcpyAsync(out_tokens, S->tokens + n_prompt, (size_t)n_new * 4, hipMemcpyDeviceToHost, s));
-    SMX_HIP(hipStreamSynchronize(s));
-    if (stats) {
-        float a = 0.0f, b = 0.0f;
-        SMX_HIP(hipEventElapsedTime(&a, S->ev[0], S->ev[1]));
-        SMX_HIP(hipEventElapsedTime(&b, S->ev[1], S->ev[2]));
-        stats->prefill_ms = a;
-        stats->decode_ms = b;
-        stats->n_prefill_steps = n_prompt - 1;
-        stats->n_decode_steps = n_new;
-    }
-    return SMX_OK;
+    return finish_generation(S, n_prompt, n_new, done, out_tokens, stats, halt);
 }
 
 // Upper bound on sessions per lockstep batch (one token tile of the GEMM per 16 sessions).
@@ -1945,11 +1896,21 @@ SMX_API int smx_batch_generate(smx_session *const *sessions, int n_sessions, con
         off[(size_t)i + 1] = off[(size_t)i] + n;
     }
     std::vector<std::unique_ptr<BusyGuard>> guards;
+    StopCheck stop;
+    const auto t0 = std::chrono::steady_clock::now();
     for (int i = 0; i < n_sessions; i++) {
         guards.emplace_back(new BusyGuard(sessions[i]->busy));
         if (!guards.back()->ok) SMX_FAIL(SMX_EBUSY, "smx_batch_generate: session %d in use on another thread", i);
         int rc = check_tokens(sessions[i], prompts + off[(size_t)i], prompt_lens[i]);
         if (rc != SMX_OK) return rc;
+        stop.add(sessions[i], t0);
+    }
+    int halt = stop.poll();
+    if (halt != SMX_OK) {
+        for (int64_t i = 0; i < (int64_t)n_sessions * n_new; i++) out_tokens[i] = -1;
+        if (stats) *stats = smx_gen_stats{0.0, 0.0, 0, 0};
+        SMX_FAIL(halt, "smx_batch_generate: stopped before the prefill (%s)",
+                 halt == SMX_ECANCELED ? "cancel request" : "time limit");
     }
     SMX_HIP(hipSetDevice(m->ctx->device));
     // every listed session is held by this call: the first one's stream carries the batch
@@ -2027,14 +1988,25 @@ SMX_API int smx_batch_generate(smx_session *const *sessions, int n_sessions, con
     }
     SMX_BHIP(ce);
     SMX_BHIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
-    for (int k = 0; k < n_new; k++) SMX_BHIP(hipGraphLaunch(exec, s));
+    int done = 0;
+    {
+        Pacer pace(s, 2);
+        while (done < n_new && (halt = stop.poll()) == SMX_OK) {
+            SMX_BHIP(hipGraphLaunch(exec, s));
+            done++;
+            SMX_BHIP(pace.launched());
+        }
+    }
     SMX_BHIP(hipEventRecord(ev[2], s));
     for (int i = 0; i < n; i++) {
-        SMX_BHIP(hipMemcpyAsync(out_tokens + (size_t)i * n_new, sessions[i]->tokens + prompt_lens[i],
-                                (size_t)n_new * 4, hipMemcpyDeviceToHost, s));
+        if (done > 0)
+            SMX_BHIP(hipMemcpyAsync(out_tokens + (size_t)i * n_new, sessions[i]->tokens + prompt_lens[i],
+                                    (size_t)done * 4, hipMemcpyDeviceToHost, s));
         SMX_BHIP(hipMemcpyAsync(sessions[i]->pos, D.pos + i, 4, hipMemcpyDeviceToDevice, s));
     }
     SMX_BHIP(hipStreamSynchronize(s));
+    for (int i = 0; i < n; i++)
+        for (int k = done; k < n_new; k++) out_tokens[(size_t)i * n_new + k] = -1;
     if (stats) {
         float a = 0.0f, b = 0.0f;
         SMX_BHIP(hipEventElapsedTime(&a, ev[0], ev[1]));
@@ -2042,10 +2014,13 @@ SMX_API int smx_batch_generate(smx_session *const *sessions, int n_sessions, con
         stats->prefill_ms = a;
         stats->decode_ms = b;
         stats->n_prefill_steps = (int32_t)n_prefill;
-        stats->n_decode_steps = n_new;
+        stats->n_decode_steps = done;
     }
 #undef SMX_BHIP
     cleanup();
+    if (halt != SMX_OK)
+        SMX_FAIL(halt, "smx_batch_generate: stopped after %d of %d steps (%s)", done, n_new,
+                 halt == SMX_ECANCELED ? "cancel request" : "time limit");
     return SMX_OK;
 }
 
@@ -2062,6 +2037,7 @@ struct smx_batcher {
     std::vector<int32_t> id, pos;   // per member: token to process next and its position
     std::vector<SampleState> samp;  // per member: sampling options, seed and draws taken
     std::vector<int32_t> on;        // per member: 1 = sampled, 0 = greedy
+    std::vector<std::chrono::steady_clock::time_point> joined;   // per member: when it joined
     SampleState *d_samp = nullptr;  // device copies, max_members entries
     int32_t *d_on = nullptr;
     float *d_probs = nullptr;       // sampling scratch, max_members x vocab
@@ -2135,6 +2111,7 @@ static int batcher_add(smx_batcher *B, smx_session *S, const int32_t *prompt, in
     B->pos.push_back(n_prompt - 1);
     B->samp.push_back(params ? SampleState{*params, seed, 0} : SampleState{});
     B->on.push_back(params ? 1 : 0);
+    B->joined.push_back(std::chrono::steady_clock::now());
     B->dirty = true;
     return SMX_OK;
 }
@@ -2170,6 +2147,7 @@ SMX_API int smx_batcher_remove(smx_batcher *B, smx_session *S)
     B->pos.erase(B->pos.begin() + (std::ptrdiff_t)i);
     B->samp.erase(B->samp.begin() + (std::ptrdiff_t)i);
     B->on.erase(B->on.begin() + (std::ptrdiff_t)i);
+    B->joined.erase(B->joined.begin() + (std::ptrdiff_t)i);
     B->dirty = true;
     S->busy.store(0);
     return SMX_OK;
@@ -2242,19 +2220,35 @@ SMX_API int smx_batcher_step(smx_batcher *B, int n_steps, int32_t *out_tokens)
             return rc;
         }
     }
-    for (int k = 0; k < n_steps; k++) SMX_HIP(hipGraphLaunch(exec, s));
-    if (n_steps == 1)   // the step's tokens are also each member's next input id: one copy
+    StopCheck stop;
+    for (int i = 0; i < n; i++) stop.add(B->slot[(size_t)i], B->joined[(size_t)i]);
+    int done = 0, halt = SMX_OK;
+    {
+        Pacer pace(s, 2);
+        while (done < n_steps && (halt = stop.poll()) == SMX_OK) {
+            SMX_HIP(hipGraphLaunch(exec, s));
+            done++;
+            SMX_HIP(pace.launched());
+        }
+    }
+    if (done == 1 && n_steps == 1)   // the step's tokens are also each member's next input id: one copy
         SMX_HIP(hipMemcpyAsync(out_tokens, D.ids, (size_t)n * 4, hipMemcpyDeviceToHost, s));
-    else
+    else if (done > 0)
         for (int i = 0; i < n; i++)
             SMX_HIP(hipMemcpyAsync(out_tokens + (size_t)i * n_steps, B->slot[(size_t)i]->tokens + B->pos[(size_t)i] + 1,
-                                   (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
+                                   (size_t)done * 4, hipMemcpyDeviceToHost, s));
     SMX_HIP(hipStreamSynchronize(s));
     for (int i = 0; i < n; i++) {
-        B->pos[(size_t)i] += n_steps;
-        B->id[(size_t)i] = out_tokens[(size_t)i * n_steps + n_steps - 1];
-        if (B->on[(size_t)i]) B->samp[(size_t)i].counter += (uint64_t)n_steps;
+        if (done > 0) {
+            B->pos[(size_t)i] += done;
+            B->id[(size_t)i] = out_tokens[(size_t)i * n_steps + done - 1];
+            if (B->on[(size_t)i]) B->samp[(size_t)i].counter += (uint64_t)done;
+        }
+        for (int k = done; k < n_steps; k++) out_tokens[(size_t)i * n_steps + k] = -1;
     }
+    if (halt != SMX_OK)
+        SMX_FAIL(halt, "smx_batcher_step: stopped after %d of %d steps (%s)", done, n_steps,
+                 halt == SMX_ECANCELED ? "cancel request" : "time limit");
     return SMX_OK;
 }
 
@@ -2282,6 +2276,7 @@ SMX_API int smx_session_reset(smx_session *S)
     if (!S) SMX_FAIL(SMX_EINVAL, "smx_session_reset: null session");
     BusyGuard guard(S->busy);
     if (!guard.ok) SMX_FAIL(SMX_EBUSY, "smx_session_reset: session in use on another thread");
+    S->cancel.store(0);
     SMX_HIP(hipSetDevice(S->m->ctx->device));
     const int32_t zero = 0;
     SMX_HIP(hipMemcpyAsync(S->pos, &zero, 4, hipMemcpyHostToDevice, S->stream));
@@ -2309,8 +2304,7 @@ SMX_API int smx_session_destroy(smx_session *S)
     free_dev(S->h); free_dev(S->logits); free_dev(S->tokens); free_dev(S->pos); free_dev(S->amax);
     free_dev(S->head_val); free_dev(S->head_idx);
     batch_free(S->pb);
-    free_dev(S->d_layers); free_dev(S->bar); free_dev(S->abort_flag); free_dev(S->wg_val);
-    free_dev(S->wg_idx); free_dev(S->logits_all); free_dev(S->trace); free_dev(S->samp); free_dev(S->probs);
+    free_dev(S->samp); free_dev(S->probs);
     S->m->sessions.fetch_sub(1);
     delete S;
     return SMX_OK;

@@ -94,10 +94,10 @@ __device__ __forceinline__ float silu_mul(float x, float u)
     return silu * u;
 }
 
-// Thread index passed through an opaque instruction.  In the persistent decode kernel every
-// phase recomputes its lane-dependent addresses from this value where it uses them, instead
-// of the compiler hoisting all of them out of the step/layer loops and keeping them live for
-// the whole kernel (which spills registers).  Costs one v_mov per call site.
+// Thread index passed through an opaque instruction, so the compiler treats values derived from
+// it as lane-varying and recomputes lane-dependent addresses where they are used instead of
+// hoisting them and keeping them live (which spills registers in the larger kernels).  Costs
+// one v_mov per call site.
 __device__ __forceinline__ int opaque_tid()
 {
     int t;

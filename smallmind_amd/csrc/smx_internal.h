@@ -219,41 +219,6 @@ size_t qgemm_xp_bytes(int M, int K);
 hipError_t launch_qgemm(const QgemmArgs &a, const float *x, int64_t x_stride, int pro,
                         const float *gamma, const float *beta, float eps, hipStream_t s);
 
-// ---- persistent decode -------------------------------------------------------------------------
-struct LayerDesc {
-    WView qkv, o, gu, down;
-    const float *attn_g, *attn_b, *ffn_g, *ffn_b;
-    const float *bqkv, *bo, *bgu, *bdown;
-    float *kc, *vc;             // this layer's K [n_kv_head][hd][max_ctx] and V [n_kv_head][max_ctx][hd]
-                                // (max_ctx here = the session's cache row length)
-};
-
-struct DecodeArgs {
-    const LayerDesc *layers;    // device array [n_layer]
-    int n_layer, llama, d, hd, n_head, n_kv_head, kv_dim, nqkv, hidden, vocab, max_ctx;
-    float eps;
-    WView tok, posw, head;      // posw.q == nullptr without learned positions
-    const float *out_g, *out_b, *rope_cos, *rope_sin;
-    float *x, *q, *att, *h;
-    float *logits;              // [vocab] of the last step with a head
-    float *logits_all;          // [n_steps - head_from][vocab] or nullptr
-    float *wg_val;              // [grid] per-workgroup argmax partials
-    int32_t *wg_idx;
-    int32_t *tokens, *pos;      // token array [max_ctx + 1] and the device position
-    unsigned *bar;              // grid barrier counter (zeroed before each launch)
-    int *abort_flag;            // set when a barrier wait exceeds its spin limit
-    int pos0, n_steps, head_from;
-    // optional phase trace: per barrier and workgroup, the realtime-clock stamps of arrival
-    // and release ([trace_cap][grid][2]); nullptr when tracing is off
-    unsigned long long *trace;
-    int trace_cap;
-};
-
-constexpr int kDecodeThreads = 512;
-// Workgroups the persistent decode kernel can keep co-resident (0 if unsupported).
-int decode_grid(int fmt, int hd, size_t lds, int device);
-hipError_t launch_decode(const DecodeArgs &a, int fmt, int grid, size_t lds, hipStream_t s);
-
 // ---- other kernels -------------------------------------------------------------------------
 hipError_t launch_dequant_gguf(int type, const void *blocks, int64_t n, float *out, hipStream_t s);
 hipError_t launch_quantize_gguf(int type, const float *x, int64_t n, void *blocks, hipStream_t s);

@@ -14,7 +14,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from ._lib import ARCH_GPT2, ARCH_LLAMA, GenStatsC, ModelConfigC, call, load
+from ._lib import ARCH_GPT2, ARCH_LLAMA, GenerationCancelled, GenerationTimeout, GenStatsC, ModelConfigC, call, load
 
 
 def uniform_draw(seed: int, i: int) -> float:
@@ -219,15 +219,22 @@ class GpuInferenceSession:
         return out
 
     def generate_greedy(self, prompt, max_new_tokens: int, return_logits: bool = False):
-        """Prefill + greedy decode on the device.  Returns (tokens, stats[, logits])."""
+        """Prefill + greedy decode on the device.  Returns (tokens, stats[, logits]).  A prompt
+        longer than the session context is cropped to its last max_ctx tokens.  A cancel request
+        or the time limit stops it between graph launches: GenerationCancelled /
+        GenerationTimeout, whose `tokens` are the ones produced before the stop."""
         p = np.ascontiguousarray(prompt, dtype=np.int32).reshape(-1)
         toks = np.empty(max_new_tokens, np.int32)
         logits = (np.empty((max_new_tokens, self.model.config.vocab_size), np.float32)
                   if return_logits else None)
         st = GenStatsC()
-        call("smx_session_generate", self._h, p.ctypes.data_as(ctypes.c_void_p), p.size,
-             max_new_tokens, toks.ctypes.data_as(ctypes.c_void_p),
-             logits.ctypes.data_as(ctypes.c_void_p) if return_logits else None, ctypes.byref(st))
+        try:
+            call("smx_session_generate", self._h, p.ctypes.data_as(ctypes.c_void_p), p.size,
+                 max_new_tokens, toks.ctypes.data_as(ctypes.c_void_p),
+                 logits.ctypes.data_as(ctypes.c_void_p) if return_logits else None, ctypes.byref(st))
+        except (GenerationCancelled, GenerationTimeout) as e:
+            e.tokens = toks[:st.n_decode_steps].copy()
+            raise
         stats = {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
                  "prefill_steps": st.n_prefill_steps, "decode_steps": st.n_decode_steps}
         return (toks, stats, logits) if return_logits else (toks, stats)
@@ -238,7 +245,7 @@ class GpuInferenceSession:
                          return_logits: bool = False):
         """Prefill + decode with the reference's sampling pipeline on the device (defaults of
         ProductionInferenceOptions.cs:19-87); draw i is uniform_draw(seed, i).  Returns
-        (tokens, stats[, logits])."""
+        (tokens, stats[, logits]); cropping and stops as in generate_greedy."""
         from ._lib import SamplingC
         p = np.ascontiguousarray(prompt, dtype=np.int32).reshape(-1)
         toks = np.empty(max_new_tokens, np.int32)
@@ -247,12 +254,26 @@ class GpuInferenceSession:
         sp = SamplingC(temperature, top_k, top_p, min_p, repetition_penalty, presence_penalty, frequency_penalty,
                        repetition_window)
         st = GenStatsC()
-        call("smx_session_generate_sampled", self._h, p.ctypes.data_as(ctypes.c_void_p), p.size, max_new_tokens,
-             ctypes.byref(sp), ctypes.c_uint64(seed), toks.ctypes.data_as(ctypes.c_void_p),
-             logits.ctypes.data_as(ctypes.c_void_p) if return_logits else None, ctypes.byref(st))
+        try:
+            call("smx_session_generate_sampled", self._h, p.ctypes.data_as(ctypes.c_void_p), p.size, max_new_tokens,
+                 ctypes.byref(sp), ctypes.c_uint64(seed), toks.ctypes.data_as(ctypes.c_void_p),
+                 logits.ctypes.data_as(ctypes.c_void_p) if return_logits else None, ctypes.byref(st))
+        except (GenerationCancelled, GenerationTimeout) as e:
+            e.tokens = toks[:st.n_decode_steps].copy()
+            raise
         stats = {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
                  "prefill_steps": st.n_prefill_steps, "decode_steps": st.n_decode_steps}
         return (toks, stats, logits) if return_logits else (toks, stats)
+
+    def cancel(self):
+        """Asks the running (or next) generation on this session to stop; callable from any
+        thread (smx_session_cancel)."""
+        call("smx_session_cancel", self._h)
+
+    def set_max_time_ms(self, max_time_ms: int):
+        """MaxTimeMs of ProductionInferenceOptions (0 = no limit): later generations stop with
+        GenerationTimeout once they have run this long."""
+        call("smx_session_set_max_time", self._h, int(max_time_ms))
 
     def reset_kv_cache(self):
         call("smx_session_reset", self._h)
@@ -271,9 +292,13 @@ class GpuInferenceSession:
         handles = (ctypes.c_void_p * n)(*[s._h.value for s in sessions])
         toks = np.empty((n, max_new_tokens), np.int32)
         st = GenStatsC()
-        call("smx_batch_generate", ctypes.cast(handles, ctypes.c_void_p), n,
-             flat.ctypes.data_as(ctypes.c_void_p), lens.ctypes.data_as(ctypes.c_void_p),
-             max_new_tokens, toks.ctypes.data_as(ctypes.c_void_p), ctypes.byref(st))
+        try:
+            call("smx_batch_generate", ctypes.cast(handles, ctypes.c_void_p), n,
+                 flat.ctypes.data_as(ctypes.c_void_p), lens.ctypes.data_as(ctypes.c_void_p),
+                 max_new_tokens, toks.ctypes.data_as(ctypes.c_void_p), ctypes.byref(st))
+        except (GenerationCancelled, GenerationTimeout) as e:
+            e.tokens = toks[:, :st.n_decode_steps].copy()
+            raise
         stats = {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
                  "prefill_steps": st.n_prefill_steps, "decode_steps": st.n_decode_steps}
         return toks, stats
@@ -331,9 +356,16 @@ class ContinuousBatcher:
         return n
 
     def step(self, n_steps: int = 1) -> np.ndarray:
-        """Tokens [n_members][n_steps], members in the order they were added."""
+        """Tokens [n_members][n_steps], members in the order they were added.  A member's cancel
+        request or time limit stops the call between steps: GenerationCancelled /
+        GenerationTimeout with `tokens` = the steps that ran."""
         out = np.empty((len(self.members), n_steps), np.int32)
-        call("smx_batcher_step", self._h, n_steps, out.ctypes.data_as(ctypes.c_void_p))
+        try:
+            call("smx_batcher_step", self._h, n_steps, out.ctypes.data_as(ctypes.c_void_p))
+        except (GenerationCancelled, GenerationTimeout) as e:
+            done = int((out[0] >= 0).sum()) if out.size else 0
+            e.tokens = out[:, :done].copy()
+            raise
         return out
 
     def close(self):

@@ -5,6 +5,7 @@ import os
 import re
 
 import numpy as np
+import pytest
 
 import oracle as O
 
@@ -58,3 +59,54 @@ def test_invalid_arguments_report_errors_without_a_device():
 def test_model_config_struct_layout():
     from smallmind_amd._lib import ModelConfigC
     assert ctypes.sizeof(ModelConfigC) == 4 * 16
+
+
+def test_cancel_and_time_limit_entry_points_check_arguments_without_a_device():
+    from smallmind_amd import _lib
+    L = _lib.load()
+    assert L.smx_session_cancel(None) == -1
+    assert L.smx_session_set_max_time(None, 5) == -1
+
+
+class _StoppingLib:
+    """Stand-in for libsmx.so whose generate calls stop after two tokens with status `rc`,
+    filling out_tokens and stats as the library does (tokens produced, then -1)."""
+
+    def __init__(self, rc):
+        self.rc = rc
+
+    def smx_last_error(self):
+        return b"stopped"
+
+    def _fill(self, toks_ptr, n_total, stats_ptr, done=2):
+        arr = (ctypes.c_int32 * n_total).from_address(toks_ptr.value)
+        for i in range(n_total):
+            arr[i] = 40 + i if i < done else -1
+        ctypes.cast(stats_ptr, ctypes.POINTER(self.stats_type)).contents.n_decode_steps = done
+
+    def smx_session_generate(self, h, p, n, n_new, toks, logits, stats):
+        self._fill(toks, n_new, stats)
+        return self.rc
+
+
+@pytest.mark.parametrize("rc,cls,reference", [(-8, "GenerationCancelled", "OperationCanceledException"),
+                                              (-9, "GenerationTimeout", "InferenceTimeoutException")])
+def test_stopped_generation_maps_to_the_reference_exception(monkeypatch, rc, cls, reference):
+    """Status mapping of a stopped generation on the host side: the Python mirror raises
+    GenerationCancelled / GenerationTimeout carrying the tokens produced before the stop, and the
+    C# binding throws the reference's exception for the same status."""
+    from smallmind_amd import _lib, model
+    fake = _StoppingLib(rc)
+    fake.stats_type = _lib.GenStatsC
+    monkeypatch.setattr(_lib, "_lib", fake)
+    sess = model.GpuInferenceSession.__new__(model.GpuInferenceSession)
+    sess._h = ctypes.c_void_p(1)
+    sess.model = type("M", (), {"config": type("C", (), {"vocab_size": 8})()})()
+    with pytest.raises(getattr(_lib, cls)) as ei:
+        sess.generate_greedy(np.arange(3, dtype=np.int32), 5)
+    assert ei.value.code == rc
+    assert list(ei.value.tokens) == [40, 41]
+    sess._h = ctypes.c_void_p()
+    cs = open(os.path.join(ROOT, "smallmind_amd", "bindings", "csharp", "Smx.cs")).read()
+    name = {-8: "ECANCELED", -9: "ETIMEDOUT"}[rc]
+    assert re.search(rf"\b{name}\s*=>\s*new {reference}\(", cs), (name, reference)

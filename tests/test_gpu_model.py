@@ -49,15 +49,12 @@ def _pair(pairs, key):
     return pairs[key]
 
 
-@pytest.mark.parametrize("mode", ["graph", "persistent"])
 @pytest.mark.parametrize("key", list(SMALL))
-def test_greedy_64_tokens_and_logits(pairs, key, mode, monkeypatch):
-    """Both decode paths: the captured per-kernel graph (default) and the single cooperative
-    kernel per generate call (SMX_DECODE=persistent)."""
+def test_greedy_64_tokens_and_logits(pairs, key):
+    """The captured decode graphs: 64 greedy tokens and every step's logits against the oracle."""
     om, gm = _pair(pairs, key)
     cfg = SMALL[key][0]
     prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, 20).astype(np.int32)
-    monkeypatch.setenv("SMX_DECODE", mode)
     sess = gm.create_session(96)
     toks, stats, logits = sess.generate_greedy(prompt, 64, return_logits=True)
     osess = om.session(96)
@@ -75,8 +72,7 @@ def test_greedy_64_tokens_and_logits(pairs, key, mode, monkeypatch):
     sess.close()
 
 
-@pytest.mark.parametrize("mode", ["graph", "persistent"])
-def test_session_context_not_a_multiple_of_four(pairs, mode, monkeypatch):
+def test_session_context_not_a_multiple_of_four(pairs):
     """A session of 83 positions keeps its KV cache rows padded to 84 (16-byte aligned K rows
     for the one-launch decode attention); prefill, decode and a lockstep batch at that stride
     match the reference."""
@@ -84,7 +80,6 @@ def test_session_context_not_a_multiple_of_four(pairs, mode, monkeypatch):
     om, gm = _pair(pairs, "llama-q4k")
     cfg = SMALL["llama-q4k"][0]
     prompt = np.random.default_rng(5).integers(0, cfg.vocab_size, 21).astype(np.int32)
-    monkeypatch.setenv("SMX_DECODE", mode)
     sess = gm.create_session(83)
     toks, _, logits = sess.generate_greedy(prompt, 62, return_logits=True)
     osess = om.session(83)

@@ -545,3 +545,25 @@ def test_prefill_many_equals_prefill_each():
             b.step(int(t), q, want_logits=False)
     for a, b, p in zip(sa, sb, prompts):
         assert np.array_equal(a.step(int(p[-1]), len(p) - 1), b.step(int(p[-1]), len(p) - 1))
+
+
+def test_generate_crops_the_prompt_to_the_block_size():
+    """InferenceSession.cs:494-508: a context longer than blockSize is cropped to its last
+    blockSize tokens before the prefill.  The oracle's generate (the C restatement) against a
+    step-by-step run of the explicitly cropped prompt; one more token than the block holds is
+    refused, as TransformerModel.Forward refuses a position past the block (:280-283)."""
+    from smallmind_amd.model import ModelConfig
+    from tests.helpers import build_pair
+    cfg = ModelConfig("llama", 200, 24, 64, 2, 4, 2, 128)
+    om, _, _ = build_pair(cfg, O.Q4_K, O.Q6_K, O.Q6_K, seed=5, with_gpu=False)
+    prompt = np.random.default_rng(2).integers(0, cfg.vocab_size, 40).astype(np.int32)
+    toks, _, _ = om.generate_greedy(prompt, 1)
+    s = om.session(24)
+    for p, t in enumerate(prompt[-24:-1]):
+        s.step(int(t), p, want_logits=False)
+    ref = s.step(int(prompt[-1]), 23)
+    assert int(toks[0]) == int(np.argmax(ref))
+    with pytest.raises(ValueError):
+        om.generate_greedy(prompt, 2)
+    short, _, _ = om.generate_greedy(prompt[-20:], 5)
+    assert short.shape == (5,)
