@@ -131,6 +131,83 @@ def c2_gemv_lines():
     return out
 
 
+# Decode GEMV shapes whose roofline fractions are tracked (label, GGUF type, rows N, cols K):
+# the configs[2] Q4_K layer matrices and the configs[1] Q4_0 shapes.
+GEMV_TRACKED = [("configs[2] QKV", 12, 2560, 2048), ("configs[2] O", 12, 2048, 2048),
+                ("configs[2] gate/up", 12, 11264, 2048), ("configs[2] down", 12, 2048, 5632),
+                ("configs[1]", 2, 4096, 4096), ("configs[1]", 2, 11008, 4096), ("configs[1]", 2, 4096, 11008)]
+
+
+def gemv_shapes(launches: int):
+    """--gemv-shapes: the fused dequant-GEMV (IWeightTensor.MatMul, m = 1) at GEMV_TRACKED, each
+    launched over rotating weight copies (>= 600 MB, beyond the 256 MB MALL) so every launch
+    streams its weights from HBM.  Launches are eager (no graph) so rocprofv3 counter passes see
+    every dispatch; the HIP-event figure includes the launch gaps."""
+    import torch
+
+    from smallmind_amd.quantization import GpuWeightTensor, fill_normal, quantize, row_bytes
+    for label, qt, N, K in GEMV_TRACKED:
+        wbytes = N * row_bytes(qt, K)
+        copies = max(2, (600 << 20) // wbytes + 1)
+        blocks = quantize(qt, fill_normal(N * 3 + K, N * K, 0.02))
+        ws = [GpuWeightTensor(qt, N, K, blocks) for _ in range(copies)]
+        del blocks
+        x = torch.randn(K, device="cuda")
+        y = torch.empty(N, device="cuda")
+        for w in ws:
+            w.mat_mul(x, y, 1, K, N)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(launches):
+            ws[i % copies].mat_mul(x, y, 1, K, N)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / launches
+        print(f"{label:20s} type {qt:2d} {N:6d} x {K:5d}  {wbytes:9d} B  {us:7.2f} us per eager launch  "
+              f"{wbytes / (us * 1e-6) / 1e9:7.1f} GB/s", flush=True)
+        for w in ws:
+            w.close()
+        del ws
+
+
+# Matrix-core GEMM shapes (label, GGUF type, layer matrices (name, N, K), token counts M): the
+# 256-token chunk, the configs' prompt chunks (configs[2]: 511 tokens; configs[3]: 2048) and the
+# 16-session lockstep step of configs[4].
+_LLAMA_1B = [("qkv", 2560, 2048), ("o", 2048, 2048), ("gate_up", 11264, 2048), ("down", 2048, 5632)]
+_SMOLLM_17B = [("qkv", 6144, 2048), ("o", 2048, 2048), ("gate_up", 16384, 2048), ("down", 2048, 8192)]
+QGEMM_TRACKED = [("configs[2] Q4_K", 12, _LLAMA_1B, (256, 511)), ("configs[3] Q8_0", 8, _LLAMA_1B, (256, 2048)),
+                 ("configs[4] Q5_K", 13, _SMOLLM_17B, (256, 16))]
+
+
+def qgemm_shapes(reps: int):
+    """--qgemm-shapes: the matrix-core GEMM (IWeightTensor.MatMul with m >= 4: k_qprep +
+    k_qgemm_st) at QGEMM_TRACKED, eager launches with the weights resident; one line per shape
+    with microseconds per call, useful TFLOP/s (2 M N K) and its fraction of the 2.5 PFLOP/s
+    bf16 dense peak."""
+    import torch
+
+    from smallmind_amd.quantization import GpuWeightTensor, fill_normal, quantize
+    for label, qt, shapes, ms in QGEMM_TRACKED:
+        for name, N, K in shapes:
+            w = GpuWeightTensor(qt, N, K, quantize(qt, fill_normal(N + K, N * K, 0.02)))
+            for M in ms:
+                x = torch.randn(M, K, device="cuda")
+                y = torch.empty(M, N, device="cuda")
+                for _ in range(3):
+                    w.mat_mul(x, y, M, K, N)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(reps):
+                    w.mat_mul(x, y, M, K, N)
+                e1.record()
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / reps
+                tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+                print(f"{label:16s} {name:8s} M={M:5d} N={N:6d} K={K:5d}  {us:8.2f} us  {tf:7.2f} TFLOP/s  "
+                      f"{tf / MFMA_BF16_PEAK_TFLOPS:.4f} of bf16 peak", flush=True)
+            w.close()
+
+
 def decode_step_bytes(wl, mean_pos: float) -> int:
     """Algorithmic HBM bytes of one decode step (one token for each of wl.sessions sessions): every
     layer matrix and the head once per step, one embedding row (and one learned-position row)
@@ -337,6 +414,12 @@ def main():
                     help="skip the configs[0]/[3]/[4] measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--gemv-shapes", action="store_true",
+                    help="time the fused GEMV at the tracked decode shapes (eager launches, for rocprofv3)")
+    ap.add_argument("--qgemm-shapes", action="store_true",
+                    help="time the matrix-core GEMM at the tracked prefill / lockstep shapes (eager launches)")
+    ap.add_argument("--launches", type=int, default=200, help="launches per shape for --gemv-shapes")
+    ap.add_argument("--reps", type=int, default=20, help="calls per shape for --qgemm-shapes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each box has one "
@@ -350,6 +433,12 @@ def main():
 
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.gemv_shapes:
+        gemv_shapes(args.launches)
+        return
+    if args.qgemm_shapes:
+        qgemm_shapes(args.reps)
         return
     if args.roofline_only:
         g = gemv_roofline()

@@ -33,13 +33,38 @@ FLAGS = [
 ]
 
 
+# The fused GEMV keeps a row group's weight chunks in registers; an instance that spilled them
+# to scratch memory once returned wrong sums (F32, 4 rows x 4 chunks; cause not established), so
+# the build refuses any GEMV instance with scratch memory.
+SPILL_CHECKED = ("k_gemv.hip",)
+
+
+def _spilling_kernels(remarks: str) -> list:
+    """Kernels whose resource remark reports scratch memory (bytes per lane > 0)."""
+    out, name = [], None
+    for line in remarks.splitlines():
+        if "Function Name:" in line:
+            name = line.split("Function Name:", 1)[1].split()[0]
+        elif "ScratchSize [bytes/lane]:" in line and name:
+            if int(line.split("ScratchSize [bytes/lane]:", 1)[1].split()[0]) > 0:
+                out.append(name)
+    return out
+
+
 def _compile(entry) -> str:
     src, name, extra = entry
     obj = os.path.join(BUILD, name + ".o")
-    cmd = [HIPCC, *FLAGS, *extra, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    check = src in SPILL_CHECKED
+    cmd = [HIPCC, *FLAGS, *extra, *(["-Rpass-analysis=kernel-resource-usage"] if check else []),
+           "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
+    if check:
+        bad = _spilling_kernels(r.stderr)
+        if bad:
+            os.remove(obj)
+            raise RuntimeError(f"{src} ({' '.join(extra)}): GEMV instances use scratch memory: {bad}")
     return obj
 
 

@@ -332,7 +332,12 @@ SMX_API int smx_model_load_smq(smx_context *ctx, const char *path, const smx_mod
             const int64_t dims[1] = {ne};
             rc = smx_model_upload_tensor(m, names[i].c_str(), SMX_TYPE_F32, dims, 1, vec.data(), vec.size() * 4, 0);
         } else {
-            if (t.dims.size() != 2) SQ_FAIL(SMX_EUNSUPPORTED, "smq: %s: rank %zu matrix", t.name.c_str(), t.dims.size());
+            if (t.dims.size() != 2) {   // the model is created: release it with the error
+                char b[512];
+                snprintf(b, sizeof(b), "smq: %s: rank %zu matrix", t.name.c_str(), t.dims.size());
+                set_error(b);
+                return fail(SMX_EUNSUPPORTED);
+            }
             const int64_t rows = t.dims[0], cols = t.dims[1];
             const int64_t gdims[2] = {cols, rows};   // upload dims: ne0 = cols
             if (t.type == kSmqF32) {

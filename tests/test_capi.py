@@ -110,3 +110,22 @@ def test_stopped_generation_maps_to_the_reference_exception(monkeypatch, rc, cls
     cs = open(os.path.join(ROOT, "smallmind_amd", "bindings", "csharp", "Smx.cs")).read()
     name = {-8: "ECANCELED", -9: "ETIMEDOUT"}[rc]
     assert re.search(rf"\b{name}\s*=>\s*new {reference}\(", cs), (name, reference)
+
+
+def test_build_refuses_gemv_instances_with_scratch_memory():
+    """The build reads the compiler's resource remarks for the GEMV source and fails on any
+    instance with scratch memory (an instance that spilled its weight registers once returned
+    wrong sums)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("smx_build", os.path.join(ROOT, "smallmind_amd", "build.py"))
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    remarks = "\n".join([
+        "k_gemv.hip:206:1: remark: Function Name: _ZN3smx6k_gemvILi4E [-Rpass-analysis=kernel-resource-usage]",
+        "k_gemv.hip:206:1: remark:     VGPRs: 254 [-Rpass-analysis=kernel-resource-usage]",
+        "k_gemv.hip:206:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "k_gemv.hip:206:1: remark: Function Name: _ZN3smx6k_gemvILi2E [-Rpass-analysis=kernel-resource-usage]",
+        "k_gemv.hip:206:1: remark:     ScratchSize [bytes/lane]: 436 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert b._spilling_kernels(remarks) == ["_ZN3smx6k_gemvILi2E"]
+    assert "k_gemv.hip" in b.SPILL_CHECKED

@@ -68,16 +68,37 @@ def test_configs2_bench_workload_64_steps(gpu):
 @pytest.mark.timeout(900)
 def test_configs0_gpt2_small_full_size(gpu):
     """GPT-2-small (12 layers, d768, V 50257 -- the head's last row group holds one
-    row), Q8_0 everywhere, tied head, learned positions; 32-token prompt, 64 greedy steps."""
+    row), Q8_0 everywhere, tied head, learned positions; 32-token prompt, 64 greedy steps.
+    A random-init GPT-2 with a tied head keeps choosing its input token, so token identity alone
+    says little here: at every step the order of the oracle's five largest logits is also
+    required wherever two neighbours differ by more than 1e-3 of the largest |logit|."""
     from smallmind_amd.synthetic import prompt_tokens
+    from tests.helpers import rel_err
     wl, gm, om = _build("gpt2-small-q8_0")
     try:
         cfg = wl.config
         prompt = prompt_tokens(7, wl.prompt_len, cfg.vocab_size)
         s = gm.create_session(wl.prompt_len + wl.new_tokens)
         toks, _, logits = s.generate_greedy(prompt, 64, return_logits=True)
-        worst = check_greedy_against_oracle(om.session(wl.prompt_len + 64), prompt, toks, logits, LOGIT_TOL)
-        _say(f"configs[0]: 64 steps match the oracle (worst logits error {worst:.2e})")
+        osess = om.session(wl.prompt_len + 64)
+        osess.prefill(prompt[:-1], 0)
+        tok, worst, pairs = int(prompt[-1]), 0.0, 0
+        for i in range(64):
+            ref = osess.step(tok, len(prompt) - 1 + i)
+            err = rel_err(logits[i], ref)
+            worst = max(worst, err)
+            assert err <= LOGIT_TOL, (i, err)
+            assert int(toks[i]) == int(np.argmax(ref)), i
+            top = np.argsort(-ref, kind="stable")[:6]
+            thr = 1e-3 * float(np.abs(ref).max())
+            for a, b in zip(top[:5], top[1:6]):
+                if ref[a] - ref[b] > thr:
+                    assert logits[i][a] > logits[i][b], (i, int(a), int(b))
+                    pairs += 1
+            tok = int(toks[i])
+        assert pairs >= 32, pairs   # the check must bite: most steps have separated neighbours
+        _say(f"configs[0]: 64 steps match the oracle (worst logits error {worst:.2e}); top-5 order held at "
+             f"{pairs} neighbour pairs")
         bench_toks, _ = s.generate_greedy(prompt, wl.new_tokens)
         assert np.array_equal(bench_toks[:64], toks)
         s.close()

@@ -103,3 +103,29 @@ def test_explicit_config_and_missing_tensor_are_reported(gpu, tmp_path):
     with pytest.raises(SmxError) as e:
         GpuTransformerModel.from_smq(str(q))
     assert "layer 1" in str(e.value)
+
+
+def test_matrix_of_wrong_rank_is_refused_and_released(gpu, tmp_path):
+    """An F32 weight matrix stored with rank 3 passes the directory checks (SmqReader takes any
+    rank for F32) but is no matrix: the load fails with SMX_EUNSUPPORTED after earlier tensors were
+    uploaded, and releases the partly built model (device memory back to where it was)."""
+    import torch
+
+    from smallmind_amd._lib import SmxError
+    from smallmind_amd.model import GpuTransformerModel
+    cfg = ModelConfig("gpt2", 1000, 128, 256, 2, 4, 4, 1024)
+    tens = _gpt2_tensors(cfg, S.Q8_0, 32, 5, True)
+    last = [t.name for t in tens if len(t.dims) == 2 and t.dims[0] > 1][-1]
+    bad = [S.SmqTensor(t.name, S.F32, (t.dims[0], t.dims[1], 1),
+                       np.random.default_rng(1).normal(0, 0.02, t.dims[0] * t.dims[1]).astype(np.float32))
+           if t.name == last else t for t in tens]
+    p = tmp_path / "rank3.smq"
+    S.write_smq(str(p), bad, S.gpt2_metadata(cfg))
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(4):
+        with pytest.raises(SmxError) as e:
+            GpuTransformerModel.from_smq(str(p))
+        assert e.value.code == -5 and "rank 3" in str(e.value)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] >= free0 - (1 << 20)
