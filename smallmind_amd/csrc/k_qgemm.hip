@@ -26,6 +26,8 @@
 //
 // Activation parts come from k_qprep: Xp[tt][s][p][g][t][8 bf16] (1 KB per (token tile,
 // sub-block, part), lane l reads 16 bytes at l*16).
+#include <algorithm>
+
 #include "smx_device.h"
 #include "smx_formats.h"
 #include "smx_internal.h"
@@ -694,8 +696,21 @@ __device__ __forceinline__ RawQ stage_raw(const uint8_t *row, const uint32_t *dr
     return r;
 }
 
+// Tile order of a launch with several token-tile groups.  The 2-D grid (row tile x, token group
+// y) runs the row tiles fastest, and workgroups land on the 8 XCDs round robin, so each XCD works
+// on 1/8 of W for ~1.5 token groups at a time: W's slice plus those groups' activation parts
+// exceed the XCD's 4 MB L2, and W is fetched again for every token group.  With G > 0 the grid
+// is 1-D and workgroup i runs tile t = (i % 8) * chunk + i / 8 of a panel-major order (panels of
+// G token groups whose parts stay in the L2, row tiles in a panel with the G groups fastest), so
+// each XCD works through one contiguous chunk of that order: the parts of its panel stay
+// resident and each W tile is read once per panel by G workgroups in a row.
+struct TileSched {
+    uint32_t R, T;       // row tiles, token-tile groups
+    uint32_t G, chunk;   // groups per panel (0: the 2-D grid), tiles per XCD
+};
+
 template <int F, int RT, int TT, int NW>
-__global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
+__global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a, TileSched ts)
 {
     using Q = QW<F>;
     using G = Stage<F>;
@@ -715,8 +730,21 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a)
     const uint32_t lane16 = (uint32_t)lane * 16u;
     const uint32_t N = (uint32_t)w.rows;
     const int nsb = (int)(w.cols >> 5), nsup = nsb >> 3;
-    const uint32_t row_base = blockIdx.x * R16;
-    const int tt0 = blockIdx.y * TT;
+    uint32_t bx = blockIdx.x, by = blockIdx.y;
+    // one token tile (the lockstep step): never scheduled, and the latency-bound launch reads
+    // no schedule argument (reading and testing it cost 2 % of the configs[4] step)
+    if constexpr (TT > 1) {
+        if (ts.G) {   // wave-uniform: the whole workgroup takes the same branch
+            const uint32_t i = blockIdx.x, t = (i & 7u) * ts.chunk + (i >> 3);
+            if (t >= ts.R * ts.T) return;
+            const uint32_t pt = ts.R * ts.G, panel = t / pt, rem = t - panel * pt;
+            const uint32_t gp = min(ts.G, ts.T - panel * ts.G);
+            bx = rem / gp;
+            by = panel * ts.G + (rem - bx * gp);
+        }
+    }
+    const uint32_t row_base = bx * R16;
+    const int tt0 = (int)by * TT;
     const int ntt = (M + 15) >> 4;
     const uint32_t row_bytes = (uint32_t)nsup * G::kBytes;
     // contiguous super-block range of this wave
@@ -1185,8 +1213,21 @@ hipError_t launch_frt(const QgemmArgs &a, hipStream_t s)
 template <int F, int RT, int TT, int NW>
 hipError_t launch_st(const QgemmArgs &a, hipStream_t s)
 {
-    const dim3 grid((unsigned)((a.w.rows + 16 * RT - 1) / (16 * RT)), (unsigned)(((a.M + 15) / 16 + TT - 1) / TT));
-    hipLaunchKernelGGL((k_qgemm_st<F, RT, TT, NW>), grid, dim3(64 * NW), 0, s, a);
+    const uint32_t R = (uint32_t)((a.w.rows + 16 * RT - 1) / (16 * RT));
+    const uint32_t T = (uint32_t)(((a.M + 15) / 16 + TT - 1) / TT);
+    TileSched ts{R, T, 0, 0};
+    dim3 grid(R, T);
+    // From 1024 tokens: panels of G token groups whose activation parts (TT tiles x K/32
+    // sub-blocks x 3 KB each) fill ~1.5 MB of an XCD's 4 MB L2.  Measured (configs[3] Q8_0 at
+    // 2048 tokens): L2 fills 2-2.3x lower (gate/up 16x -> 8.6x the algorithmic bytes), kernel
+    // times 0-2 % lower; at 511 tokens the 2-D order is 2-5 % faster, so shorter chunks keep it.
+    if (TT > 1 && T > 1 && a.M >= 1024) {
+        const uint64_t group_bytes = (uint64_t)TT * (uint64_t)(a.w.cols / 32) * 3072u;
+        ts.G = (uint32_t)std::min<uint64_t>(T, std::max<uint64_t>(1, (3u << 19) / group_bytes));
+        ts.chunk = (R * T + 7) / 8;
+        grid = dim3(8 * ts.chunk, 1);
+    }
+    hipLaunchKernelGGL((k_qgemm_st<F, RT, TT, NW>), grid, dim3(64 * NW), 0, s, a, ts);
     return hipGetLastError();
 }
 

@@ -92,8 +92,13 @@ def test_matmul_m_rows_equals_gemv_rows(gpu, name):
                                    (64, 1000, 2048), (100, 48, 5632), (16, 40, 160),
                                    (20, 8200, 256), (9, 300, 8192),
                                    # prefill-chunk tiles: 512 / 1100 tokens on few-row, long-K
-                                   # and other matrices (every 5th row checked)
-                                   (511, 2048, 2048), (517, 2560, 2048), (1100, 1040, 5632)])
+                                   # and other matrices (every 5th row checked); from 1024 tokens
+                                   # the XCD panel order (1100: one token group per panel;
+                                   # 2600 x 2048 at 1504 tokens: 47 token groups in panels of 3
+                                   # for the K-quants, a partial last panel, 82 row tiles of
+                                   # which the last is ragged)
+                                   (511, 2048, 2048), (517, 2560, 2048), (1100, 1040, 5632),
+                                   (1504, 2600, 2048)])
 def test_matmul_matrix_core_path_vs_oracle(gpu, name, m, N, K):
     """m >= 4 rows: bf16 MFMA on exact integer codes and three-part activations; held to the
     same bounds as the GEMV, row by row (ragged m and N exercise the tile padding)."""
