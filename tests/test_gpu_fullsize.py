@@ -19,6 +19,7 @@ from tests.helpers import check_greedy_against_oracle, oracle_from_kept
 pytestmark = pytest.mark.gpu
 
 LOGIT_TOL = 1e-3
+N4 = 64   # configs[4]: oracle-checked steps per session (16 sessions)
 
 
 def _say(msg):
@@ -109,7 +110,7 @@ def test_configs0_gpt2_small_full_size(gpu):
 @pytest.mark.timeout(900)
 def test_configs4_sixteen_sessions_full_size(gpu):
     """SmolLM-1.7B Q5_K, tied embeddings, 16 sessions with the bench's prompts
-    (prompt_tokens(100 + i, 256)).  Every session's first 8 steps (logits and tokens) against
+    (prompt_tokens(100 + i, 256)).  Every session's first 64 steps (logits and tokens) against
     the oracle; then all 128 tokens of every session are the same whether the session decodes
     alone (GEMV graphs), in the lockstep batch (smx_batch_generate, 16-token GEMM with folded
     RMSNorm) or through the continuous batcher one step per call."""
@@ -123,10 +124,10 @@ def test_configs4_sixteen_sessions_full_size(gpu):
         alone, first = [], []
         for p in prompts:
             s = gm.create_session(ctx)
-            t8, _, l8 = s.generate_greedy(p, 8, return_logits=True)
+            t8, _, l8 = s.generate_greedy(p, N4, return_logits=True)
             first.append((t8, l8))
             t, _ = s.generate_greedy(p, wl.new_tokens)
-            assert np.array_equal(t[:8], t8)
+            assert np.array_equal(t[:N4], t8)
             alone.append(t)
             s.close()
         sess = [gm.create_session(ctx) for _ in range(n)]
@@ -148,7 +149,7 @@ def test_configs4_sixteen_sessions_full_size(gpu):
         _say(f"configs[4]: oracle prefill of 16 x 255 tokens in {time.time() - t0:.1f} s")
         tok = [int(p[-1]) for p in prompts]
         worst = 0.0
-        for k in range(8):
+        for k in range(N4):
             ref = om.multi_step(osess, tok, [wl.prompt_len - 1 + k] * n)
             for i in range(n):
                 err = float(np.abs(first[i][1][k] - ref[i]).max() / np.abs(ref[i]).max())
@@ -156,7 +157,7 @@ def test_configs4_sixteen_sessions_full_size(gpu):
                 assert err <= LOGIT_TOL, (i, k, err)
                 assert int(first[i][0][k]) == int(np.argmax(ref[i])), (i, k)
             tok = [int(first[i][0][k]) for i in range(n)]
-        _say(f"configs[4]: 16 sessions x 8 steps match the oracle (worst logits error {worst:.2e}, "
+        _say(f"configs[4]: 16 sessions x {N4} steps match the oracle (worst logits error {worst:.2e}, "
              f"{time.time() - t0:.1f} s)")
     finally:
         gm.close()
@@ -165,18 +166,19 @@ def test_configs4_sixteen_sessions_full_size(gpu):
 @pytest.mark.timeout(900)
 def test_configs3_long_prompt_full_size(gpu):
     """LLaMA-1.1B with Q8_0 layers and a Q6_K head, the bench's 4096-token prompt
-    through 16 prefill chunks (matrix-core GEMM + prefill attention), then 8 greedy decode
-    steps at ~4.1K positions (two-workgroup P.V attention) against the oracle."""
+    through two 2048-token prefill chunks (matrix-core GEMM in the XCD panel order + prefill
+    attention), then 64 greedy decode steps at ~4.1K positions (two-workgroup P.V attention)
+    against the oracle."""
     from smallmind_amd.synthetic import prompt_tokens
     wl, gm, om = _build("llama-1.1b-q8_0-4k")
     try:
         cfg = wl.config
         prompt = prompt_tokens(7, wl.prompt_len, cfg.vocab_size)
         s = gm.create_session(wl.prompt_len + wl.new_tokens)
-        toks, _, logits = s.generate_greedy(prompt, 8, return_logits=True)
+        toks, _, logits = s.generate_greedy(prompt, 64, return_logits=True)
         t0 = time.time()
-        worst = check_greedy_against_oracle(om.session(wl.prompt_len + 8), prompt, toks, logits, LOGIT_TOL)
-        _say(f"configs[3]: 8 steps at 4096+ positions match the oracle (worst {worst:.2e}, "
+        worst = check_greedy_against_oracle(om.session(wl.prompt_len + 64), prompt, toks, logits, LOGIT_TOL)
+        _say(f"configs[3]: 64 steps at 4096+ positions match the oracle (worst {worst:.2e}, "
              f"oracle {time.time() - t0:.1f} s)")
         s.close()
     finally:
