@@ -396,7 +396,7 @@ namespace SmallMind.Backends.Rocm
             if (maxTimeMs < 0) throw new ArgumentOutOfRangeException(nameof(maxTimeMs));
             cancellationToken.ThrowIfCancellationRequested();
             var outTokens = new int[nNew];
-            Smx.GenStats stats;
+            Smx.GenStats stats = default;
             Smx.Check(Smx.smx_session_set_max_time(_s, maxTimeMs));
             int rc;
             using (cancellationToken.Register(() => Smx.smx_session_cancel(_s)))
