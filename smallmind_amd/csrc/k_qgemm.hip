@@ -27,6 +27,7 @@
 // Activation parts come from k_qprep: Xp[tt][s][p][g][t][8 bf16] (1 KB per (token tile,
 // sub-block, part), lane l reads 16 bytes at l*16).
 #include <algorithm>
+#include <type_traits>
 
 #include "smx_device.h"
 #include "smx_formats.h"
@@ -295,7 +296,7 @@ constexpr uint32_t kOnes = 0x3F803F80u;   // bf16 1.0 pair
 // epilogue: the token's position, the RoPE factors of the row's pair (when it is rotated) and
 // the token's K or V cache base (for K / V rows).
 struct QkvPre {
-    int pos;
+    uint32_t pos;   // never negative: widening it is a zero extension, which waits for no load
     float c, sn;
     float *cache;
 };
@@ -344,7 +345,7 @@ __device__ __forceinline__ float qgemm_epilogue(const QgemmArgs &a, float v, uin
     case EPI_QKV: {
         if (row & 1) break;
         const int d = a.d_model, kv = a.kv_dim, hd = a.head_dim, r = (int)row;
-        const int pos = pre ? qp.pos : a.tok_pos[tok];
+        const uint32_t pos = pre ? qp.pos : (uint32_t)a.tok_pos[tok];
         float v0 = v, v1 = nb;
         if (a.use_rope && r < d + kv) {
             const int pair = ((r < d ? r : r - d) % hd) / 2, half = hd / 2;
@@ -1001,6 +1002,250 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a, TileSched ts)
     }
 }
 
+// ---- row-split variant for one token tile ---------------------------------------------------
+// Up to 16 tokens, the K-split workgroups above each read the activation parts of the whole K
+// for their own 16-32 rows (6 bytes per token and k against 0.69 bytes per Q5_K weight), and
+// a wave can only hold a few sub-blocks of them in registers, so its part loads queue behind
+// its weight loads.  Here a workgroup of NW = NR * NKH waves owns NR row tiles (16 rows each)
+// and the whole K: wave (r, h) multiplies row tile r by the sub-blocks h * 8 / NKH ... of every
+// super-block.  Super-block by super-block, a slot of an NS-slot LDS ring receives the
+// super-block's activation parts (24 KB, read by every wave) and its NR * 16 rows of weights,
+// both loaded straight into LDS (global_load_lds_dwordx4, no registers) NS - 1 super-blocks
+// ahead of use; one barrier per super-block publishes a slot.  Each wave issues the same
+// number of loads per super-block (every one with at least one active lane), so the wait for
+// a slot is a fixed vector-memory count.  The loads into LDS are issued by inline assembly:
+// through the builtin, the compiler cannot tell the slots apart in this kernel and waits for
+// every load into LDS in flight before each LDS read, which leaves no load in flight across a
+// super-block's multiplications.  The explicit wait before each barrier is what orders a
+// slot's reads after its loads.
+template <int F, int NR> struct RsSlot {
+    uint4 xp[24][64];                  // [sub-block][part] x (64 lanes x 16 bytes)
+    uint4 w[NR * Stage<F>::kBytes];    // NR * 16 rows x kBytes, row-major, in 16-byte pieces
+};
+
+template <int N> using ic = std::integral_constant<int, N>;
+
+// 16 bytes per lane from global address g into LDS at l + 16 * lane (l wave-uniform; M0 holds
+// it, with the one wait state between the M0 write and the load)
+__device__ __forceinline__ void lds_dma16(const void *g, void *l)
+{
+    const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)l;
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(la) : "memory");
+}
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt in bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8)
+template <int N> __device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int F, int NR, int NKH, int NS>
+__global__ __launch_bounds__(64 * NR * NKH) void k_qgemm_rs(QgemmArgs a)
+{
+    using Q = QW<F>;
+    constexpr int kB = Stage<F>::kBytes;
+    constexpr int NW = NR * NKH, JP = 8 / NKH;
+    constexpr int WP = NR * kB;            // 16-byte weight pieces per super-block
+    constexpr int PPW = WP / NW;           // ... per wave
+    constexpr int WI = (PPW + 63) / 64;    // weight loads per wave and super-block
+    constexpr int NPW = 24 / NW;           // part loads per wave and super-block
+    constexpr int L = WI + NPW;            // vector-memory instructions per wave and super-block
+    static_assert(Stage<F>::kDW == 0, "weights without a separate scale stream");
+    static_assert(WP % NW == 0 && 24 % NW == 0 && 8 % NKH == 0 && NS >= 2 && NS <= 4, "work split");
+    static_assert((NS - 2) * L < 64, "vmcnt range");
+    __shared__ RsSlot<F, NR> slot[NS];
+    __shared__ f32x4 s_part[NKH > 1 ? NKH - 1 : 1][NR][64];
+    __shared__ float s_r[16];
+    const WView &w = a.w;
+    const int M = a.M;
+    const int wv = wave_id();
+    const int r = wv % NR, h = wv / NR;
+    const int lane = lane_id();
+    const int g = lane >> 4, li = lane & 15;
+    const uint32_t N = (uint32_t)w.rows;
+    const int nsup = (int)(w.cols >> 8);
+    const uint32_t row_base = blockIdx.x * (16u * NR);
+    const uint32_t row_bytes = (uint32_t)nsup * kB;
+    const uint32_t my_row = row_base + 16u * r + (uint32_t)li;
+
+    // loads of super-block sup into a slot: this wave's parts (instructions wv * NPW ...) and
+    // its share of the weight pieces (wv * PPW ...)
+    auto issue = [&](int sup, auto &S) {
+        const uint8_t *xs = a.xp + (size_t)sup * (24u * 1024u) + (uint32_t)lane * 16u;
+#pragma unroll
+        for (int k = 0; k < NPW; k++) {
+            const int c = wv * NPW + k;
+            lds_dma16(xs + c * 1024, &S.xp[c][0]);
+        }
+#pragma unroll
+        for (int k = 0; k < WI; k++) {
+            const int q = wv * PPW + 64 * k + lane;
+            if (64 * k + lane < PPW) {
+                const int rw = q / (kB / 16), col = q % (kB / 16);
+                const uint32_t gr = min(row_base + (uint32_t)rw, N - 1);
+                lds_dma16(w.q + gr * row_bytes + (uint32_t)sup * kB + 16u * col, &S.w[wv * PPW + 64 * k]);
+            }
+        }
+    };
+    // the first super-blocks' loads go out before anything else
+#pragma unroll
+    for (int i = 0; i < NS - 1; i++)
+        if (i < nsup) issue(i, slot[i]);
+
+    // Folded RMSNorm: the tile sums of x^2 of wave wv's tokens wv + NW*j, requested here and
+    // reduced after the main loop.
+    constexpr int RJ = (16 + NW - 1) / NW, RP = 4;
+    float rl[RJ][RP];
+    const bool fold = a.rss != nullptr;
+    if (fold) {
+#pragma unroll
+        for (int j = 0; j < RJ; j++) {
+            const int tk = min(wv + NW * j, M - 1);
+#pragma unroll
+            for (int q = 0; q < RP; q++) {
+                const int p = lane + 64 * q;
+                rl[j][q] = p < a.rss_n ? a.rss[(int64_t)p * M + tk] : 0.0f;
+            }
+        }
+    }
+    // The epilogue waves' residual values and next-norm gamma (EPI_RESID), or their tokens'
+    // positions (EPI_QKV), requested at entry so that the epilogue's stores wait for no load.
+    const bool pre = a.epi == EPI_RESID || a.epi == EPI_QKV;
+    const bool preq = a.epi == EPI_QKV;
+    float pres[4] = {0.0f, 0.0f, 0.0f, 0.0f}, pg = 0.0f;
+    QkvPre qp[4] = {};
+    if (pre && h == 0) {
+        const uint32_t rc = min(my_row, N - 1);
+        if (preq) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) qp[i].pos = a.tok_pos[min(4 * g + i, M - 1)];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) pres[i] = a.y[(int64_t)min(4 * g + i, M - 1) * a.y_stride + rc];
+            if (a.np) pg = a.ngamma[rc];
+        }
+    }
+
+    // Publishes the slot of super-block i: this wave's loads of it have landed (the loads of
+    // the n_after later super-blocks already issued may still be in flight), then every wave's.
+    auto sync = [&](int n_after) {
+        asm volatile("" ::: "memory");
+        if (NS > 3 && n_after >= 2) wait_vm<(NS > 3 ? 2 * L : 0)>();
+        else if (NS > 2 && n_after >= 1) wait_vm<(NS > 2 ? L : 0)>();
+        else wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint4 ones = make_uint4(kOnes, kOnes, kOnes, kOnes);
+    auto compute = [&](const auto &S) {
+        const uint8_t *wrow = (const uint8_t *)S.w + (16 * r + li) * kB;
+        auto body = [&](auto hc) {
+            constexpr int H = decltype(hc)::value;
+#pragma unroll
+            for (int jj = 0; jj < JP; jj++) {
+                const int j = H * JP + jj;
+                uint4 xa[3];
+#pragma unroll
+                for (int p = 0; p < 3; p++) xa[p] = S.xp[3 * j + p][lane];
+                const RawQ raw = stage_raw<F>(wrow, nullptr, j, g);
+                const uint4 wc = Q::codes(raw, g);
+                const Scl sc = Q::scale(raw, j);
+                f32x4 sa = {0.0f, 0.0f, 0.0f, 0.0f}, dc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int p = 0; p < 3; p++) sa = mfma(xa[p], ones, sa);
+#pragma unroll
+                for (int p = 0; p < 3; p++) dc = mfma(xa[p], wc, dc);
+                const float c = sc.sc, cs = sc.sc * Q::kOff + sc.m;
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i] = accumulate1(acc[i], c, cs, dc[i], sa[i]);
+            }
+        };
+        if constexpr (NKH == 1) body(ic<0>{});
+        else if constexpr (NKH == 2) { if (h == 0) body(ic<0>{}); else body(ic<1>{}); }
+        else if constexpr (NKH == 4) {
+            if (h == 0) body(ic<0>{}); else if (h == 1) body(ic<1>{}); else if (h == 2) body(ic<2>{}); else body(ic<3>{});
+        } else {
+            switch (h) {
+            case 0: body(ic<0>{}); break;
+            case 1: body(ic<1>{}); break;
+            case 2: body(ic<2>{}); break;
+            case 3: body(ic<3>{}); break;
+            case 4: body(ic<4>{}); break;
+            case 5: body(ic<5>{}); break;
+            case 6: body(ic<6>{}); break;
+            default: body(ic<7>{}); break;
+            }
+        }
+    };
+    // super-block i lives in slot i % NS; its loads were issued NS - 1 super-blocks earlier,
+    // into the slot that super-block i - 1 used, which every wave finished reading before the
+    // barrier of step i
+    for (int i = 0; i < nsup; i++) {
+        sync(min(NS - 2, nsup - 1 - i));
+        if (i + NS - 1 < nsup) issue(i + NS - 1, slot[(i + NS - 1) % NS]);
+        compute(slot[i % NS]);
+    }
+
+    if (preq && h == 0) {
+        const int d = a.d_model, kv = a.kv_dim, hd = a.head_dim, half = hd / 2;
+        const int rr = (int)min(my_row, N - 1);
+        const int pair = ((rr < d ? rr : rr - d) % hd) / 2;
+        const bool rot = a.use_rope && rr < d + kv && !(rr & 1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tk = min(4 * g + i, M - 1);
+            qp[i].c = rot ? a.rope_cos[(int64_t)qp[i].pos * half + pair] : 0.0f;
+            qp[i].sn = rot ? a.rope_sin[(int64_t)qp[i].pos * half + pair] : 0.0f;
+            qp[i].cache = rr < d ? nullptr : (rr < d + kv ? a.kc_tok[tk] : a.vc_tok[tk]);
+        }
+    }
+    if (fold) {   // r = 1 / sqrt(sum x^2 / K + eps) (RMSNormOps.cs:114)
+#pragma unroll
+        for (int j = 0; j < RJ; j++) {
+            float t = rl[j][0];
+#pragma unroll
+            for (int q = 1; q < RP; q++) t += rl[j][q];
+            t = wave_sum_uniform(t);
+            if (lane == 0 && wv + NW * j < 16) s_r[wv + NW * j] = 1.0f / sqrtf(t / (float)w.cols + a.r_eps);
+        }
+    }
+    // sum the NKH partial tiles of each row tile in a fixed order; wave (r, 0) applies the
+    // epilogue
+    if (NKH > 1 && h > 0) s_part[h - 1][r][lane] = acc;
+    __syncthreads();   // s_part, and the folded-norm factors in s_r
+    if (h != 0) return;
+    float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if (fold) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) rs[i] = s_r[4 * g + i];
+    }
+    f32x4 v = acc;
+#pragma unroll
+    for (int k = 0; k < NKH - 1; k++) {
+        const f32x4 o = s_part[k][r][lane];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] += o[i];
+    }
+    float sq[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float xn = qgemm_epilogue(a, v[i] * rs[i], my_row, 4 * g + i, true, pre, pres[i], pg, qp[i]);
+        sq[i] = xn * xn;
+    }
+    if (a.np != nullptr) {   // producer of a folded norm: x^2 summed over the tile's 16 rows
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float t = row16_sum(sq[i]);
+            const int tok = 4 * g + i;
+            if (li == 0 && tok < M) a.nss[(int64_t)(row_base / 16 + r) * M + tok] = t;
+        }
+    }
+}
+
 // Activation parts: token m, sub-block s, part p -> Xp[m/16][s][p][g][m%16][perm] (bf16).
 // x = hi + mid + lo with hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid), each
 // rounded to nearest even (bf16_rne, xp_store); tokens beyond M (tile padding) are zero.
@@ -1231,6 +1476,14 @@ hipError_t launch_st(const QgemmArgs &a, hipStream_t s)
     return hipGetLastError();
 }
 
+template <int F, int NR, int NKH, int NS>
+hipError_t launch_rs(const QgemmArgs &a, hipStream_t s)
+{
+    const dim3 grid((unsigned)((a.w.rows + 16 * NR - 1) / (16 * NR)));
+    hipLaunchKernelGGL((k_qgemm_rs<F, NR, NKH, NS>), grid, dim3(64 * NR * NKH), 0, s, a);
+    return hipGetLastError();
+}
+
 template <int F>
 hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
 {
@@ -1259,6 +1512,11 @@ hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
             if (narrow && a.M < 1024) return launch_st<F, 2, 4, 8>(a, s);
             return launch_st<F, 2, 4, 4>(a, s);
         }
+        // tall K-quant matrices up to one workgroup of 64 rows per CU: the row-split kernel
+        // (configs[4] gate/up 16.9 -> 13.6 us; the 49152-row head stays faster on the K-split
+        // kernel's several workgroups per CU)
+        if constexpr (F == FMT_Q4_K || F == FMT_Q5_K)
+            if (tall && a.w.rows <= 256 * 64) return launch_rs<F, 4, 2, 3>(a, s);
         if constexpr (F != FMT_Q6_K)   // 16 waves of >= 2 super-blocks (Q6_K would spill at 128 registers)
             if (a.w.cols >= 8192) return launch_st<F, 1, 1, 16>(a, s);
         return tall ? launch_st<F, 2, 1, 4>(a, s) : launch_st<F, 1, 1, 8>(a, s);

@@ -20,6 +20,26 @@ pytestmark = pytest.mark.gpu
 
 LOGIT_TOL = 1e-3
 N4 = 64   # configs[4]: oracle-checked steps per session (16 sessions)
+# Paths that reach a step through different kernels (GEMV or 16-token GEMM decode, per-session
+# or batched prefill) sum in different orders, so their logits differ by ~1e-6 of max|logit|.
+# Where the reference's two best logits are closer than that, either path may pick either token:
+# greedy sequences of two paths must be identical except at such a near-tie, where the other
+# path must take the reference's second choice (the sequences part there).
+TIE_TOL = 1e-4
+
+
+def _same_tokens_or_near_tie(other, ref_toks, ref_logits):
+    """None if the token sequences are equal; else the first differing step, after checking that
+    it is a near-tie of the reference logits resolved to the runner-up."""
+    diff = np.nonzero(np.asarray(other) != np.asarray(ref_toks))[0]
+    if len(diff) == 0:
+        return None
+    k = int(diff[0])
+    lg = ref_logits[k]
+    top2 = np.argsort(lg)[::-1][:2]
+    margin = float((lg[top2[0]] - lg[top2[1]]) / np.abs(lg).max())
+    assert margin <= TIE_TOL and int(other[k]) == int(top2[1]), (k, margin, int(other[k]), top2.tolist())
+    return k
 
 
 def _say(msg):
@@ -112,8 +132,10 @@ def test_configs4_sixteen_sessions_full_size(gpu):
     """SmolLM-1.7B Q5_K, tied embeddings, 16 sessions with the bench's prompts
     (prompt_tokens(100 + i, 256)).  Every session's first 64 steps (logits and tokens) against
     the oracle; then all 128 tokens of every session are the same whether the session decodes
-    alone (GEMV graphs), in the lockstep batch (smx_batch_generate, 16-token GEMM with folded
-    RMSNorm) or through the continuous batcher one step per call."""
+    alone (GEMV graphs), in the lockstep batch (smx_batch_generate, 16-token split-K GEMM with
+    folded RMSNorm) or through the continuous batcher one step per call -- up to a near-tie of
+    the single-session logits (top-2 margin <= TIE_TOL of max|logit|), where the batch path must
+    take the runner-up.  (Session 5 has one at step 35: margin 4.6e-6.)"""
     from smallmind_amd.model import ContinuousBatcher, GpuInferenceSession
     from smallmind_amd.synthetic import prompt_tokens
     wl, gm, om = _build("smollm-1.7b-q5_k")
@@ -121,14 +143,15 @@ def test_configs4_sixteen_sessions_full_size(gpu):
         cfg = wl.config
         n, ctx = wl.sessions, wl.prompt_len + wl.new_tokens
         prompts = [prompt_tokens(100 + i, wl.prompt_len, cfg.vocab_size) for i in range(n)]
-        alone, first = [], []
+        alone, alone_logits, first = [], [], []
         for p in prompts:
             s = gm.create_session(ctx)
-            t8, _, l8 = s.generate_greedy(p, N4, return_logits=True)
-            first.append((t8, l8))
+            tl, _, ll = s.generate_greedy(p, wl.new_tokens, return_logits=True)
+            first.append((tl[:N4], ll[:N4]))
             t, _ = s.generate_greedy(p, wl.new_tokens)
-            assert np.array_equal(t[:N4], t8)
+            assert np.array_equal(t, tl)
             alone.append(t)
+            alone_logits.append(ll)
             s.close()
         sess = [gm.create_session(ctx) for _ in range(n)]
         lock, _ = GpuInferenceSession.generate_greedy_batch(sess, prompts, wl.new_tokens)
@@ -139,10 +162,15 @@ def test_configs4_sixteen_sessions_full_size(gpu):
         b.close()
         for x in sess:
             x.close()
+        ties = []
         for i in range(n):
-            assert np.array_equal(lock[i], alone[i]), (i, int(np.argmax(lock[i] != alone[i])))
-            assert np.array_equal(cont[i], alone[i]), (i, int(np.argmax(cont[i] != alone[i])))
-        _say("configs[4]: lockstep, batcher and single-session tokens agree for 16 x 128 steps")
+            for name, other in (("lockstep", lock[i]), ("batcher", cont[i])):
+                k = _same_tokens_or_near_tie(other, alone[i], alone_logits[i])
+                if k is not None:
+                    ties.append((name, i, k))
+        del alone_logits
+        _say(f"configs[4]: lockstep, batcher and single-session tokens agree for 16 x 128 steps except at "
+             f"near-ties resolved to the runner-up: {ties}")
         t0 = time.time()
         osess = [om.session(ctx) for _ in range(n)]
         om.prefill_many(osess, [p[:-1] for p in prompts])

@@ -91,6 +91,12 @@ def test_matmul_m_rows_equals_gemv_rows(gpu, name):
 @pytest.mark.parametrize("m,N,K", [(4, 272, 512), (16, 2560, 2048), (37, 300, 768),
                                    (64, 1000, 2048), (100, 48, 5632), (16, 40, 160),
                                    (20, 8200, 256), (9, 300, 8192),
+                                   # one token tile: on tall K-quant matrices the row-split
+                                   # kernel with 1, 3 and 8 super-blocks per row (the LDS ring
+                                   # partly filled, full, wrapping) and a ragged last row
+                                   # group; the K-split kernel at 1 and 12 super-blocks
+                                   (6, 300, 256), (5, 8300, 256), (12, 8200, 768),
+                                   (13, 5000, 2048), (7, 4000, 3072), (8, 9000, 2048),
                                    # prefill-chunk tiles: 512 / 1100 tokens on few-row, long-K
                                    # and other matrices (every 5th row checked); from 1024 tokens
                                    # the XCD panel order (1100: one token group per panel;

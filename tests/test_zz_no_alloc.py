@@ -36,8 +36,10 @@ def test_noalloc_matmul_equals_matmul_on_consecutive_calls(gpu):
     lib = load()
     ref_f, na_f = _fn(lib, "smx_weight_matmul"), _fn(lib, "smx_weight_matmul_noalloc")
     # (type, n, k, m): the second call is smaller than the first (fewer rows, shorter k); then the
-    # GEMV path (m < 4) and a third matrix-core call
-    cases = [(O.Q4_K, 512, 4096, 64), (O.Q8_0, 96, 2048, 20), (O.Q6_K, 256, 1024, 2), (O.Q5_K, 64, 512, 33)]
+    # GEMV path (m < 4), a third matrix-core call, and two one-token-tile calls (the second smaller)
+    cases = [(O.Q4_K, 512, 4096, 64), (O.Q8_0, 96, 2048, 20), (O.Q6_K, 256, 1024, 2), (O.Q5_K, 64, 512, 33),
+             # one token tile on K-quant rows, the second call smaller
+             (O.Q5_K, 2048, 2048, 16), (O.Q4_K, 300, 1024, 8)]
     for i, (qt, n, k, m) in enumerate(cases):
         w = GpuWeightTensor(qt, n, k, quantized(qt, (n, k), seed=50 + i))
         x = torch.randn(m, k, device="cuda", generator=torch.Generator("cuda").manual_seed(i))
