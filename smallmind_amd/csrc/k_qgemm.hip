@@ -1033,12 +1033,13 @@ __device__ __forceinline__ void lds_dma16(const void *g, void *l)
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(la) : "memory");
 }
 
-// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt in bits 3:0 and
-// 15:14, expcnt 6:4, lgkmcnt 11:8)
-template <int N> __device__ __forceinline__ void wait_vm()
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 left
+// alone, lgkmcnt 11:8): the wave's vector-memory loads older than its last n have landed and
+// its own LDS reads have completed
+template <int N> __device__ __forceinline__ void wait_vm_lds()
 {
     static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
 template <int F, int NR, int NKH, int NS>
@@ -1130,11 +1131,13 @@ __global__ __launch_bounds__(64 * NR * NKH) void k_qgemm_rs(QgemmArgs a)
 
     // Publishes the slot of super-block i: this wave's loads of it have landed (the loads of
     // the n_after later super-blocks already issued may still be in flight), then every wave's.
+    // The wave's LDS reads of the previous super-block's slot have completed too, so the loads
+    // that go into that slot after the barrier cannot overtake them.
     auto sync = [&](int n_after) {
         asm volatile("" ::: "memory");
-        if (NS > 3 && n_after >= 2) wait_vm<(NS > 3 ? 2 * L : 0)>();
-        else if (NS > 2 && n_after >= 1) wait_vm<(NS > 2 ? L : 0)>();
-        else wait_vm<0>();
+        if (NS > 3 && n_after >= 2) wait_vm_lds<(NS > 3 ? 2 * L : 0)>();
+        else if (NS > 2 && n_after >= 1) wait_vm_lds<(NS > 2 ? L : 0)>();
+        else wait_vm_lds<0>();
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
