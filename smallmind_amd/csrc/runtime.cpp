@@ -618,7 +618,8 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
     // Up to 16 tokens, RMSNorm is folded into the GEMMs around it: the O and down projections
     // write the next norm's input as parts of gamma (.) x plus per-tile sums of x^2, and the
     // QKV (after layer 0) and gate/up GEMMs scale by 1 / rms -- no k_qprep launch per norm.
-    const bool fold = m->llama && M <= 16 && d % 256 == 0 && m->hidden % 256 == 0 && !m->dense_layers;
+    // (the GEMMs reduce up to 256 tile sums per token: d_model up to 4096)
+    const bool fold = m->llama && M <= 16 && d % 256 == 0 && d <= 4096 && m->hidden % 256 == 0 && !m->dense_layers;
     WView posw = m->pos.view();
     SMX_HIP(launch_embed_tokens(m->tok.view(), m->llama ? nullptr : &posw, B.ids, B.pos, B.x, d, M, s));
     for (int l = 0; l < c.n_layer; l++) {
