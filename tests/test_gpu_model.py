@@ -30,6 +30,10 @@ SMALL = {
     # unquantized F16 / F32 matrices (GgufModelLoader.ConvertF16Tensor / F32; the FP32 Linear)
     "llama-f16": (ModelConfig("llama", 1000, 160, 256, 2, 8, 2, 512), O.F16, O.F16, O.F32),
     "gpt2-f32": (ModelConfig("gpt2", 1000, 160, 256, 2, 4, 4, 1024), O.F32, O.F32, O.F16),
+    # d_model a multiple of 256 and d_ff 4096: token batches of up to 16 run the 16-token GEMMs
+    # with the RMSNorm folded into them, the 8192-row gate/up matrix on the row-split kernel
+    "llama-q4k-wide": (ModelConfig("llama", 1000, 256, 256, 2, 4, 2, 4096), O.Q4_K, O.Q6_K, O.Q6_K),
+    "smollm-q5k-wide": (ModelConfig("llama", 1000, 256, 256, 2, 4, 4, 4096), O.Q5_K, O.Q5_K, None),
 }
 
 
@@ -270,7 +274,8 @@ def test_prefill_across_chunks_matches_reference():
 
 
 @pytest.mark.parametrize("n_sess", [17, 12])
-@pytest.mark.parametrize("key", ["smollm-q5k", "llama-q4k", "gpt2-q8_0", "llama-f16", "gpt2-smq_q8"])
+@pytest.mark.parametrize("key", ["smollm-q5k", "llama-q4k", "gpt2-q8_0", "llama-f16", "gpt2-smq_q8",
+                                 "llama-q4k-wide", "smollm-q5k-wide"])
 def test_batch_generate_lockstep_matches_single_sessions_and_reference(pairs, key, n_sess):
     """several sessions stepping together (smx_batch_generate) produce, per
     session, the greedy tokens of the reference run alone; prompts of different lengths, so
@@ -316,7 +321,7 @@ def _ref_greedy(om, prompt, n_new):
     return out
 
 
-@pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0", "smollm-q5k"])
+@pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0", "smollm-q5k", "smollm-q5k-wide"])
 def test_continuous_batching_matches_reference_per_request(pairs, key):
     """Continuous batching (smx_batcher_*): 11 queued requests of different prompt lengths and
     token budgets, at most 4 decoding together; requests leave when done and queued ones join
