@@ -710,9 +710,16 @@ struct TileSched {
     uint32_t G, chunk;   // groups per panel (0: the 2-D grid), tiles per XCD
 };
 
-template <int F, int RT, int TT, int NW>
+// TS > 1 (one token tile only): the tile's 16 tokens are split over TS workgroups of 16 / TS
+// tokens each (grid y).  Each workgroup still multiplies whole 16 x 16 MFMA tiles, but it loads
+// the activation parts of its own tokens only (the other token lanes repeat them) and stores
+// only their outputs: the parts of the whole K, which every workgroup of a row tile reads, are
+// most of what a one-token-tile workgroup moves into its CU, and the split also spreads a
+// matrix of few row tiles over more CUs.  No partial sums cross workgroups.
+template <int F, int RT, int TT, int NW, int TS = 1>
 __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a, TileSched ts)
 {
+    static_assert(TS == 1 || (TT == 1 && (TS == 2 || TS == 4)), "token split of one token tile into 8 or 4");
     using Q = QW<F>;
     using G = Stage<F>;
     constexpr int R16 = 16 * RT;
@@ -745,8 +752,17 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a, TileSched ts)
         }
     }
     const uint32_t row_base = bx * R16;
-    const int tt0 = (int)by * TT;
+    // token split: this workgroup's tokens are tlo .. tlo + TW - 1 of the single token tile
+    constexpr int TW = 16 / TS;
+    const int tlo = TS > 1 ? (int)by * TW : 0;
+    const int tt0 = TS > 1 ? 0 : (int)by * TT;
     const int ntt = (M + 15) >> 4;
+    // lanes whose results are this workgroup's tokens (tokens 4g .. 4g + 3; TW is a multiple of
+    // 4).  A lane supplies token li's parts to the MFMA; lanes of the other tokens read those of
+    // token tlo + li % TW instead, so the loads touch only this workgroup's tokens' lines and
+    // need no mask or select (the duplicated tokens' results are not stored).
+    const bool tlive = TS == 1 || (uint32_t)(4 * g - tlo) < (uint32_t)TW;
+    const uint32_t xl16 = TS == 1 ? lane16 : (uint32_t)(16 * g + tlo + (li & (TW - 1))) * 16u;
     const uint32_t row_bytes = (uint32_t)nsup * G::kBytes;
     // contiguous super-block range of this wave
     const int per = (nsup + NW - 1) / NW;
@@ -788,7 +804,7 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a, TileSched ts)
     const bool preq = PRE && a.epi == EPI_QKV;
     float pres[4] = {0.0f, 0.0f, 0.0f, 0.0f}, pg = 0.0f;
     QkvPre qp[4] = {};
-    if (pre && wv == 0) {
+    if (pre && wv == 0 && tlive) {
         const uint32_t rc = min(row_base + (uint32_t)li, N - 1);
         if (preq) {
 #pragma unroll
@@ -882,7 +898,7 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a, TileSched ts)
                     const int tt = tt0 + t < ntt ? tt0 + t : ntt - 1;
 #pragma unroll
                     for (int p = 0; p < 3; p++)
-                        xa[u][t][p] = ld_part(xp, tt, nsb, s, p, lane16);
+                        xa[u][t][p] = ld_part(xp, tt, nsb, s, p, xl16);
                 }
             }
 #pragma unroll
@@ -933,7 +949,7 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a, TileSched ts)
         }
     }
 
-    if (preq && wv == 0) {
+    if (preq && wv == 0 && tlive) {
         const int d = a.d_model, kv = a.kv_dim, hd = a.head_dim, half = hd / 2;
         const int r = (int)min(row_base + (uint32_t)li, N - 1);
         const int pair = ((r < d ? r : r - d) % hd) / 2;
@@ -986,8 +1002,8 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a, TileSched ts)
             const uint32_t row = row_base + 16 * r + li;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float xn = qgemm_epilogue(a, v[i] * rs[i], row, (tt0 + t) * 16 + 4 * g + i, true, pre, pres[i], pg,
-                                                qp[i]);
+                const float xn = qgemm_epilogue(a, v[i] * rs[i], row, (tt0 + t) * 16 + 4 * g + i, tlive, pre, pres[i],
+                                                pg, qp[i]);
                 sq[t][i] = xn * xn;
             }
         }
@@ -996,7 +1012,7 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a, TileSched ts)
             for (int i = 0; i < 4; i++) {
                 const float t = row16_sum(sq[0][i]);
                 const int tok = tt0 * 16 + 4 * g + i;
-                if (li == 0 && tok < M) a.nss[(int64_t)(row_base / 16 + r) * M + tok] = t;
+                if (li == 0 && tok < M && tlive) a.nss[(int64_t)(row_base / 16 + r) * M + tok] = t;
             }
         }
     }
@@ -1458,11 +1474,14 @@ hipError_t launch_frt(const QgemmArgs &a, hipStream_t s)
     return hipGetLastError();
 }
 
-template <int F, int RT, int TT, int NW>
+template <int F, int RT, int TT, int NW, int TS = 1>
 hipError_t launch_st(const QgemmArgs &a, hipStream_t s)
 {
     const uint32_t R = (uint32_t)((a.w.rows + 16 * RT - 1) / (16 * RT));
-    const uint32_t T = (uint32_t)(((a.M + 15) / 16 + TT - 1) / TT);
+    // with a token split, one workgroup per 16 / TS tokens of the (single) token tile
+    const uint32_t T = TS > 1 ? (uint32_t)((a.M + 16 / TS - 1) / (16 / TS))
+                              : (uint32_t)(((a.M + 15) / 16 + TT - 1) / TT);
+    if (TS > 1 && a.M > 16) return hipErrorInvalidValue;
     TileSched ts{R, T, 0, 0};
     dim3 grid(R, T);
     // From 1024 tokens: panels of G token groups whose activation parts (TT tiles x K/32
@@ -1475,7 +1494,7 @@ hipError_t launch_st(const QgemmArgs &a, hipStream_t s)
         ts.chunk = (R * T + 7) / 8;
         grid = dim3(8 * ts.chunk, 1);
     }
-    hipLaunchKernelGGL((k_qgemm_st<F, RT, TT, NW>), grid, dim3(64 * NW), 0, s, a, ts);
+    hipLaunchKernelGGL((k_qgemm_st<F, RT, TT, NW, TS>), grid, dim3(64 * NW), 0, s, a, ts);
     return hipGetLastError();
 }
 
@@ -1521,7 +1540,7 @@ hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
         if constexpr (F == FMT_Q4_K || F == FMT_Q5_K)
             if (tall && a.w.rows <= 256 * 64) return launch_rs<F, 4, 2, 3>(a, s);
         if constexpr (F != FMT_Q6_K)   // 16 waves of >= 2 super-blocks (Q6_K would spill at 128 registers)
-            if (a.w.cols >= 8192) return launch_st<F, 1, 1, 16>(a, s);
+            if (a.w.cols >= 8192) return a.M > 8 ? launch_st<F, 1, 1, 16, 2>(a, s) : launch_st<F, 1, 1, 16>(a, s);
         return tall ? launch_st<F, 2, 1, 4>(a, s) : launch_st<F, 1, 1, 8>(a, s);
     }
     // Up to 16 tokens: one token tile, 16 waves per workgroup splitting K, 4 sub-blocks per

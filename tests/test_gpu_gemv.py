@@ -97,6 +97,9 @@ def test_matmul_m_rows_equals_gemv_rows(gpu, name):
                                    # group; the K-split kernel at 1 and 12 super-blocks
                                    (6, 300, 256), (5, 8300, 256), (12, 8200, 768),
                                    (13, 5000, 2048), (7, 4000, 3072), (8, 9000, 2048),
+                                   # K >= 8192 above 8 tokens: the tile's tokens split over two
+                                   # workgroups (the second with 1, 3 and 8 tokens)
+                                   (16, 2100, 8192), (11, 1000, 11008),
                                    # prefill-chunk tiles: 512 / 1100 tokens on few-row, long-K
                                    # and other matrices (every 5th row checked); from 1024 tokens
                                    # the XCD panel order (1100: one token group per panel;
