@@ -456,7 +456,6 @@ hipError_t launch_pe(const GemvArgs &a, int m, hipStream_t s)
             case GS_R2S1: return launch_v<2, 1, 1, PRO, EC, 3>(a, m, s);
             case GS_R2S2: return launch_v<2, 2, 1, PRO, EC, 3>(a, m, s);
             case GS_R4S2: return launch_v<4, 2, 1, PRO, EC, 3>(a, m, s);
-            case GS_R2S1C3: return launch_v<2, 1, 3, PRO, EC, 3>(a, m, s);
             case GS_R4S4: return launch_v<4, 4, 1, PRO, EC, 3>(a, m, s);
             default: return launch_v<2, 4, 1, PRO, EC, 3>(a, m, s);
             }
@@ -485,7 +484,6 @@ hipError_t launch_pe(const GemvArgs &a, int m, hipStream_t s)
     case GS_R2S1: return launch_v<2, 1, 1, PRO, EC, 1>(a, m, s);
     case GS_R2S2: return launch_v<2, 2, 1, PRO, EC, 1>(a, m, s);
     case GS_R4S2: return launch_v<4, 2, 1, PRO, EC, 1>(a, m, s);
-    case GS_R2S1C3: return launch_v<2, 1, 3, PRO, EC, 1>(a, m, s);
     case GS_R4S4: return launch_v<4, 4, 1, PRO, EC, 1>(a, m, s);
     default: return launch_v<2, 4, 1, PRO, EC, 1>(a, m, s);   // GS_R2S4: nch <= 256
     }

@@ -153,7 +153,6 @@ hipError_t launch_gemv(const GemvArgs &a, int m, hipStream_t s);
 // whole row for the staged launches.
 enum GemvShape {
     GS_R4S1, GS_R2S1, GS_R2S2, GS_R4S2, GS_R2S4,   // C = 1
-    GS_R2S1C3,                                     // K <= 6144: whole rows per wave
     GS_R4S4,                                       // K <= 8192
     GS_R4S2C3, GS_R4S2C4,                          // K <= 12288 / 16384 (plain GEMVs)
     GS_WIDE                                        // R=2, S=4, C=2 (plain GEMVs, few rows)
@@ -161,15 +160,17 @@ enum GemvShape {
 // Every workgroup stages the whole activation vector (K floats), so the longer the rows, the
 // more rows one staged copy should serve; short matrices keep more, smaller workgroups in
 // flight.  Measured on MI355X (graph-timed, weights from HBM): 2048 x 5632 Q8_0 5.20 us with two
-// rows per workgroup (R2S4), 4.75 us with eight (R2S1C3); 2048 x 8192 Q5_K 6.05 us (R2S4), 5.53
-// (R4S4), 6.50 (R2S1C4); 4096 x 11008 Q4_0 12.1 us (R2S4C2), 9.2 us (R4S2C3).
+// rows per workgroup (R2S4), 4.75 us with eight (2 rows x 3 chunks per wave, one wave per row
+// group); 2048 x 8192 Q5_K 6.05 us (R2S4), 5.53 (R4S4), 6.50 (R2S1C4); 4096 x 11008 Q4_0 12.1 us
+// (R2S4C2), 9.2 us (R4S2C3).  In the decode step the 2048 x 5632 down projection runs faster as
+// R4S4 (4 rows per workgroup, 512 workgroups) than with 8 rows per workgroup (256 workgroups,
+// one wave per SIMD): configs[2] decode 1880 -> 1908 tok/s.
 inline GemvShape gemv_shape(int64_t rows, int64_t cols)
 {
     const int64_t nch = cols / 32;
     if (nch <= 64) return rows >= 8192 ? GS_R4S1 : GS_R2S1;
     if (nch <= 128) return rows >= 4096 ? GS_R4S2 : GS_R2S2;
     if (rows < 1024) return nch <= 256 ? GS_R2S4 : GS_WIDE;
-    if (nch <= 192) return GS_R2S1C3;
     if (nch <= 256) return GS_R4S4;
     if (nch <= 384) return GS_R4S2C3;
     return nch <= 512 ? GS_R4S2C4 : GS_WIDE;
