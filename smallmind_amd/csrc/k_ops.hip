@@ -91,11 +91,14 @@ __global__ __launch_bounds__(kThreads) void k_softmax(float *__restrict__ scores
 }
 
 // Attention of one (token, head) by a whole workgroup (attention_head), as used by the token
-// batches below: 512 threads; for head_dim 64 the score pass (one position per thread) and the
-// P.V pass (16 positions per thread) each cover 512 positions per round of loads.
+// batches below: 256 threads; for head_dim 64 the score pass (one position per thread) covers
+// 256 positions and the P.V pass (32 positions per thread) 512 per round of loads.  Measured
+// on configs[4] (16 sessions x 32 heads, ~320 positions): 1.561 -> 1.545 ms per lockstep step
+// against 512 threads x 16 positions (171 VGPRs, two waves per SIMD, no spills); 256 x 16 and
+// 128 x 16 fell in between.
 template <int HD> struct AttnCfg {
-    static constexpr int NT = 512;
-    static constexpr int U = HD <= 64 ? 16 : 8;
+    static constexpr int NT = 256;
+    static constexpr int U = HD <= 64 ? 32 : 8;
 };
 
 // Decode attention split over the whole chip in two launches (one workgroup per head would
