@@ -16,11 +16,17 @@ OUT = os.path.join(HERE, "libsmx.so")
 BUILD = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
+# The matrix-core kernels keep MFMA results in ordinary VGPRs (gfx950 allows either register
+# file): in the accumulation-register form every sub-block's results were copied out with one
+# v_accvgpr_read per value, 20-30 % of the GEMM loop's VALU-slot instructions (configs[2]
+# prefill 62.6-63.1K -> 66.1-66.4K tok/s, configs[4] +2.2 %; same results).
+MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+
 # (source, object name, extra flags); the GEMV is built once per block format so its
 # instantiations compile in parallel.
 SOURCES = [("k_quant.hip", "k_quant", []), ("k_ops.hip", "k_ops", []), ("runtime.cpp", "runtime", []),
-           ("gemv_dispatch.cpp", "gemv_dispatch", []), ("k_qgemm.hip", "k_qgemm", []),
-           ("k_attn_prefill.hip", "k_attn_prefill", []), ("gguf.cpp", "gguf", []), ("smq.cpp", "smq", []), ("k_sample.hip", "k_sample", [])] + [
+           ("gemv_dispatch.cpp", "gemv_dispatch", []), ("k_qgemm.hip", "k_qgemm", MFMA_VGPR),
+           ("k_attn_prefill.hip", "k_attn_prefill", MFMA_VGPR), ("gguf.cpp", "gguf", []), ("smq.cpp", "smq", []), ("k_sample.hip", "k_sample", [])] + [
            ("k_gemv.hip", f"k_gemv_f{f}", [f"-DSMX_GEMV_FMT={f}"]) for f in range(9)]
 
 FLAGS = [
