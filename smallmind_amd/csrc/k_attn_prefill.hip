@@ -65,17 +65,32 @@ __device__ __forceinline__ float rows_sum(float v)
     return p.x + p.y;
 }
 
+// With pb.blk set (several sessions' runs of a batch in one launch), workgroup b's rows, cache
+// and first position come from the block table instead of the arguments: q, out and tok_off
+// move to the block's first batch row, and the block is a run of M <= TT tokens at t0 = 0.
 __global__ __launch_bounds__(kWaves * 64) void k_attn_prefill(
     const float *__restrict__ q, int q_stride, const float *__restrict__ kc, const float *__restrict__ vc,
     float *__restrict__ out, int out_stride, int n_head, int n_kv_head, int ctx_stride, int p_first, int M,
-    uint8_t *__restrict__ out_parts, int tok_off)
+    uint8_t *__restrict__ out_parts, int tok_off, PrefillBlocks pb)
 {
     extern __shared__ float s_out[];          // [kWaves][kRows][kPitch]
     __shared__ float s_max[kWaves][kRows], s_sum[kWaves][kRows], s_inv[kRows];
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int li = lane & 15, g = lane >> 4;
     const int G = n_head / n_kv_head, TT = kRows / G;
-    const int kvh = blockIdx.y, t0 = blockIdx.x * TT;
+    const int kvh = blockIdx.y;
+    int t0 = blockIdx.x * TT;
+    if (pb.blk) {   // uniform over the workgroup
+        const int r0 = pb.blk[2 * blockIdx.x];
+        M = pb.blk[2 * blockIdx.x + 1];
+        t0 = 0;
+        kc = pb.kc_tok[r0] + pb.layer_off;
+        vc = pb.vc_tok[r0] + pb.layer_off;
+        p_first = pb.pos[r0];
+        q += (int64_t)r0 * q_stride;
+        out += (int64_t)r0 * out_stride;
+        tok_off += r0;
+    }
     const float scale = 1.0f / sqrtf((float)kHD);   // MultiHeadAttention.cs:682
 
     // this lane's query in row block rb: row 16 rb + li
@@ -274,7 +289,26 @@ hipError_t launch_attention_prefill(const float *q, int q_stride, const float *k
     const int TT = kRows / (n_head / n_kv_head);
     const dim3 grid((unsigned)((M + TT - 1) / TT), (unsigned)n_kv_head);
     hipLaunchKernelGGL(k_attn_prefill, grid, dim3(kWaves * 64), lds, s, q, q_stride, kc, vc, out, out_stride,
-                       n_head, n_kv_head, ctx_stride, p_first, M, out_parts, tok_off);
+                       n_head, n_kv_head, ctx_stride, p_first, M, out_parts, tok_off, PrefillBlocks{});
+    return hipGetLastError();
+}
+
+int attention_prefill_block_rows(int n_head, int n_kv_head) { return kRows / (n_head / n_kv_head); }
+
+hipError_t launch_attention_prefill_blocks(const float *q, int q_stride, float *out, int out_stride, int n_head,
+                                           int n_kv_head, int hd, int ctx_stride, int n_blocks,
+                                           const PrefillBlocks &pb, hipStream_t s, uint8_t *out_parts)
+{
+    if (!attention_prefill_supported(n_head, n_kv_head, hd) || n_blocks <= 0 || !pb.blk || !pb.kc_tok ||
+        !pb.vc_tok || !pb.pos || ((n_head * hd) & 31) || (q_stride & 3) || (out_stride & 3))
+        return hipErrorInvalidValue;
+    const size_t lds = (size_t)kWaves * kRows * kPitch * 4;
+    const hipError_t e = hipFuncSetAttribute((const void *)k_attn_prefill,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    const dim3 grid((unsigned)n_blocks, (unsigned)n_kv_head);
+    hipLaunchKernelGGL(k_attn_prefill, grid, dim3(kWaves * 64), lds, s, q, q_stride, nullptr, nullptr, out,
+                       out_stride, n_head, n_kv_head, ctx_stride, 0, 0, out_parts, 0, pb);
     return hipGetLastError();
 }
 

@@ -264,6 +264,7 @@ struct TokBatch {
     int32_t *ids = nullptr, *pos = nullptr;
     float **kc = nullptr, **vc = nullptr;
     int32_t **tok_arr = nullptr;
+    int32_t *blk = nullptr;   // prefill attention blocks of several sessions' runs: (row, rows) pairs
 };
 
 struct smx_session {
@@ -553,7 +554,7 @@ void batch_free(TokBatch &B)
 {
     free_dev(B.x); free_dev(B.q); free_dev(B.att); free_dev(B.h); free_dev(B.logits);
     free_dev(B.xp); free_dev(B.xp2); free_dev(B.ss); free_dev(B.ids); free_dev(B.pos); free_dev(B.kc); free_dev(B.vc);
-    free_dev(B.tok_arr);
+    free_dev(B.tok_arr); free_dev(B.blk);
     B = TokBatch{};
 }
 
@@ -576,6 +577,7 @@ int batch_alloc(const smx_model *m, TokBatch &B, int cap, int logits_rows)
     A((void **)&B.kc, (size_t)cap * sizeof(float *));
     A((void **)&B.vc, (size_t)cap * sizeof(float *));
     A((void **)&B.tok_arr, (size_t)cap * sizeof(int32_t *));
+    A((void **)&B.blk, (size_t)cap * 2 * 4);   // every block holds at least one row
     if (e != hipSuccess) {
         batch_free(B);
         SMX_HIP(e);
@@ -597,8 +599,10 @@ struct PrefillRun {
 // Runs tokens 0..M-1 of B (ids, pos, kc, vc filled on the device) through every layer on the
 // matrix-core GEMM path, writing K/V into each token's cache; the final norm + head run on rows
 // head_from..M-1 into B.logits.  Same graph as enqueue_step, per token.
+// With n_blk > 0, B.blk holds the runs split into attention blocks (attention_prefill_blocks),
+// and the prefill attention of all runs is one launch per layer.
 int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_from, hipStream_t s,
-               const PrefillRun *run, int n_run = 1)
+               const PrefillRun *run, int n_run = 1, int n_blk = 0)
 {
     const smx_model_config &c = m->cfg;
     const int d = c.d_model, hd = m->hd, Hkv = c.n_kv_head;
@@ -606,6 +610,8 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
     // host-side bounds of the batch buffers: M rows fit the buffers, the head rows fit the logits
     // buffer, and every prefill run lies inside the M rows
     if (M <= 0 || M > B.cap) SMX_FAIL(SMX_EINVAL, "run_tokens: %d rows for a batch of %d", M, B.cap);
+    if (n_blk < 0 || n_blk > M || (n_blk > 0 && !run))
+        SMX_FAIL(SMX_EINVAL, "run_tokens: %d attention blocks for %d rows", n_blk, M);
     if (head_from < M && (head_from < 0 || M - head_from > B.logits_rows))
         SMX_FAIL(SMX_EINVAL, "run_tokens: head rows %d..%d for %d logits rows", head_from, M - 1, B.logits_rows);
     for (int i = 0; run && i < n_run; i++) {
@@ -654,7 +660,11 @@ int run_tokens(const smx_model *m, TokBatch &B, int M, int ctx_stride, int head_
             SMX_HIP(launch_qgemm(a, B.x, d, pro, L.d_attn_g, L.d_attn_b, c.norm_eps, s));
         }
         // attention writes the O projection's activation parts directly (no k_qprep launch)
-        if (run && attention_prefill_supported(c.n_head, Hkv, hd)) {
+        if (run && n_blk > 0 && attention_prefill_supported(c.n_head, Hkv, hd)) {
+            const PrefillBlocks pb{B.blk, B.kc, B.vc, B.pos, layer_off};
+            SMX_HIP(launch_attention_prefill_blocks(B.q, m->nqkv, B.att, d, c.n_head, Hkv, hd, ctx_stride, n_blk, pb,
+                                                    s, B.xp2));
+        } else if (run && attention_prefill_supported(c.n_head, Hkv, hd)) {
             for (int i = 0; i < n_run; i++) {
                 const PrefillRun &r = run[i];
                 const int cnt = r.count < 0 ? M : r.count;
@@ -816,15 +826,31 @@ int prefill_sessions(smx_model *m, TokBatch &P, smx_session *const *sessions, in
     std::vector<float *> kc((size_t)cap), vc((size_t)cap);
     std::vector<int32_t *> ta((size_t)cap);
     std::vector<PrefillRun> runs;
+    // the runs of a chunk split into prefill-attention blocks (batch row, rows): one attention
+    // launch per layer for all sessions of the chunk instead of one per run
+    const smx_model_config &c = m->cfg;
+    const bool blocks = attention_prefill_supported(c.n_head, c.n_kv_head, m->hd);
+    const int TB = blocks ? attention_prefill_block_rows(c.n_head, c.n_kv_head) : 1;
+    std::vector<int32_t> blk((size_t)cap * 2);
     int M = 0;
     auto flush = [&]() -> int {
         if (M == 0) return SMX_OK;
+        int nb = 0;
+        if (blocks && runs.size() > 1) {
+            for (const PrefillRun &r : runs)
+                for (int t = 0; t < r.count; t += TB) {
+                    blk[(size_t)(2 * nb)] = r.row0 + t;
+                    blk[(size_t)(2 * nb + 1)] = std::min(TB, r.count - t);
+                    nb++;
+                }
+            SMX_HIP(hipMemcpyAsync(P.blk, blk.data(), (size_t)nb * 8, hipMemcpyHostToDevice, s));
+        }
         SMX_HIP(hipMemcpyAsync(P.ids, ids.data(), (size_t)M * 4, hipMemcpyHostToDevice, s));
         SMX_HIP(hipMemcpyAsync(P.pos, pos.data(), (size_t)M * 4, hipMemcpyHostToDevice, s));
         SMX_HIP(hipMemcpyAsync(P.kc, kc.data(), (size_t)M * sizeof(float *), hipMemcpyHostToDevice, s));
         SMX_HIP(hipMemcpyAsync(P.vc, vc.data(), (size_t)M * sizeof(float *), hipMemcpyHostToDevice, s));
         SMX_HIP(hipMemcpyAsync(P.tok_arr, ta.data(), (size_t)M * sizeof(int32_t *), hipMemcpyHostToDevice, s));
-        const int rc = run_tokens(m, P, M, ctx_stride, M, s, runs.data(), (int)runs.size());
+        const int rc = run_tokens(m, P, M, ctx_stride, M, s, runs.data(), (int)runs.size(), nb);
         if (rc != SMX_OK) return rc;
         // the host arrays are reused by the next chunk: let this chunk's copies finish
         SMX_HIP(hipStreamSynchronize(s));

@@ -303,6 +303,20 @@ hipError_t launch_attention_prefill(const float *q, int q_stride, const float *k
                                     int out_stride, int n_head, int n_kv_head, int hd, int ctx_stride,
                                     int p_first, int M, hipStream_t s, uint8_t *out_parts = nullptr,
                                     int tok_off = 0);
+// Several sessions' runs of a token batch in one launch: workgroup b takes the rows
+// blk[2b] .. blk[2b] + blk[2b+1] - 1 of the batch (at most attention_prefill_block_rows rows, all
+// of one run), with that session's cache (kc_tok / vc_tok of its first row, plus layer_off) and
+// the first row's position; q, out and the parts are addressed by batch row.
+struct PrefillBlocks {
+    const int32_t *blk;
+    float *const *kc_tok, *const *vc_tok;
+    const int32_t *pos;
+    int64_t layer_off;
+};
+int attention_prefill_block_rows(int n_head, int n_kv_head);
+hipError_t launch_attention_prefill_blocks(const float *q, int q_stride, float *out, int out_stride, int n_head,
+                                           int n_kv_head, int hd, int ctx_stride, int n_blocks,
+                                           const PrefillBlocks &pb, hipStream_t s, uint8_t *out_parts = nullptr);
 hipError_t launch_attention_tokens(const float *q, int64_t q_stride, float *const *kc_tok,
                                    float *const *vc_tok, int64_t layer_off, float *out,
                                    int64_t out_stride, int n_head, int n_kv_head, int hd,
