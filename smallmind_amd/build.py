@@ -41,8 +41,8 @@ FLAGS = [
 
 # The fused GEMV keeps a row group's weight chunks in registers; an instance that spilled them
 # to scratch memory once returned wrong sums (F32, 4 rows x 4 chunks; cause not established), so
-# the build refuses any GEMV instance with scratch memory.
-SPILL_CHECKED = ("k_gemv.hip",)
+# the build refuses any GEMV or matrix-core GEMM instance with scratch memory.
+SPILL_CHECKED = ("k_gemv.hip", "k_qgemm.hip", "k_attn_prefill.hip")
 
 
 def _spilling_kernels(remarks: str) -> list:
@@ -70,7 +70,7 @@ def _compile(entry) -> str:
         bad = _spilling_kernels(r.stderr)
         if bad:
             os.remove(obj)
-            raise RuntimeError(f"{src} ({' '.join(extra)}): GEMV instances use scratch memory: {bad}")
+            raise RuntimeError(f"{src} ({' '.join(extra)}): kernel instances use scratch memory: {bad}")
     return obj
 
 

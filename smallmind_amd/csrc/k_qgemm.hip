@@ -885,8 +885,10 @@ __global__ __launch_bounds__(64 * NW) void k_qgemm_st(QgemmArgs a, TileSched ts)
     for (int sup = sup0; sup < sup1; sup++) {
         stage();                               // this wave's LDS region only: in-order LDS ops
         if (sup + 1 < sup1) issue(sup + 1);    // next super-block in flight
-        // XU sub-blocks of activation parts in flight at once (fewer with more token tiles)
-        constexpr int XU = TT == 1 ? 4 : 1;
+        // XU sub-blocks of activation parts in flight at once (fewer with more token tiles, and
+        // two for the 16-wave SMQ Q8 tile, whose two staged scale words per sub-block would
+        // otherwise push it past the 128 registers of a 1024-thread workgroup)
+        constexpr int XU = TT == 1 ? (F == FMT_SQ8 && NW == 16 ? 2 : 4) : 1;
 #pragma unroll
         for (int h = 0; h < 8 / XU; h++) {
             uint4 xa[XU][TT][3];
@@ -1531,7 +1533,9 @@ hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
                 return launch_st<F, 2, 2, 4>(a, s);
             }
             if constexpr (F == FMT_Q6_K) return narrow ? launch_st<F, 2, 4, 8>(a, s) : launch_st<F, 1, 4, 8>(a, s);
-            if (narrow && a.M < 1024) return launch_st<F, 2, 4, 8>(a, s);
+            // (SMQ Q8's two staged scale words per sub-block do not fit 8 waves' registers)
+            if constexpr (F != FMT_SQ8)
+                if (narrow && a.M < 1024) return launch_st<F, 2, 4, 8>(a, s);
             return launch_st<F, 2, 4, 4>(a, s);
         }
         // tall K-quant matrices up to one workgroup of 64 rows per CU: the row-split kernel
@@ -1539,16 +1543,22 @@ hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
         // kernel's several workgroups per CU)
         if constexpr (F == FMT_Q4_K || F == FMT_Q5_K)
             if (tall && a.w.rows <= 256 * 64) return launch_rs<F, 4, 2, 3>(a, s);
-        if constexpr (F != FMT_Q6_K)   // 16 waves of >= 2 super-blocks (Q6_K would spill at 128 registers)
+        // 16 waves of >= 2 super-blocks (Q6_K and Q4_0 would spill at 128 registers)
+        if constexpr (F != FMT_Q6_K && F != FMT_Q4_0)
             if (a.w.cols >= 8192) return a.M > 8 ? launch_st<F, 1, 1, 16, 2>(a, s) : launch_st<F, 1, 1, 16>(a, s);
         return tall ? launch_st<F, 2, 1, 4>(a, s) : launch_st<F, 1, 1, 8>(a, s);
     }
-    // Up to 16 tokens: one token tile, 16 waves per workgroup splitting K, 4 sub-blocks per
-    // wave in flight.  More tokens: 4 token tiles per workgroup (the weight codes are reused
-    // across 64 tokens), 4 waves, 2 sub-blocks in flight.
-    if (a.M > 16) return launch_frt<F, 1, 4, 4, 2>(a, s);
-    if (a.w.rows >= 16 * 2 * 512) return launch_frt<F, 2, 1, 16, 4>(a, s);
-    return launch_frt<F, 1, 1, 16, 4>(a, s);
+    // Rows of 32-element blocks only (K-quant rows are whole super-blocks).  Up to 16 tokens:
+    // one token tile, 16 waves per workgroup splitting K, 4 sub-blocks per wave in flight.  More
+    // tokens: 4 token tiles per workgroup (the weight codes are reused across 64 tokens), 4
+    // waves, 2 sub-blocks in flight.
+    if constexpr (F == FMT_Q4_K || F == FMT_Q5_K || F == FMT_Q6_K) {
+        return hipErrorInvalidValue;
+    } else {
+        if (a.M > 16) return launch_frt<F, 1, 4, 4, 2>(a, s);
+        if (a.w.rows >= 16 * 2 * 512) return launch_frt<F, 2, 1, 16, 4>(a, s);
+        return launch_frt<F, 1, 1, 16, 4>(a, s);
+    }
 }
 
 template <int F, int RT, int TT, int NW, int SB>

@@ -128,4 +128,5 @@ def test_build_refuses_gemv_instances_with_scratch_memory():
         "k_gemv.hip:206:1: remark:     ScratchSize [bytes/lane]: 436 [-Rpass-analysis=kernel-resource-usage]",
     ])
     assert b._spilling_kernels(remarks) == ["_ZN3smx6k_gemvILi2E"]
-    assert "k_gemv.hip" in b.SPILL_CHECKED
+    # the GEMV and the matrix-core kernels (GEMM tiles, prefill attention) are all checked
+    assert {"k_gemv.hip", "k_qgemm.hip", "k_attn_prefill.hip"} <= set(b.SPILL_CHECKED)
