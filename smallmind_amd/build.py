@@ -41,8 +41,8 @@ FLAGS = [
 
 # The fused GEMV keeps a row group's weight chunks in registers; an instance that spilled them
 # to scratch memory once returned wrong sums (F32, 4 rows x 4 chunks; cause not established), so
-# the build refuses any GEMV or matrix-core GEMM instance with scratch memory.
-SPILL_CHECKED = ("k_gemv.hip", "k_qgemm.hip", "k_attn_prefill.hip")
+# the build refuses any kernel instance with scratch memory, in every HIP source.
+SPILL_CHECKED = tuple(sorted({src for src, _, _ in SOURCES if src.endswith(".hip")}))
 
 
 def _spilling_kernels(remarks: str) -> list:
