@@ -1539,10 +1539,14 @@ hipError_t launch_f(const QgemmArgs &a, hipStream_t s)
             return launch_st<F, 2, 4, 4>(a, s);
         }
         // tall K-quant matrices up to one workgroup of 64 rows per CU: the row-split kernel
-        // (configs[4] gate/up 16.9 -> 13.6 us; the 49152-row head stays faster on the K-split
-        // kernel's several workgroups per CU)
-        if constexpr (F == FMT_Q4_K || F == FMT_Q5_K)
+        // (configs[4] gate/up 16.9 -> 13.6 us); up to 192 rows per CU, 12 row tiles of 16 rows
+        // per workgroup, each wave all of K, a two-slot ring (117 KB of LDS: one workgroup per
+        // CU in a single round; the 64-row form took three rounds on the 49152-row head, which
+        // the K-split kernel's several workgroups per CU beat): configs[4] step 1.536 -> 1.528 ms
+        if constexpr (F == FMT_Q4_K || F == FMT_Q5_K) {
             if (tall && a.w.rows <= 256 * 64) return launch_rs<F, 4, 2, 3>(a, s);
+            if (tall && a.w.rows <= 256 * 192) return launch_rs<F, 12, 1, 2>(a, s);
+        }
         // 16 waves of >= 2 super-blocks (Q6_K and Q4_0 would spill at 128 registers)
         if constexpr (F != FMT_Q6_K && F != FMT_Q4_0)
             if (a.w.cols >= 8192) return a.M > 8 ? launch_st<F, 1, 1, 16, 2>(a, s) : launch_st<F, 1, 1, 16>(a, s);

@@ -100,6 +100,9 @@ def test_matmul_m_rows_equals_gemv_rows(gpu, name):
                                    # K >= 8192 above 8 tokens: the tile's tokens split over two
                                    # workgroups (the second with 1, 3 and 8 tokens)
                                    (16, 2100, 8192), (11, 1000, 11008),
+                                   # one token tile on K-quant matrices of 16385-49152 rows:
+                                   # 192-row workgroups, the last one ragged
+                                   (16, 30000, 512), (7, 17000, 256),
                                    # prefill-chunk tiles: 512 / 1100 tokens on few-row, long-K
                                    # and other matrices (every 5th row checked); from 1024 tokens
                                    # the XCD panel order (1100: one token group per panel;
