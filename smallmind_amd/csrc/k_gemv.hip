@@ -201,10 +201,15 @@ __device__ __forceinline__ int xs_pos(int c, int i) { return 8 * c + (i ^ (c & 7
 // NT: the weights are read with the non-temporal hint (streamed); false for matrices the
 // runtime keeps resident in the MALL (WView::cache).  A template argument, not a branch on
 // the flag: with both load sequences in one kernel the plain one ran ~10 % slower.
-template <int F, int R, int S, int C, int PRO, int EC, int STG, bool NT>
+// HW = 2 (rows of at most 32 chunks, K <= 1024): each half of a wave takes its own R rows, lanes
+// 32h + l taking chunk l of rows row0 + R*h ..., so a wave covers 2R rows with every lane busy
+// instead of leaving the lanes past the row's chunks idle; the rows are reduced one half at a
+// time (the other half's partials zeroed).
+template <int F, int R, int S, int C, int PRO, int EC, int STG, bool NT, int HW = 1>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
 {
     static_assert(STG || PRO == PRO_NONE, "a fused norm needs the staged activation path");
+    static_assert(HW == 1 || (HW == 2 && S == 1 && C == 1 && STG), "half-wave rows: one chunk per lane");
     constexpr int G = 4 / S;    // row groups per workgroup
     constexpr int KPT = STG == 2 ? 16 : 8;   // staged float4 per thread: K <= 1024*KPT
     static_assert(STG < 2 || PRO == PRO_NONE, "the wide staging is for plain GEMVs");
@@ -216,12 +221,14 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
     const int lane = lane_id();
     const uint32_t N = (uint32_t)a.w.rows;
     const int K = (int)a.w.cols, nch = K >> 5, K4 = K >> 2;
-    const uint32_t row0 = (blockIdx.x * G + grp) * R;
+    const uint32_t row0 = (blockIdx.x * G + grp) * R * HW;
     const int my = blockIdx.y;
     const float *x = a.x + (int64_t)my * a.x_stride;
+    const int half = HW == 2 ? lane >> 5 : 0, cl = HW == 2 ? lane & 31 : lane;
+    const uint32_t rh = row0 + (uint32_t)(R * half);   // first row of this lane's half
     uint32_t rb[R];   // row * blocks-per-row (rows past the end re-read the last row)
 #pragma unroll
-    for (int r = 0; r < R; r++) rb[r] = (row0 + r < N ? row0 + r : N - 1) * (uint32_t)a.w.nb;
+    for (int r = 0; r < R; r++) rb[r] = (rh + r < N ? rh + r : N - 1) * (uint32_t)a.w.nb;
 
     // 1. activations (+ norm parameters): coalesced, issued first
     const int tid = STG ? opaque_tid() : 0;
@@ -254,7 +261,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
     Raw<F> wr[C][R];
 #pragma unroll
     for (int j = 0; j < C; j++) {
-        const int c = (ws + S * j) * 64 + lane;
+        const int c = (ws + S * j) * (64 / HW) + cl;
         on[j] = c < nch;
         cj[j] = on[j] ? c : nch - 1;
     }
@@ -263,9 +270,10 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
 #pragma unroll
         for (int r = 0; r < R; r++) wr[j][r].template load32<NT>(a.w, rb[r], cj[j]);
     __builtin_amdgcn_sched_barrier(0);
-    // 3. epilogue operands
-    EpiIn<R, EC> e;
-    epi_load<R, EC>(a, row0, N, my, e);
+    // 3. epilogue operands (of each half's rows)
+    EpiIn<R, EC> e[HW];
+#pragma unroll
+    for (int h = 0; h < HW; h++) epi_load<R, EC>(a, row0 + (uint32_t)(R * h), N, my, e[h]);
     __builtin_amdgcn_sched_barrier(0);
     // 4. norm statistic over the workgroup, normalise, stage in LDS
     if constexpr (STG) {
@@ -325,7 +333,10 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
         __syncthreads();
     }
 
-    if constexpr (EC == EC_QKV) epi_load_rope<R, EC>(a, row0, e);
+    if constexpr (EC == EC_QKV) {
+#pragma unroll
+        for (int h = 0; h < HW; h++) epi_load_rope<R, EC>(a, row0 + (uint32_t)(R * h), e[h]);
+    }
 
     float acc[R];
 #pragma unroll
@@ -374,32 +385,44 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
     }
 
     // 6. reduction across the wave (row r's total in lane block r), then across the S waves
-    // of the row group in a fixed order
+    // of the row group in a fixed order; with half-wave rows, one half at a time
     constexpr int LB = 64 / R;
-    float c = wave_totals_t<R>(acc);
-    if constexpr (S > 1) {
-        if (lane % LB == 0) s_red[w][lane / LB] = c;
-        __syncthreads();
-        float v = s_red[grp * S][lane / LB];
+    float t[HW][R];   // the row totals (argmax epilogue)
 #pragma unroll
-        for (int s = 1; s < S; s++) v += s_red[grp * S + s][lane / LB];
-        c = v;
+    for (int h = 0; h < HW; h++) {
+        float ah[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) ah[r] = HW == 1 || half == h ? acc[r] : 0.0f;
+        float c = wave_totals_t<R>(ah);
+        if constexpr (S > 1) {
+            if (lane % LB == 0) s_red[w][lane / LB] = c;
+            __syncthreads();
+            float v = s_red[grp * S][lane / LB];
+#pragma unroll
+            for (int s = 1; s < S; s++) v += s_red[grp * S + s][lane / LB];
+            c = v;
+        }
+        if (a.bias) c += spread<R>(e[h].bias);   // in the first lane of each block
+        const uint32_t r0 = row0 + (uint32_t)(R * h);
+        if (ws == 0 && r0 < N) epi_store<R, EC>(a, c, e[h], r0, N, my, lane);
+        if constexpr (EC == EC_ARGMAX) {
+#pragma unroll
+            for (int r = 0; r < R; r++) t[h][r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), r * LB));
+        }
     }
-    if (a.bias) c += spread<R>(e.bias);   // in the first lane of each block
-    if (ws == 0 && row0 < N) epi_store<R, EC>(a, c, e, row0, N, my, lane);
     if constexpr (EC == EC_ARGMAX) {
         __shared__ float s_bv[4];
         __shared__ int s_bi[4];
-        float t[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) t[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), r * LB));
         if (ws == 0 && lane == 0) {
             float bv = -INFINITY;
             int bi = 0x7FFFFFFF;
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                if (row0 + r < N && am_better(t[r], (int)(row0 + r), bv, bi)) { bv = t[r]; bi = (int)(row0 + r); }
-            }
+            for (int h = 0; h < HW; h++)
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const uint32_t row = row0 + (uint32_t)(R * h + r);
+                    if (row < N && am_better(t[h][r], (int)row, bv, bi)) { bv = t[h][r]; bi = (int)row; }
+                }
             s_bv[grp] = bv;
             s_bi[grp] = bi;
         }
@@ -416,17 +439,17 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
     }
 }
 
-template <int R, int S, int C, int PRO, int EC, int STG>
+template <int R, int S, int C, int PRO, int EC, int STG, int HW = 1>
 hipError_t launch_v(const GemvArgs &a, int m, hipStream_t s)
 {
     constexpr int F = SMX_GEMV_FMT;
-    // a staged launch runs one round of 64*S*C chunks: it must cover the row
-    if (STG && a.w.cols > (int64_t)64 * S * C * 32) return hipErrorInvalidValue;
-    const int64_t groups = (a.w.rows + R - 1) / R;
+    // a staged launch runs one round of 64*S*C/HW chunks: it must cover the row
+    if (STG && a.w.cols > (int64_t)64 / HW * S * C * 32) return hipErrorInvalidValue;
+    const int64_t groups = (a.w.rows + R * HW - 1) / (R * HW);
     const dim3 grid((unsigned)((groups + (4 / S) - 1) / (4 / S)), (unsigned)m);
     const size_t lds = STG ? (size_t)a.w.cols * 4 : 0;
-    if (a.w.cache) hipLaunchKernelGGL((k_gemv<F, R, S, C, PRO, EC, STG, false>), grid, dim3(256), lds, s, a);
-    else hipLaunchKernelGGL((k_gemv<F, R, S, C, PRO, EC, STG, true>), grid, dim3(256), lds, s, a);
+    if (a.w.cache) hipLaunchKernelGGL((k_gemv<F, R, S, C, PRO, EC, STG, false, HW>), grid, dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((k_gemv<F, R, S, C, PRO, EC, STG, true, HW>), grid, dim3(256), lds, s, a);
     if constexpr (EC == EC_ARGMAX) {
         // the per-workgroup partials are reduced by a one-workgroup kernel; the kernel boundary
         // makes them visible without a device-scope fence in each of the many workgroups
@@ -452,6 +475,7 @@ hipError_t launch_pe(const GemvArgs &a, int m, hipStream_t s)
         if (a.x_parts == 2) {
             if (K > 8192) return hipErrorInvalidValue;
             switch (gemv_shape(a.w.rows, K)) {
+            case GS_R4S1H2:
             case GS_R4S1: return launch_v<4, 1, 1, PRO, EC, 3>(a, m, s);
             case GS_R2S1: return launch_v<2, 1, 1, PRO, EC, 3>(a, m, s);
             case GS_R2S2: return launch_v<2, 2, 1, PRO, EC, 3>(a, m, s);
@@ -480,6 +504,7 @@ hipError_t launch_pe(const GemvArgs &a, int m, hipStream_t s)
             }
         }
         return hipErrorInvalidValue;
+    case GS_R4S1H2: return launch_v<4, 1, 1, PRO, EC, 1, 2>(a, m, s);
     case GS_R4S1: return launch_v<4, 1, 1, PRO, EC, 1>(a, m, s);
     case GS_R2S1: return launch_v<2, 1, 1, PRO, EC, 1>(a, m, s);
     case GS_R2S2: return launch_v<2, 2, 1, PRO, EC, 1>(a, m, s);

@@ -33,7 +33,10 @@ def _gemv(qt, blocks, N, K, x, m=1):
 
 
 SHAPES = [(2, 256), (48, 512), (2560, 2048), (2048, 5632), (1000, 768), (3, 3072), (1030, 8192), (1024, 11008),
-          (700, 8192), (1100, 6144), (1024, 16384)]
+          (700, 8192), (1100, 6144), (1024, 16384),
+          # tall matrices of rows up to 32 chunks: each half of a wave takes its own rows
+          # (a ragged last row group at 9001 rows, full half-waves at K = 1024)
+          (9001, 768), (8200, 256), (8192, 1024)]
 
 
 @pytest.mark.parametrize("name", list(TYPES))
