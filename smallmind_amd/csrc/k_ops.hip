@@ -422,8 +422,8 @@ __global__ __launch_bounds__(NT) void k_attn_dec(const float *__restrict__ q, co
     // every load is issued before the position is known, with indices clamped into the cache
     // row (valid memory); entries at or past n_pos are dropped by selection, never multiplied
     const int lastg = ctx_stride / 4 - 1;
-    auto kload = [&](float4 *kv, int pass) {
-        const uint32_t pc = 4u * (uint32_t)min(pg + NPG * pass, lastg);
+    auto kload = [&](float4 *kv, int pass, int lim) {
+        const uint32_t pc = 4u * (uint32_t)min(pg + NPG * pass, lim);
 #pragma unroll
         for (int e = 0; e < DQ; e++) kv[e] = *(const float4 *)(Kb + 4u * ((uint32_t)e * (uint32_t)ctx_stride + pc));
     };
@@ -443,7 +443,7 @@ __global__ __launch_bounds__(NT) void k_attn_dec(const float *__restrict__ q, co
     constexpr int PA = P <= 2 ? P : P - 1;   // passes loaded at entry (registers: 16 * DQ * PA)
     float4 kv[PA][DQ];
 #pragma unroll
-    for (int i = 0; i < PA; i++) kload(kv[i], i);
+    for (int i = 0; i < PA; i++) kload(kv[i], i, lastg);
     float4 vv[U];
 #pragma unroll
     for (int u = 0; u < U; u++)
@@ -452,8 +452,10 @@ __global__ __launch_bounds__(NT) void k_attn_dec(const float *__restrict__ q, co
     const int n_pos = pos_dev ? ld_uniform(pos_dev) + 1 : n_pos_fixed;
     kdot(kv[0], 0);
     if constexpr (PA < P) {
+        // the last pass is issued once the position is known: groups past it re-read the last
+        // written group instead of streaming cache entries not yet written
         __builtin_amdgcn_sched_barrier(0);
-        kload(kv[0], P - 1);
+        kload(kv[0], P - 1, min(lastg, (n_pos - 1) >> 2));
         __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
