@@ -17,8 +17,10 @@
 //
 // Work decomposition.  A workgroup owns 32 query rows of one KV head: 32 / G tokens x the G
 // query heads that share the KV head (GQA), so every K/V element it loads serves 32 rows.  Its
-// 8 waves split the keys in 16-key tiles (wave w: tiles w, w + 8, ...), each wave keeping its
-// next tile's loads in flight while it computes on the current one.  Partial maxima, sums and
+// 8 waves split the keys in 16-key tiles (wave w: tiles w, w + 8, ...).  A wave loads one tile
+// at a time: without a register copy of the next tile the kernel takes 115 VGPRs and two
+// workgroups fit a CU, whose other waves hide the loads (prefill +0.6-1.3 % against one
+// workgroup per CU with the next tile's loads in flight).  Partial maxima, sums and
 // outputs of the 8 waves are combined through LDS in a fixed order.
 //
 // Matrix cores: v_mfma_f32_16x16x4_f32 (fp32 products, fp32 accumulation).
@@ -143,11 +145,10 @@ __global__ __launch_bounds__(kWaves * 64) void k_attn_prefill(
     // ---- pass 1: row maxima -----------------------------------------------------------------
     float mx[2] = {-INFINITY, -INFINITY};
     {
-        float kv[16], kn[16];
+        float kv[16];
         int ti = w;
-        if (ti < n_tiles) load_k(ti, kv);
         for (; ti < n_tiles; ti += kWaves) {
-            if (ti + kWaves < n_tiles) load_k(ti + kWaves, kn);
+            load_k(ti, kv);
             float s[2][4];
             scores(kv, s);
 #pragma unroll
@@ -155,8 +156,6 @@ __global__ __launch_bounds__(kWaves * 64) void k_attn_prefill(
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     if (16 * ti + 4 * g + i < npos[rb]) mx[rb] = fmaxf(mx[rb], s[rb][i]);
-#pragma unroll
-            for (int j = 0; j < 16; j++) kv[j] = kn[j];
         }
     }
 #pragma unroll
@@ -181,17 +180,11 @@ __global__ __launch_bounds__(kWaves * 64) void k_attn_prefill(
 #pragma unroll
         for (int mb = 0; mb < 4; mb++) o[rb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     {
-        float kv[16], kn[16], vv[4][4], vn[4][4];
+        float kv[16], vv[4][4];
         int ti = w;
-        if (ti < n_tiles) {
+        for (; ti < n_tiles; ti += kWaves) {
             load_k(ti, kv);
             load_v(ti, vv);
-        }
-        for (; ti < n_tiles; ti += kWaves) {
-            if (ti + kWaves < n_tiles) {
-                load_k(ti + kWaves, kn);
-                load_v(ti + kWaves, vn);
-            }
             float s[2][4];
             scores(kv, s);
 #pragma unroll
@@ -214,12 +207,7 @@ __global__ __launch_bounds__(kWaves * 64) void k_attn_prefill(
                     o[1][mb] = mma(s[1][j], vz, o[1][mb]);
                 }
             }
-#pragma unroll
-            for (int j = 0; j < 16; j++) kv[j] = kn[j];
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int mb = 0; mb < 4; mb++) vv[j][mb] = vn[j][mb];
+
         }
     }
     // partial sums and outputs of this wave to LDS
