@@ -211,8 +211,14 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
     static_assert(STG || PRO == PRO_NONE, "a fused norm needs the staged activation path");
     static_assert(HW == 1 || (HW == 2 && S == 1 && C == 1 && STG), "half-wave rows: one chunk per lane");
     constexpr int G = 4 / S;    // row groups per workgroup
-    constexpr int KPT = STG == 2 ? 16 : 8;   // staged float4 per thread: K <= 1024*KPT
-    static_assert(STG < 2 || PRO == PRO_NONE, "the wide staging is for plain GEMVs");
+    // STG = 4 (K <= 1024, S = 1): every wave loads the whole activation vector, takes the norm
+    // statistic with wave reductions and stages its own copy in LDS, so the prologue has no
+    // workgroup barrier (the waves need nothing from each other)
+    constexpr bool WAVE = STG == 4;
+    static_assert(!WAVE || S == 1, "wave-private staging: each wave owns whole rows");
+    constexpr int TSTEP = WAVE ? 64 : 256;   // threads sharing the staging loads
+    constexpr int KPT = WAVE ? 4 : STG == 2 ? 16 : 8;   // staged float4 per thread: K <= 4*TSTEP*KPT
+    static_assert(STG != 2 || PRO == PRO_NONE, "the wide staging is for plain GEMVs");
     __shared__ float s_red[4][R];
     __shared__ float s_st[2][4];
     extern __shared__ float4 xs[];
@@ -221,6 +227,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
     const int lane = lane_id();
     const uint32_t N = (uint32_t)a.w.rows;
     const int K = (int)a.w.cols, nch = K >> 5, K4 = K >> 2;
+    float4 *const xsb = WAVE ? xs + w * K4 : xs;   // this wave's staged copy (STG 4)
     const uint32_t row0 = (blockIdx.x * G + grp) * R * HW;
     const int my = blockIdx.y;
     const float *x = a.x + (int64_t)my * a.x_stride;
@@ -231,7 +238,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
     for (int r = 0; r < R; r++) rb[r] = (rh + r < N ? rh + r : N - 1) * (uint32_t)a.w.nb;
 
     // 1. activations (+ norm parameters): coalesced, issued first
-    const int tid = STG ? opaque_tid() : 0;
+    const int tid = STG ? (WAVE ? (opaque_tid() & 63) : opaque_tid()) : 0;
     float4 xr[STG ? KPT : 1], gr[PRO != PRO_NONE ? KPT : 1], br[PRO == PRO_LN ? KPT : 1];
     constexpr bool TWO = STG == 3;   // x = x + x[x_part_stride] (two partial sums)
     static_assert(!TWO || PRO == PRO_NONE, "partial sums are added before any norm");
@@ -239,7 +246,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
     if constexpr (STG) {
 #pragma unroll
         for (int k = 0; k < KPT; k++) {
-            const int i4 = tid + 256 * k;
+            const int i4 = tid + TSTEP * k;
             if (i4 < K4) {
                 xr[k] = ((const float4 *)x)[i4];
                 if constexpr (PRO != PRO_NONE) gr[k] = ((const float4 *)a.gamma)[i4];
@@ -249,7 +256,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
         if constexpr (TWO) {
 #pragma unroll
             for (int k = 0; k < KPT; k++) {
-                const int i4 = tid + 256 * k;
+                const int i4 = tid + TSTEP * k;
                 if (i4 < K4) x2[k] = ((const float4 *)(x + a.x_part_stride))[i4];
             }
         }
@@ -282,37 +289,37 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
             float ss = 0.0f;
 #pragma unroll
             for (int k = 0; k < KPT; k++)
-                if (tid + 256 * k < K4) {
+                if (tid + TSTEP * k < K4) {
                     float q;
                     q = xr[k].x * xr[k].x; ss += q;
                     q = xr[k].y * xr[k].y; ss += q;
                     q = xr[k].z * xr[k].z; ss += q;
                     q = xr[k].w * xr[k].w; ss += q;
                 }
-            ss = wg_sum(ss, s_st[0], w);
+            ss = WAVE ? wave_sum_uniform(ss) : wg_sum(ss, s_st[0], w);
             sc = 1.0f / sqrtf(ss / (float)K + a.eps);   // RMSNormOps.cs:114
         } else if constexpr (PRO == PRO_LN) {
             float t = 0.0f;
 #pragma unroll
             for (int k = 0; k < KPT; k++)
-                if (tid + 256 * k < K4) { t += xr[k].x; t += xr[k].y; t += xr[k].z; t += xr[k].w; }
-            mean = wg_sum(t, s_st[0], w) / (float)K;     // LayerNormOps.cs:92-101
+                if (tid + TSTEP * k < K4) { t += xr[k].x; t += xr[k].y; t += xr[k].z; t += xr[k].w; }
+            mean = (WAVE ? wave_sum_uniform(t) : wg_sum(t, s_st[0], w)) / (float)K;   // LayerNormOps.cs:92-101
             float sq = 0.0f;
 #pragma unroll
             for (int k = 0; k < KPT; k++)
-                if (tid + 256 * k < K4) {
+                if (tid + TSTEP * k < K4) {
                     float dd, q;
                     dd = xr[k].x - mean; q = dd * dd; sq += q;
                     dd = xr[k].y - mean; q = dd * dd; sq += q;
                     dd = xr[k].z - mean; q = dd * dd; sq += q;
                     dd = xr[k].w - mean; q = dd * dd; sq += q;
                 }
-            sq = wg_sum(sq, s_st[1], w);
+            sq = WAVE ? wave_sum_uniform(sq) : wg_sum(sq, s_st[1], w);
             sc = 1.0f / sqrtf(sq / (float)K + a.eps);     // LayerNormOps.cs:103-119
         }
 #pragma unroll
         for (int k = 0; k < KPT; k++) {
-            const int i4 = tid + 256 * k;
+            const int i4 = tid + TSTEP * k;
             if (i4 < K4) {
                 float4 v = xr[k];
                 if constexpr (TWO) { v.x += x2[k].x; v.y += x2[k].y; v.z += x2[k].z; v.w += x2[k].w; }
@@ -327,10 +334,13 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
                     v.z = __builtin_fmaf(g.z, (v.z - mean) * sc, b.z);
                     v.w = __builtin_fmaf(g.w, (v.w - mean) * sc, b.w);
                 }
-                xs[xs_pos(i4 >> 3, i4 & 7)] = v;
+                xsb[xs_pos(i4 >> 3, i4 & 7)] = v;
             }
         }
-        __syncthreads();
+        // wave-private staging: a wave's LDS operations complete in issue order, so its reads
+        // below see its writes; otherwise every wave reads what all of them staged
+        if constexpr (WAVE) __builtin_amdgcn_wave_barrier();
+        else __syncthreads();
     }
 
     if constexpr (EC == EC_QKV) {
@@ -350,7 +360,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
             float4 xv[8];
             if constexpr (STG) {
 #pragma unroll
-                for (int i = 0; i < 8; i++) xv[i] = xs[xs_pos(cj[j], i)];
+                for (int i = 0; i < 8; i++) xv[i] = xsb[xs_pos(cj[j], i)];
             } else {
                 const float4 *xp = (const float4 *)(x + 32 * cj[j]);
 #pragma unroll
@@ -447,7 +457,8 @@ hipError_t launch_v(const GemvArgs &a, int m, hipStream_t s)
     if (STG && a.w.cols > (int64_t)64 / HW * S * C * 32) return hipErrorInvalidValue;
     const int64_t groups = (a.w.rows + R * HW - 1) / (R * HW);
     const dim3 grid((unsigned)((groups + (4 / S) - 1) / (4 / S)), (unsigned)m);
-    const size_t lds = STG ? (size_t)a.w.cols * 4 : 0;
+    if (STG == 4 && a.w.cols > 1024) return hipErrorInvalidValue;
+    const size_t lds = STG ? (size_t)a.w.cols * 4 * (STG == 4 ? 4 : 1) : 0;
     if (a.w.cache) hipLaunchKernelGGL((k_gemv<F, R, S, C, PRO, EC, STG, false, HW>), grid, dim3(256), lds, s, a);
     else hipLaunchKernelGGL((k_gemv<F, R, S, C, PRO, EC, STG, true, HW>), grid, dim3(256), lds, s, a);
     if constexpr (EC == EC_ARGMAX) {
@@ -504,9 +515,18 @@ hipError_t launch_pe(const GemvArgs &a, int m, hipStream_t s)
             }
         }
         return hipErrorInvalidValue;
-    case GS_R4S1H2: return launch_v<4, 1, 1, PRO, EC, 1, 2>(a, m, s);
-    case GS_R4S1: return launch_v<4, 1, 1, PRO, EC, 1>(a, m, s);
-    case GS_R2S1: return launch_v<2, 1, 1, PRO, EC, 1>(a, m, s);
+    // K <= 1024 with a fused norm: wave-private staging (no workgroup barrier in the prologue)
+    case GS_R4S1H2:
+        if constexpr (PRO != PRO_NONE) return launch_v<4, 1, 1, PRO, EC, 4, 2>(a, m, s);
+        else return launch_v<4, 1, 1, PRO, EC, 1, 2>(a, m, s);
+    case GS_R4S1:
+        if constexpr (PRO != PRO_NONE)
+            if (K <= 1024) return launch_v<4, 1, 1, PRO, EC, 4>(a, m, s);
+        return launch_v<4, 1, 1, PRO, EC, 1>(a, m, s);
+    case GS_R2S1:
+        if constexpr (PRO != PRO_NONE)
+            if (K <= 1024) return launch_v<2, 1, 1, PRO, EC, 4>(a, m, s);
+        return launch_v<2, 1, 1, PRO, EC, 1>(a, m, s);
     case GS_R2S2: return launch_v<2, 2, 1, PRO, EC, 1>(a, m, s);
     case GS_R4S2: return launch_v<4, 2, 1, PRO, EC, 1>(a, m, s);
     case GS_R4S4: return launch_v<4, 4, 1, PRO, EC, 1>(a, m, s);
