@@ -9,7 +9,10 @@
 // Work decomposition.  A workgroup is 4 wave64s.  A "row group" of R consecutive rows is owned
 // by S waves (S = 1, 2 or 4) that split the 32-element chunks of K between them; lane l of wave
 // ws takes chunks (ws + S*j)*64 + l for j < C, so one pass ("round") covers 64*S*C chunks and
-// every lane holds at most C chunks of x and C*R chunks of weights in registers.
+// every lane holds at most C chunks of x and C*R chunks of weights in registers.  Rows of at
+// most 32 chunks (K <= 1024) on tall matrices put a row group on each half of a wave (HW = 2),
+// and with a fused norm at K <= 1024 every wave stages its own copy of the activations
+// (STG = 4), so the prologue needs no workgroup barrier.
 //
 // Latency is the budget at decode sizes (a 3 MB matrix is 0.4 us of HBM time), so each wave
 // issues all of its loads before it consumes any of them, in the order in which it needs them:
