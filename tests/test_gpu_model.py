@@ -34,6 +34,10 @@ SMALL = {
     # with the RMSNorm folded into them, the 8192-row gate/up matrix on the row-split kernel
     "llama-q4k-wide": (ModelConfig("llama", 1000, 256, 256, 2, 4, 2, 4096), O.Q4_K, O.Q6_K, O.Q6_K),
     "smollm-q5k-wide": (ModelConfig("llama", 1000, 256, 256, 2, 4, 4, 4096), O.Q5_K, O.Q5_K, None),
+    # d_model 1024, the longest row whose fused-norm GEMVs stage the activations per wave (four
+    # float4 per lane), with RMSNorm and with LayerNorm
+    "llama-q4k-d1024": (ModelConfig("llama", 1000, 128, 1024, 2, 16, 4, 1024), O.Q4_K, O.Q6_K, O.Q6_K),
+    "gpt2-q8_0-d1024": (ModelConfig("gpt2", 1000, 128, 1024, 2, 16, 16, 1024), O.Q8_0, O.Q8_0, None),
 }
 
 
@@ -275,7 +279,7 @@ def test_prefill_across_chunks_matches_reference():
 
 @pytest.mark.parametrize("n_sess", [17, 12])
 @pytest.mark.parametrize("key", ["smollm-q5k", "llama-q4k", "gpt2-q8_0", "llama-f16", "gpt2-smq_q8",
-                                 "llama-q4k-wide", "smollm-q5k-wide"])
+                                 "llama-q4k-wide", "smollm-q5k-wide", "llama-q4k-d1024"])
 def test_batch_generate_lockstep_matches_single_sessions_and_reference(pairs, key, n_sess):
     """several sessions stepping together (smx_batch_generate) produce, per
     session, the greedy tokens of the reference run alone; prompts of different lengths, so
