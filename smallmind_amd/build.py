@@ -26,7 +26,7 @@ MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 # instantiations compile in parallel.
 SOURCES = [("k_quant.hip", "k_quant", []), ("k_ops.hip", "k_ops", []), ("runtime.cpp", "runtime", []),
            ("gemv_dispatch.cpp", "gemv_dispatch", []), ("k_qgemm.hip", "k_qgemm", MFMA_VGPR),
-           ("k_attn_prefill.hip", "k_attn_prefill", MFMA_VGPR), ("gguf.cpp", "gguf", []), ("smq.cpp", "smq", []), ("k_sample.hip", "k_sample", [])] + [
+           ("k_attn_prefill.hip", "k_attn_prefill", MFMA_VGPR), ("gguf.cpp", "gguf", []), ("smq.cpp", "smq", []), ("host_common.cpp", "host_common", []), ("k_sample.hip", "k_sample", [])] + [
            ("k_gemv.hip", f"k_gemv_f{f}", [f"-DSMX_GEMV_FMT={f}"]) for f in range(9)]
 
 FLAGS = [

@@ -253,13 +253,19 @@ int config_from_meta(const GgFile &f, smx_model_config &cfg)
     return SMX_OK;
 }
 
-// Byte size of a tensor of `type` with GGUF dims (0 if the type has no known layout).
+// Byte size of a tensor of `type` with GGUF dims; 0 if the type has no known layout, a
+// dimension is not positive, or the size does not fit 64 bits (the products are checked, so a
+// corrupt table cannot wrap to a size that passes the file-bounds check).
 uint64_t tensor_bytes(uint32_t type, const std::vector<int64_t> &dims)
 {
-    int64_t rows = 1;
-    for (size_t k = 1; k < dims.size(); k++) rows *= dims[k];
+    uint64_t rows = 1;
+    for (size_t k = 1; k < dims.size(); k++) {
+        if (dims[k] <= 0 || rows > UINT64_MAX / (uint64_t)dims[k]) return 0;
+        rows *= (uint64_t)dims[k];
+    }
     const int64_t rb = smx_type_row_bytes((int)type, dims[0]);
-    return rb > 0 && rows > 0 ? (uint64_t)rb * (uint64_t)rows : 0;
+    if (rb <= 0 || (uint64_t)rb > UINT64_MAX / rows) return 0;
+    return (uint64_t)rb * rows;
 }
 
 struct Mapping {

@@ -25,14 +25,6 @@
 
 #include "smx_internal.h"
 
-namespace smx {
-
-static thread_local std::string g_err;
-void set_error(const std::string &msg) { g_err = msg; }
-const char *last_error() { return g_err.c_str(); }
-
-}  // namespace smx
-
 using namespace smx;
 
 #define SMX_FAIL(code, ...)                                          \
@@ -51,32 +43,6 @@ using namespace smx;
     } while (0)
 
 namespace {
-
-int type_block_elems(int type)
-{
-    switch (type) {
-    case SMX_TYPE_F32: case SMX_TYPE_F16: return 1;
-    case SMX_TYPE_Q4_0: case SMX_TYPE_Q8_0: case SMX_TYPE_SMQ_Q8: case SMX_TYPE_SMQ_Q4: return 32;
-    case SMX_TYPE_Q4_K: case SMX_TYPE_Q5_K: case SMX_TYPE_Q6_K: return 256;
-    default: return 0;
-    }
-}
-
-int type_block_bytes(int type)
-{
-    switch (type) {
-    case SMX_TYPE_F32: return 4;
-    case SMX_TYPE_F16: return 2;
-    case SMX_TYPE_Q4_0: return 18;
-    case SMX_TYPE_Q8_0: return 34;
-    case SMX_TYPE_Q4_K: return 144;
-    case SMX_TYPE_Q5_K: return 176;
-    case SMX_TYPE_Q6_K: return 210;
-    case SMX_TYPE_SMQ_Q8: return 36;
-    case SMX_TYPE_SMQ_Q4: return 20;
-    default: return 0;
-    }
-}
 
 // A weight matrix in the backend layout.
 struct Mat {
@@ -909,17 +875,6 @@ struct BusyGuard {
 extern "C" {
 
 SMX_API const char *smx_version(void) { return "smx 0.1.0 (gfx950)"; }
-SMX_API const char *smx_last_error(void) { return smx::last_error(); }
-SMX_API int smx_type_block_elems(int type) { return type_block_elems(type); }
-SMX_API int smx_type_block_bytes(int type) { return type_block_bytes(type); }
-
-SMX_API int64_t smx_type_row_bytes(int type, int64_t k)
-{
-    const int be = type_block_elems(type);
-    if (!be || k < 0 || k % be) return -1;
-    return k / be * type_block_bytes(type);
-}
-
 SMX_API int smx_dequant(int type, const void *blocks_dev, int64_t n, float *out_dev, void *stream)
 {
     if (!type_block_elems(type)) SMX_FAIL(SMX_EUNSUPPORTED, "smx_dequant: unsupported type %d", type);
@@ -1480,7 +1435,10 @@ SMX_API int smx_model_upload_tensor(smx_model *m, const char *name, int type, co
     if (fmt < 0) SMX_FAIL(SMX_EUNSUPPORTED, "%s: weight type %d is not a supported block format", name, type);
     if (cols <= 0 || rows <= 0 || cols % fmt_block_elems(fmt))
         SMX_FAIL(SMX_EINVAL, "%s: ne0=%lld is not a multiple of the block size %d", name, (long long)cols, fmt_block_elems(fmt));
-    const size_t expect = (size_t)(rows * (cols / fmt_block_elems(fmt)) * fmt_gguf_bytes(fmt));
+    const int64_t blocks = cols / fmt_block_elems(fmt), bb = fmt_gguf_bytes(fmt);
+    if (rows > INT64_MAX / blocks / bb)
+        SMX_FAIL(SMX_EINVAL, "%s: shape [%lld x %lld] is too large", name, (long long)rows, (long long)cols);
+    const size_t expect = (size_t)(rows * blocks * bb);
     if (nbytes != expect) SMX_FAIL(SMX_EINVAL, "%s: %zu bytes, expected %zu", name, nbytes, expect);
     hipStream_t s = m->ctx->stream;
 

@@ -61,10 +61,15 @@ struct SmqEntry {
     uint32_t type = 0, block = 0;
     std::vector<int64_t> dims;   // as stored: dims[0] = rows
     uint64_t data_off = 0, data_len = 0, aux_off = 0, aux_len = 0;
+    // element count, or -1 when it exceeds 2^60 (so that the byte sizes derived from it, at
+    // most 4 bytes per element, cannot wrap)
     int64_t elems() const
     {
         int64_t n = 1;
-        for (int64_t d : dims) n *= d;
+        for (int64_t d : dims) {
+            if (d <= 0 || n > (INT64_C(1) << 60) / d) return -1;
+            n *= d;
+        }
         return n;
     }
 };
@@ -107,6 +112,7 @@ int parse(const uint8_t *p, uint64_t n, SmqFile &f)
         t.data_len = rd64(e + 116);
         t.aux_off = rd64(e + 124);
         t.aux_len = rd64(e + 132);
+        if (t.elems() < 0) SQ_FAIL(SMX_EINVAL, "smq: %s: too many elements", t.name.c_str());
         const uint64_t ne = (uint64_t)t.elems();
         if (t.type == kSmqF32) {
             if (t.data_len != ne * 4 || t.aux_len != 0) SQ_FAIL(SMX_EINVAL, "smq: %s: F32 sizes", t.name.c_str());

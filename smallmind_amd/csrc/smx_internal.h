@@ -329,8 +329,10 @@ hipError_t launch_attention_tokens(const float *q, int64_t q_stride, float *cons
 hipError_t launch_argmax_rows(const float *x, int n, int64_t stride, int M, int32_t *tok_next,
                               int32_t *tok_pos, int32_t *const *tok_arr, hipStream_t s);
 
-// ---- errors --------------------------------------------------------------------------------
+// ---- errors and block geometry (host_common.cpp) ------------------------------------------
 void set_error(const std::string &msg);
 const char *last_error();
+int type_block_elems(int type);   // elements per block (1 for F32 / F16), 0 if unknown
+int type_block_bytes(int type);   // bytes per block, 0 if unknown
 
 }  // namespace smx

@@ -5,6 +5,8 @@ from __future__ import annotations
 import numpy as np
 
 import oracle as O
+from oracle import smq as OS
+from smallmind_amd import smq as S
 
 TYPES = {"Q4_0": O.Q4_0, "Q8_0": O.Q8_0, "Q4_K": O.Q4_K, "Q5_K": O.Q5_K, "Q6_K": O.Q6_K}
 # every weight-matrix format of the backend: the GGUF blocks, SmallMind's SMQ blocks and the
@@ -121,3 +123,28 @@ def check_greedy_against_oracle(osess, prompt, toks, logits, tol, prefilled=Fals
         assert int(toks[i]) == ref_tok, (i, int(toks[i]), ref_tok)
         tok = ref_tok
     return worst
+
+
+def gpt2_smq_tensors(cfg, scheme, block, seed, named):
+    """A GPT-2 TransformerModel's parameters quantized as the SMQ tools do (every parameter,
+    1-D ones as [1][n]), in parameter order."""
+    rng = np.random.default_rng(seed)
+    d, V, T, hid = cfg.embedding_length, cfg.vocab_size, cfg.context_length, 4 * cfg.embedding_length
+    shapes = [(V, d), (T, d)]
+    for _ in range(cfg.block_count):
+        shapes += [(1, d), (1, d), (3 * d, d), (1, 3 * d), (d, d), (1, d), (1, d), (1, d), (hid, d), (1, hid),
+                   (d, hid), (1, d)]
+    shapes += [(1, d), (1, d), (V, d)]
+    names = OS.gpt2_parameter_names(cfg.block_count)
+    out = []
+    for i, (shp, name) in enumerate(zip(shapes, names)):
+        n = shp[0] * shp[1]
+        if name.endswith("norm.weight"):
+            x = rng.normal(1.0, 0.1, n)
+        elif name.endswith(".bias"):
+            x = rng.normal(0.0, 0.05, n)
+        else:
+            x = rng.normal(0.0, 0.02, n)
+        q, sc = (O.quantize_ref_q8 if scheme == S.Q8_0 else O.quantize_ref_q4)(x.astype(np.float32), block)
+        out.append(S.SmqTensor(name if named else f"param_{i:04d}", scheme, shp, q, sc, block))
+    return out

@@ -13,7 +13,7 @@ import oracle as O
 from oracle import smq as OS
 from smallmind_amd import smq as S
 from smallmind_amd.model import ModelConfig
-from tests.helpers import check_greedy_against_oracle, rel_err
+from tests.helpers import check_greedy_against_oracle, gpt2_smq_tensors, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -46,37 +46,12 @@ def test_reference_benchmark_model(gpu):
     gm.close()
 
 
-def _gpt2_tensors(cfg, scheme, block, seed, named):
-    """A GPT-2 TransformerModel's parameters quantized as the SMQ tools do (every parameter,
-    1-D ones as [1][n]), in parameter order."""
-    rng = np.random.default_rng(seed)
-    d, V, T, hid = cfg.embedding_length, cfg.vocab_size, cfg.context_length, 4 * cfg.embedding_length
-    shapes = [(V, d), (T, d)]
-    for _ in range(cfg.block_count):
-        shapes += [(1, d), (1, d), (3 * d, d), (1, 3 * d), (d, d), (1, d), (1, d), (1, d), (hid, d), (1, hid),
-                   (d, hid), (1, d)]
-    shapes += [(1, d), (1, d), (V, d)]
-    names = OS.gpt2_parameter_names(cfg.block_count)
-    out = []
-    for i, (shp, name) in enumerate(zip(shapes, names)):
-        n = shp[0] * shp[1]
-        if name.endswith("norm.weight"):
-            x = rng.normal(1.0, 0.1, n)
-        elif name.endswith(".bias"):
-            x = rng.normal(0.0, 0.05, n)
-        else:
-            x = rng.normal(0.0, 0.02, n)
-        q, sc = (O.quantize_ref_q8 if scheme == S.Q8_0 else O.quantize_ref_q4)(x.astype(np.float32), block)
-        out.append(S.SmqTensor(name if named else f"param_{i:04d}", scheme, shp, q, sc, block))
-    return out
-
-
 @pytest.mark.parametrize("scheme,block,named", [(S.Q4_0, 32, True), (S.Q8_0, 64, False)])
 def test_written_gpt2_models(gpu, tmp_path, scheme, block, named):
     from smallmind_amd.model import GpuTransformerModel
     cfg = ModelConfig("gpt2", 1000, 128, 256, 2, 4, 4, 1024)
     p = tmp_path / "m.smq"
-    S.write_smq(str(p), _gpt2_tensors(cfg, scheme, block, 11 + block, named), S.gpt2_metadata(cfg))
+    S.write_smq(str(p), gpt2_smq_tensors(cfg, scheme, block, 11 + block, named), S.gpt2_metadata(cfg))
     om, _ = OS.oracle_from_smq(p.read_bytes())
     gm = GpuTransformerModel.from_smq(str(p))
     rng = np.random.default_rng(block)
@@ -91,7 +66,7 @@ def test_explicit_config_and_missing_tensor_are_reported(gpu, tmp_path):
     from smallmind_amd._lib import SmxError
     from smallmind_amd.model import GpuTransformerModel
     cfg = ModelConfig("gpt2", 1000, 128, 256, 2, 4, 4, 1024)
-    tens = _gpt2_tensors(cfg, S.Q8_0, 32, 3, True)
+    tens = gpt2_smq_tensors(cfg, S.Q8_0, 32, 3, True)
     p = tmp_path / "nometa.smq"
     S.write_smq(str(p), tens, {"model_name": "no-config"})
     gm = GpuTransformerModel.from_smq(str(p), config=cfg)
@@ -114,7 +89,7 @@ def test_matrix_of_wrong_rank_is_refused_and_released(gpu, tmp_path):
     from smallmind_amd._lib import SmxError
     from smallmind_amd.model import GpuTransformerModel
     cfg = ModelConfig("gpt2", 1000, 128, 256, 2, 4, 4, 1024)
-    tens = _gpt2_tensors(cfg, S.Q8_0, 32, 5, True)
+    tens = gpt2_smq_tensors(cfg, S.Q8_0, 32, 5, True)
     last = [t.name for t in tens if len(t.dims) == 2 and t.dims[0] > 1][-1]
     bad = [S.SmqTensor(t.name, S.F32, (t.dims[0], t.dims[1], 1),
                        np.random.default_rng(1).normal(0, 0.02, t.dims[0] * t.dims[1]).astype(np.float32))
