@@ -84,9 +84,26 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, OUT)
+    build_consumer()
     if verbose:
         print(f"built {OUT}")
     return OUT
+
+
+ROOT = os.path.dirname(HERE)
+CONSUMER = os.path.join(ROOT, "tests", "capi", "smx_consumer")
+
+
+def build_consumer() -> str:
+    """The C99 consumer of the C-ABI (tests/capi/smx_consumer.c), linked against libsmx.so with
+    a relative run path so that it finds the in-tree library wherever the tree is copied."""
+    cmd = ["gcc", "-std=c99", "-pedantic", "-Wall", "-Wextra", "-Werror", "-I", os.path.join(ROOT, "include"),
+           CONSUMER + ".c", "-L", HERE, "-l:libsmx.so", "-Wl,-rpath,$ORIGIN/../../smallmind_amd",
+           "-Wl,--allow-shlib-undefined", "-o", CONSUMER]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"C consumer build failed:\n{r.stdout}\n{r.stderr}")
+    return CONSUMER
 
 
 if __name__ == "__main__":

@@ -3,6 +3,8 @@
 Bar (stated by the north star): logits within 1e-3 relative error (max|dl| / max|l_ref| per
 step) and greedy tokens identical for the first 64 steps, on the same seeded weights and
 prompts."""
+import os
+
 import numpy as np
 import pytest
 
@@ -170,6 +172,36 @@ def test_model_from_gguf_equals_direct_upload(key, tmp_path):
     s2.close()
     gg.close()
     gm.close()
+
+
+@pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0"])
+def test_c_consumer_generates_the_reference_tokens(key, tmp_path):
+    """A C99 program of its own (tests/capi/smx_consumer.c, built with libsmx.so) loads a GGUF
+    file through include/smx.h, generates greedily on device 0 and writes its tokens and logits:
+    they follow the reference forward of the same tensors (logits within LOGIT_TOL, tokens
+    identical).  A cancel requested before a second generation stops it at its first check."""
+    import subprocess
+
+    from smallmind_amd import gguf as G
+    cfg, lt, et, ht = SMALL[key]
+    om, _, tensors = build_pair(cfg, lt, et, ht, seed=91, with_gpu=False)
+    p = tmp_path / "m.gguf"
+    G.write_gguf(str(p), G.model_metadata(cfg), [(n, q, d, x) for n, (q, d, x) in tensors.items()])
+    prompt = np.random.default_rng(12).integers(0, cfg.vocab_size, 11).astype(np.int32)
+    n_new, out = 12, tmp_path / "out.bin"
+    consumer = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "tests", "capi",
+                            "smx_consumer")
+    print(f"[capi] {key}: {consumer} generate ({n_new} tokens)", flush=True)
+    r = subprocess.run([consumer, "generate", str(p), str(n_new), str(out), *map(str, prompt)],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, (r.stdout, r.stderr)
+    lines = dict(line.split(" ", 1) for line in r.stdout.strip().splitlines())
+    raw = out.read_bytes()
+    toks = np.frombuffer(raw[:4 * n_new], np.int32)
+    logits = np.frombuffer(raw[4 * n_new:], np.float32).reshape(n_new, cfg.vocab_size)
+    assert [int(x) for x in lines["tokens"].split()] == toks.tolist()
+    check_greedy_against_oracle(om.session(64), prompt, toks, logits, LOGIT_TOL)
+    assert lines["cancel"].split() == ["-8", "0", "1"], lines["cancel"]
 
 
 @pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0", "llama-f16", "llama-smq_q4"])
