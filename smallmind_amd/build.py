@@ -99,7 +99,7 @@ def build_consumer() -> str:
     a relative run path so that it finds the in-tree library wherever the tree is copied."""
     cmd = ["gcc", "-std=c99", "-pedantic", "-Wall", "-Wextra", "-Werror", "-I", os.path.join(ROOT, "include"),
            CONSUMER + ".c", "-L", HERE, "-l:libsmx.so", "-Wl,-rpath,$ORIGIN/../../smallmind_amd",
-           "-Wl,--allow-shlib-undefined", "-o", CONSUMER]
+           "-Wl,--allow-shlib-undefined", "-lm", "-o", CONSUMER]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"C consumer build failed:\n{r.stdout}\n{r.stderr}")

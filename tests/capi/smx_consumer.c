@@ -9,7 +9,13 @@
  *       prompt TOKEN...; OUT.bin receives the N_NEW tokens (int32) and their logits (float32,
  *       N_NEW x vocab).  Then a cancel requested before a second generation must stop it at
  *       its first check (SMX_ECANCELED, no tokens).
+ *   smx_consumer suite MODEL.gguf TOKEN...
+ *       device 0: the other host-heavy entry points on one model -- lockstep generation of
+ *       three sessions, a continuous batcher with a greedy and a sampled member (one leaves
+ *       between steps), sampled generation, and a Q8_0 weight through the host-memory operator
+ *       (checked here against its own dequantization) -- printing what each produced.
  */
+#include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -90,10 +96,100 @@ static int generate(const char *path, int n_new, const char *out_path, int n_pro
     return 0;
 }
 
+static void print_row(const char *tag, const int32_t *t, int n)
+{
+    int i;
+    printf("%s", tag);
+    for (i = 0; i < n; i++) printf(" %d", t[i]);
+    printf("\n");
+}
+
+static int suite(const char *path, int n_prompt, char **tokens)
+{
+    enum { NS = 3, NB = 16, NK = 256, NR = 64, NM = 5 };
+    smx_context *ctx = NULL;
+    smx_model *m = NULL;
+    smx_session *s[NS];
+    smx_batcher *b = NULL;
+    smx_weight *w = NULL;
+    smx_sampling sp;
+    smx_gen_stats st;
+    int32_t *prompts, lens[NS], out[NS * NB], steps[2 * 6];
+    static uint8_t blocks[NR * (NK / 32) * 34];
+    static float act[NM * NK], y[NM * NR], wf[NR * NK];
+    double worst = 0.0;
+    int i, j, r;
+
+    prompts = (int32_t *)malloc(sizeof(int32_t) * (size_t)(NS * n_prompt));
+    if (!prompts) return 3;
+    for (i = 0; i < NS; i++) {   /* session i: the prompt rotated by i */
+        lens[i] = n_prompt;
+        for (j = 0; j < n_prompt; j++) prompts[i * n_prompt + j] = (int32_t)atoi(tokens[(i + j) % n_prompt]);
+    }
+    check(smx_context_create(0, &ctx), "smx_context_create");
+    check(smx_model_load_gguf(ctx, path, &m), "smx_model_load_gguf");
+    for (i = 0; i < NS; i++) check(smx_session_create(m, n_prompt + NB, &s[i]), "smx_session_create");
+
+    check(smx_batch_generate(s, NS, prompts, lens, NB, out, &st), "smx_batch_generate");
+    for (i = 0; i < NS; i++) print_row(i == 0 ? "batch0" : i == 1 ? "batch1" : "batch2", out + i * NB, NB);
+
+    memset(&sp, 0, sizeof(sp));
+    sp.temperature = 0.8f;
+    sp.top_k = 40;
+    sp.top_p = 0.95;
+    sp.repetition_penalty = 1.1f;
+    for (i = 0; i < NS; i++) check(smx_session_reset(s[i]), "smx_session_reset");
+    check(smx_batcher_create(m, 2, n_prompt + NB, &b), "smx_batcher_create");
+    check(smx_batcher_add(b, s[0], prompts, n_prompt), "smx_batcher_add");
+    check(smx_batcher_add_sampled(b, s[1], prompts + n_prompt, n_prompt, &sp, 5), "smx_batcher_add_sampled");
+    check(smx_batcher_step(b, 6, steps), "smx_batcher_step");
+    print_row("batcher_greedy", steps, 6);
+    print_row("batcher_sampled", steps + 6, 6);
+    check(smx_batcher_remove(b, s[0]), "smx_batcher_remove");
+    printf("batcher_count %d\n", smx_batcher_count(b));
+    check(smx_batcher_step(b, 3, steps), "smx_batcher_step");
+    print_row("batcher_after_leave", steps, 3);
+    check(smx_batcher_destroy(b), "smx_batcher_destroy");
+
+    check(smx_session_reset(s[2]), "smx_session_reset");
+    check(smx_session_generate_sampled(s[2], prompts, n_prompt, 10, &sp, 9, out, NULL, &st), "smx_session_generate_sampled");
+    print_row("sampled", out, 10);
+
+    /* a Q8_0 weight [NR][NK]: scale 2^-7 (fp16 0x2000), codes from a fixed sequence */
+    for (r = 0; r < NR * (NK / 32); r++) {
+        uint8_t *blk = blocks + 34 * r;
+        blk[0] = 0x00;
+        blk[1] = 0x20;
+        for (j = 0; j < 32; j++) blk[2 + j] = (uint8_t)((r * 37 + j * 11) % 255);
+    }
+    for (i = 0; i < NM * NK; i++) act[i] = (float)((i * 7919) % 200 - 100) / 64.0f;
+    check(smx_weight_create(SMX_TYPE_Q8_0, NR, NK, blocks, 0, &w), "smx_weight_create");
+    check(smx_weight_to_float32_host(w, wf), "smx_weight_to_float32_host");
+    check(smx_weight_matmul_host(w, act, y, NM, NK, NR), "smx_weight_matmul_host");
+    for (i = 0; i < NM; i++)
+        for (r = 0; r < NR; r++) {
+            double ref = 0.0, scale = 0.0;
+            for (j = 0; j < NK; j++) {
+                ref += (double)act[i * NK + j] * (double)wf[r * NK + j];
+                scale += fabs((double)act[i * NK + j] * (double)wf[r * NK + j]);
+            }
+            if (scale > 0.0 && fabs((double)y[i * NR + r] - ref) / scale > worst) worst = fabs((double)y[i * NR + r] - ref) / scale;
+        }
+    printf("weight_matmul_host worst %.3g\n", worst);
+    check(smx_weight_destroy(w), "smx_weight_destroy");
+
+    for (i = 0; i < NS; i++) check(smx_session_destroy(s[i]), "smx_session_destroy");
+    check(smx_model_destroy(m), "smx_model_destroy");
+    check(smx_context_destroy(ctx), "smx_context_destroy");
+    free(prompts);
+    return 0;
+}
+
 int main(int argc, char **argv)
 {
     if (argc == 3 && !strcmp(argv[1], "info")) return info(argv[2]);
     if (argc >= 6 && !strcmp(argv[1], "generate")) return generate(argv[2], atoi(argv[3]), argv[4], argc - 5, argv + 5);
-    fprintf(stderr, "usage: smx_consumer info MODEL.gguf | generate MODEL.gguf N_NEW OUT.bin TOKEN...\n");
+    if (argc >= 4 && !strcmp(argv[1], "suite")) return suite(argv[2], argc - 3, argv + 3);
+    fprintf(stderr, "usage: smx_consumer info MODEL.gguf | generate MODEL.gguf N_NEW OUT.bin TOKEN... | suite MODEL.gguf TOKEN...\n");
     return 1;
 }

@@ -204,6 +204,46 @@ def test_c_consumer_generates_the_reference_tokens(key, tmp_path):
     assert lines["cancel"].split() == ["-8", "0", "1"], lines["cancel"]
 
 
+def test_c_consumer_suite_matches_the_python_binding(tmp_path):
+    """The C consumer's suite mode on a GGUF model: lockstep generation of three sessions and
+    sampled generation give the tokens the Python binding gets from the same file and library;
+    the continuous batcher keeps its members' order and count as one leaves; a Q8_0 weight
+    through the host-memory operator agrees with its own dequantization to fp32 rounding."""
+    import subprocess
+
+    from smallmind_amd import gguf as G
+    from smallmind_amd.model import GpuInferenceSession, GpuTransformerModel
+    cfg, lt, et, ht = SMALL["llama-q4k"]
+    _, _, tensors = build_pair(cfg, lt, et, ht, seed=93, with_gpu=False)
+    p = tmp_path / "m.gguf"
+    G.write_gguf(str(p), G.model_metadata(cfg), [(n, q, d, x) for n, (q, d, x) in tensors.items()])
+    prompt = np.random.default_rng(13).integers(0, cfg.vocab_size, 9).astype(np.int32)
+    consumer = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "tests", "capi",
+                            "smx_consumer")
+    print(f"[capi] suite: {consumer}", flush=True)
+    r = subprocess.run([consumer, "suite", str(p), *map(str, prompt)], capture_output=True, text=True, timeout=180)
+    assert r.returncode == 0, (r.stdout, r.stderr)
+    out = {line.split(" ", 1)[0]: line.split(" ", 1)[1].split() for line in r.stdout.strip().splitlines()}
+    gm = GpuTransformerModel.from_gguf(str(p))
+    sess = [gm.create_session(len(prompt) + 16) for _ in range(3)]
+    prompts = [np.roll(prompt, -i) for i in range(3)]
+    toks, _ = GpuInferenceSession.generate_greedy_batch(sess, prompts, 16)
+    for i in range(3):
+        assert [int(t) for t in out[f"batch{i}"]] == toks[i].tolist(), i
+    sess[2].reset_kv_cache()
+    stoks, _ = sess[2].generate_sampled(prompt, 10, seed=9, temperature=0.8, top_k=40, top_p=0.95,
+                                        repetition_penalty=1.1)
+    assert [int(t) for t in out["sampled"]] == list(stoks)
+    assert len(out["batcher_greedy"]) == 6 and len(out["batcher_sampled"]) == 6
+    assert out["batcher_count"] == ["1"] and len(out["batcher_after_leave"]) == 3
+    assert all(0 <= int(t) < cfg.vocab_size for k in ("batcher_greedy", "batcher_sampled", "batcher_after_leave")
+               for t in out[k])
+    assert float(out["weight_matmul_host"][1]) <= 1e-6
+    for s_ in sess:
+        s_.close()
+    gm.close()
+
+
 @pytest.mark.parametrize("key", ["llama-q4k", "gpt2-q8_0", "llama-f16", "llama-smq_q4"])
 def test_forward_api_matches_nocache_reference(pairs, key):
     """GpuInferenceSession.forward mirrors TransformerModel.Forward(idx, positionOffset) with the
