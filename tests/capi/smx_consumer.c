@@ -187,6 +187,7 @@ static int suite(const char *path, int n_prompt, char **tokens)
 
 int main(int argc, char **argv)
 {
+    setvbuf(stdout, NULL, _IOLBF, 0);   /* each result line leaves the process as it is printed */
     if (argc == 3 && !strcmp(argv[1], "info")) return info(argv[2]);
     if (argc >= 6 && !strcmp(argv[1], "generate")) return generate(argv[2], atoi(argv[3]), argv[4], argc - 5, argv + 5);
     if (argc >= 4 && !strcmp(argv[1], "suite")) return suite(argv[2], argc - 3, argv + 3);
