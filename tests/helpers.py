@@ -148,3 +148,18 @@ def gpt2_smq_tensors(cfg, scheme, block, seed, named):
         q, sc = (O.quantize_ref_q8 if scheme == S.Q8_0 else O.quantize_ref_q4)(x.astype(np.float32), block)
         out.append(S.SmqTensor(name if named else f"param_{i:04d}", scheme, shp, q, sc, block))
     return out
+
+
+def c_consumer() -> str:
+    """The C99 consumer of the C-ABI (tests/capi/smx_consumer.c), which the build links next to
+    libsmx.so; built here (gcc) if it is absent."""
+    import importlib.util
+    import os
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    path = os.path.join(root, "tests", "capi", "smx_consumer")
+    if not os.path.exists(path):
+        spec = importlib.util.spec_from_file_location("smx_build", os.path.join(root, "smallmind_amd", "build.py"))
+        b = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(b)
+        b.build_consumer()
+    return path

@@ -132,18 +132,6 @@ def test_build_refuses_gemv_instances_with_scratch_memory():
     assert {"k_gemv.hip", "k_qgemm.hip", "k_attn_prefill.hip"} <= set(b.SPILL_CHECKED)
 
 
-def _consumer():
-    """The C99 consumer built next to libsmx.so (tests/capi/smx_consumer.c), built here if absent."""
-    path = os.path.join(ROOT, "tests", "capi", "smx_consumer")
-    if not os.path.exists(path):
-        import importlib.util
-        spec = importlib.util.spec_from_file_location("smx_build", os.path.join(ROOT, "smallmind_amd", "build.py"))
-        b = importlib.util.module_from_spec(spec)
-        spec.loader.exec_module(b)
-        b.build_consumer()
-    return path
-
-
 def test_c_consumer_reads_a_model_file_through_the_header(tmp_path):
     """include/smx.h compiles as C99 with -pedantic -Werror (the build fails otherwise), and a
     C program linked against libsmx.so reads the version, the block geometry and a GGUF file's
@@ -152,12 +140,12 @@ def test_c_consumer_reads_a_model_file_through_the_header(tmp_path):
 
     from smallmind_amd import gguf as G
     from smallmind_amd.model import ModelConfig, read_gguf_config
-    from tests.helpers import build_pair
+    from tests.helpers import build_pair, c_consumer
     cfg = ModelConfig("llama", 300, 96, 256, 2, 8, 2, 512, 500000.0, 1e-6)
     _, _, t = build_pair(cfg, O.Q4_K, O.Q6_K, O.Q6_K, seed=3, with_gpu=False)
     p = tmp_path / "m.gguf"
     G.write_gguf(str(p), G.model_metadata(cfg), [(n, q, d, x) for n, (q, d, x) in t.items()])
-    r = subprocess.run([_consumer(), "info", str(p)], capture_output=True, text=True, timeout=120)
+    r = subprocess.run([c_consumer(), "info", str(p)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
     lines = dict(line.split(" ", 1) for line in r.stdout.strip().splitlines())
     assert lines["version"].startswith("smx ")

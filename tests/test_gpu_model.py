@@ -3,14 +3,12 @@
 Bar (stated by the north star): logits within 1e-3 relative error (max|dl| / max|l_ref| per
 step) and greedy tokens identical for the first 64 steps, on the same seeded weights and
 prompts."""
-import os
-
 import numpy as np
 import pytest
 
 import oracle as O
 from smallmind_amd.model import ModelConfig
-from tests.helpers import build_pair, check_greedy_against_oracle, rel_err
+from tests.helpers import build_pair, c_consumer, check_greedy_against_oracle, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -189,8 +187,7 @@ def test_c_consumer_generates_the_reference_tokens(key, tmp_path):
     G.write_gguf(str(p), G.model_metadata(cfg), [(n, q, d, x) for n, (q, d, x) in tensors.items()])
     prompt = np.random.default_rng(12).integers(0, cfg.vocab_size, 11).astype(np.int32)
     n_new, out = 12, tmp_path / "out.bin"
-    consumer = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "tests", "capi",
-                            "smx_consumer")
+    consumer = c_consumer()
     print(f"[capi] {key}: {consumer} generate ({n_new} tokens)", flush=True)
     r = subprocess.run([consumer, "generate", str(p), str(n_new), str(out), *map(str, prompt)],
                        capture_output=True, text=True, timeout=120)
@@ -218,8 +215,7 @@ def test_c_consumer_suite_matches_the_python_binding(tmp_path):
     p = tmp_path / "m.gguf"
     G.write_gguf(str(p), G.model_metadata(cfg), [(n, q, d, x) for n, (q, d, x) in tensors.items()])
     prompt = np.random.default_rng(13).integers(0, cfg.vocab_size, 9).astype(np.int32)
-    consumer = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "tests", "capi",
-                            "smx_consumer")
+    consumer = c_consumer()
     print(f"[capi] suite: {consumer}", flush=True)
     r = subprocess.run([consumer, "suite", str(p), *map(str, prompt)], capture_output=True, text=True, timeout=180)
     assert r.returncode == 0, (r.stdout, r.stderr)
