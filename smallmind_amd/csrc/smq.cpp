@@ -237,6 +237,8 @@ SMX_API int smx_smq_pack(int type, const void *data, const float *scales, int64_
     if (cols % 32 != 0 || block_size % 32 != 0)
         SQ_FAIL(SMX_EUNSUPPORTED, "smx_smq_pack: cols %lld and block size %d must be multiples of 32", (long long)cols,
                 block_size);
+    if (rows > (INT64_C(1) << 58) / cols)   // the byte counts below stay far inside 64 bits
+        SQ_FAIL(SMX_EINVAL, "smx_smq_pack: %lld x %lld elements is too large", (long long)rows, (long long)cols);
     const bool q8 = type == SMX_TYPE_SMQ_Q8;
     const int64_t nchunk = rows * cols / 32;
     const size_t bb = q8 ? 36 : 20;

@@ -235,3 +235,20 @@ def test_writer_output_is_what_smqwriter_lays_out(tmp_path):
     assert struct.unpack_from("<QQQQ", b, e + 108) == (data, 64, data + 64, 8)
     assert b[e + 140:e + 156] == bytes(16)
     assert b[data:data + 64] == np.ascontiguousarray(q).tobytes() and b[data + 64:] == sc.tobytes()
+
+
+def test_smq_pack_refuses_sizes_past_64_bits():
+    """rows x cols whose byte counts would not fit 64 bits are refused before any arithmetic on
+    them (the product itself would overflow); the small buffers are never touched."""
+    import ctypes
+
+    from smallmind_amd import _lib
+    from smallmind_amd._lib import SmxError
+    data = np.zeros(64, np.int8)
+    scales = np.ones(4, np.float32)
+    out = np.zeros(64, np.uint8)
+    for rows, cols in [(2**40, 2**40), (2**62, 32), (2**31, 2**31)]:
+        with pytest.raises(SmxError, match="too large"):
+            _lib.call("smx_smq_pack", 1010, data.ctypes.data_as(ctypes.c_void_p),
+                      scales.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), ctypes.c_int64(rows),
+                      ctypes.c_int64(cols), 32, out.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(out.size))
