@@ -91,6 +91,11 @@ int mat_alloc(Mat &m, int fmt, int64_t rows, int64_t cols)
         return SMX_OK;
     }
     const int64_t nb = cols / fmt_block_elems(fmt);
+    // the kernels address a matrix with 32-bit byte offsets, so larger ones are refused here,
+    // before any size arithmetic could wrap into a short allocation (callers bound cols)
+    if (rows > (INT64_C(1) << 32) || (uint64_t)rows * (uint64_t)nb * (uint64_t)fmt_main_bytes(fmt) >= (1ull << 32))
+        SMX_FAIL(SMX_EUNSUPPORTED, "matrix [%lld x %lld] exceeds the 4 GiB the kernels address", (long long)rows,
+                 (long long)cols);
     SMX_HIP(hipMalloc((void **)&m.q, (size_t)(rows * nb * fmt_main_bytes(fmt))));
     if (fmt_has_d(fmt)) SMX_HIP(hipMalloc((void **)&m.d, (size_t)(rows * nb * fmt_d_bytes(fmt))));
     m.fmt = fmt;

@@ -178,6 +178,23 @@ def test_matmul_dimension_mismatch_raises(gpu):
     w.close()
 
 
+def test_weight_create_refuses_matrices_past_4_gib(gpu):
+    """A weight whose blocks would exceed the 4 GiB the kernels address (32-bit byte offsets) is
+    refused at creation, before any allocation or copy: rows large enough to wrap the size
+    arithmetic, and a plainly too large Q8_0 matrix.  The source pointer is never read."""
+    import ctypes
+
+    from smallmind_amd import _lib
+    L = _lib.load()
+    src = np.zeros(64, np.uint8)
+    for rows, cols in [(2**60, 32), (2**33, 32), (2**20, 16384)]:
+        w = ctypes.c_void_p()
+        rc = L.smx_weight_create(int(O.Q8_0), ctypes.c_int64(rows), ctypes.c_int64(cols),
+                                        src.ctypes.data_as(ctypes.c_void_p), 0, ctypes.byref(w))
+        assert rc == -5 and not w.value, (rows, cols, rc)
+        assert b"4 GiB" in L.smx_last_error()
+
+
 @pytest.mark.parametrize("name", ["Q4_K", "Q8_0", "Q6_K"])
 def test_host_memory_matmul_matches_oracle_and_device_api(gpu, name):
     """IWeightTensor.MatMul with the reference's host operands (smx_weight_matmul_host): numpy
