@@ -1357,6 +1357,14 @@ SMX_API int smx_model_create(smx_context *ctx, const smx_model_config *cfg, smx_
     if (hd != 16 && hd != 32 && hd != 64 && hd != 128)
         SMX_FAIL(SMX_EUNSUPPORTED, "smx_model_create: head_dim %d (supported: 16, 32, 64, 128)", hd);
     if (c.arch == SMX_ARCH_LLAMA && c.d_ff <= 0) SMX_FAIL(SMX_EINVAL, "smx_model_create: d_ff");
+    // the weight uploads take rows of at most 16384 elements (d_model and the MLP width); the
+    // other limits keep every derived size (QKV width, MLP width, cache and logits bytes) far
+    // inside its type whatever a file's metadata says
+    const int64_t mlp = c.arch == SMX_ARCH_LLAMA ? c.d_ff : 4 * (int64_t)c.d_model;
+    if (c.d_model > 16384 || mlp > 16384 || c.vocab > (1 << 24) || c.ctx > (1 << 24) || c.n_layer > 4096)
+        SMX_FAIL(SMX_EUNSUPPORTED, "smx_model_create: d_model %d, MLP width %lld, vocab %d, ctx %d, %d layers exceed "
+                 "d_model, MLP width <= 16384, vocab, ctx <= 2^24, layers <= 4096", c.d_model, (long long)mlp, c.vocab,
+                 c.ctx, c.n_layer);
     for (int i = 0; i < 6; i++) if (c.reserved[i]) SMX_FAIL(SMX_EINVAL, "smx_model_create: reserved fields must be 0");
     smx_model *m = new smx_model();
     m->ctx = ctx;

@@ -201,6 +201,39 @@ def test_c_consumer_generates_the_reference_tokens(key, tmp_path):
     assert lines["cancel"].split() == ["-8", "0", "1"], lines["cancel"]
 
 
+def test_model_create_refuses_configurations_out_of_range(gpu):
+    """Configurations whose derived sizes could overflow (as a file's metadata may claim) are
+    refused at creation: d_model or the MLP width above the 16384-element rows the uploads take,
+    a vocabulary or context above 2^24, more than 4096 layers; the largest accepted values pass."""
+    import ctypes
+
+    from smallmind_amd import _lib
+    L = _lib.load()
+    ctx = ctypes.c_void_p()
+    assert L.smx_context_create(0, ctypes.byref(ctx)) == 0
+
+    def create(**kw):
+        c = _lib.ModelConfigC(arch=0, vocab=1000, ctx=256, d_model=256, n_layer=2, n_head=4, n_kv_head=4, d_ff=512,
+                              rope_theta=10000.0, norm_eps=1e-5)
+        for k, v in kw.items():
+            setattr(c, k, v)
+        m = ctypes.c_void_p()
+        rc = L.smx_model_create(ctx, ctypes.byref(c), ctypes.byref(m))
+        if rc == 0:
+            L.smx_model_destroy(m)
+        return rc
+
+    assert create() == 0
+    assert create(d_model=16384, n_head=128, n_kv_head=128, d_ff=16384) == 0
+    assert create(arch=1, d_model=4096, n_head=32, n_kv_head=32) == 0   # GPT-2: MLP width 4 d
+    for kw in [dict(d_model=2**30, n_head=2**24, n_kv_head=2**24), dict(d_model=32768, n_head=256, n_kv_head=256),
+               dict(d_ff=2**31 - 1), dict(arch=1, d_model=8192, n_head=64, n_kv_head=64), dict(vocab=2**24 + 1),
+               dict(ctx=2**30), dict(n_layer=5000)]:
+        assert create(**kw) == -5, kw
+        assert b"exceed" in L.smx_last_error()
+    assert L.smx_context_destroy(ctx) == 0
+
+
 def test_c_consumer_suite_matches_the_python_binding(tmp_path):
     """The C consumer's suite mode on a GGUF model: lockstep generation of three sessions and
     sampled generation give the tokens the Python binding gets from the same file and library;
