@@ -1586,7 +1586,7 @@ hipError_t launch_d(const QgemmArgs &a, hipStream_t s)
 
 }  // namespace
 
-size_t qgemm_xp_bytes(int M, int K) { return (size_t)((M + 15) / 16) * (K / 32) * 3 * 1024; }
+size_t qgemm_xp_bytes(int M, int K) { return (size_t)(((int64_t)M + 15) / 16) * (size_t)(K / 32) * 3 * 1024; }
 
 hipError_t launch_qgemm(const QgemmArgs &a, const float *x, int64_t x_stride, int pro,
                         const float *gamma, const float *beta, float eps, hipStream_t s)
